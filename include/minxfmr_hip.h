@@ -1,0 +1,146 @@
+/*
+ * minxfmr_hip.h — C ABI of the MI355X (gfx950) backend for minXfmr.cpp.
+ *
+ * Plain C types only: device pointers are `void*` / `float*` obtained from
+ * mxh_alloc (or any HIP allocation on the current device), sizes are
+ * int64_t/size_t, status is an int (MXH_OK == 0, negative on failure, with a
+ * message from mxh_last_error()).  Every launch goes to the library's own
+ * stream on the current device and is asynchronous unless the function says
+ * otherwise.
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the minXfmr.cpp tree).  The library is
+ * thread-compatible, not thread-safe: one caller thread per process, as in
+ * the reference's single-context runtime (src/api/minxfmr.cpp globals).
+ */
+#ifndef MINXFMR_HIP_H
+#define MINXFMR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Tensor element types, numbered as GGUF type ids.  Replaces DataType
+ * (src/tensor/tensor.h:5-14), which lacks F16 and Q5_K. */
+enum {
+    MXH_F32 = 0,
+    MXH_F16 = 1,
+    MXH_Q5_0 = 6,
+    MXH_Q8_0 = 8,
+    MXH_Q4_K = 12,
+    MXH_Q5_K = 13
+};
+
+/* Q4_K/Q5_K 6-bit scale unpacking.  MXH_FORM_REF is the reference CPU
+ * decoder (src/tensor/tensor.cpp:395-403) and the default; MXH_FORM_GGML is
+ * the ggml decoder used by the reference CUDA kernels
+ * (src/backend/cuda/cuda_backend.cu:175-183). */
+enum { MXH_FORM_REF = 0, MXH_FORM_GGML = 1 };
+
+enum {
+    MXH_OK = 0,
+    MXH_ERR_ARG = -1,         /* bad pointer / shape / type combination */
+    MXH_ERR_UNSUPPORTED = -2, /* valid request the backend does not implement */
+    MXH_ERR_HIP = -3,         /* HIP runtime error */
+    MXH_ERR_NODEV = -4,       /* no usable gfx950 device */
+    MXH_ERR_OOM = -5          /* device allocation failed */
+};
+
+/* ---- lifecycle ------------------------------------------------------ */
+
+/* Select `device`, create the library stream.  Idempotent.
+ * Replaces cuda_backend_is_available's lazy ensure_ready
+ * (src/backend/cuda/cuda_backend.cu:123-133). */
+int mxh_init(int device);
+
+/* 1 when a gfx950 device is usable (initialising on first call).
+ * Replaces cuda_backend_is_available (src/backend/cuda/cuda_backend.h:5). */
+int mxh_is_available(void);
+
+/* Message of the last failure on this thread ("" when none); library-owned.
+ * Replaces cuda_backend_last_error_msg (src/backend/cuda/cuda_backend.h:21)
+ * and backend_last_preload_error (src/backend/backend_runtime.h:48). */
+const char *mxh_last_error(void);
+
+/* Block until all work on the library stream is done. */
+int mxh_synchronize(void);
+
+/* The library stream as an opaque hipStream_t, for callers that order their
+ * own work (events, copies) against the library's launches. */
+void *mxh_stream(void);
+
+/* ---- device memory (plumbing) ---------------------------------------- */
+int mxh_alloc(void **dptr, size_t bytes);
+int mxh_free(void *dptr);
+int mxh_upload(void *dst, const void *src, size_t bytes);   /* synchronous */
+int mxh_download(void *dst, const void *src, size_t bytes); /* synchronous */
+int mxh_memset(void *dptr, int value, size_t bytes);        /* async */
+
+/* Elapsed time of the work enqueued between begin and end, measured with
+ * events on the library stream.  mxh_timer_end synchronizes. */
+int mxh_timer_begin(void);
+int mxh_timer_end(float *ms);
+
+/* ---- the decode hot path (device pointers) ---------------------------- */
+
+/* y[n] = sum_k x[k] * dequant(W[n, k]) for W a row-major [n x k] tensor of
+ * raw GGUF blocks (k a multiple of the block size).  W must be 16-byte
+ * aligned for Q4_K/Q5_K/F32 and 4-byte aligned for Q8_0/Q5_0.
+ * Replaces the m == 1 case of backend_matmul_rhs_transposed
+ * (src/backend/backend_runtime.cpp:266-376, cuda_backend.cu:1198-1415). */
+int mxh_gemv(int type, const void *w, const float *x, float *y, int64_t n, int64_t k, int form);
+
+/* out[m x n] = A[m x k] . dequant(W[n x k])^T for any m (prefill).
+ * Replaces backend_matmul_rhs_transposed (src/backend/backend_runtime.h:37). */
+int mxh_matmul_rhs_t(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out,
+                     int form);
+
+/* out[rows x cols] fp32 = dequant(W) — bit-exact with the CPU decoder.
+ * Replaces the debug dequant kernels
+ * (src/backend/cuda/cuda_backend.cu:583-674, cuda_backend_compare_dequant). */
+int mxh_dequant(int type, const void *w, float *out, int64_t rows, int64_t cols, int form);
+
+/* ---- per-op backend interface (host pointers) ------------------------- */
+/* These keep the reference op semantics for drop-in use: host pointers in
+ * and out, one synchronous device round trip per call.  Quantized weights
+ * are cached on the device keyed by (host pointer, bytes). */
+
+/* Replaces cuda_backend_preload_tensor (src/backend/cuda/cuda_backend.h:7). */
+int mxh_preload(const void *host, size_t bytes);
+
+/* Replaces cuda_backend_release_resources (src/backend/cuda/cuda_backend.h:6). */
+void mxh_release_resources(void);
+
+/* Replaces cuda_backend_matmul_rhs_transposed (cuda_backend.h:25). */
+int mxh_host_matmul_rhs_t(int type, const float *a, int64_t m, int64_t k, const void *w, size_t w_bytes, int64_t n,
+                          float *out, int form);
+
+/* F32 out[m x n] = A[m x k] . B[k x n].  Replaces cuda_backend_matmul for F32
+ * operands (cuda_backend.h:24). */
+int mxh_host_matmul_f32(const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n);
+
+/* out[n] = sum_k vec[k] * mat[k * stride + n].
+ * Replaces cuda_backend_matvec_strided (cuda_backend.h:26). */
+int mxh_host_matvec_strided(const float *vec, const float *mat, float *out, size_t K, size_t N, size_t stride);
+
+/* out[j] = dot(vec, rows[j * stride .. +K]).
+ * Replaces cuda_backend_vec_dot_rows (cuda_backend.h:27). */
+int mxh_host_vec_dot_rows(const float *vec, const float *rows, float *out, size_t K, size_t nrows, size_t stride);
+
+/* out[j] = dot(vec, ring[((head + j) % seq_max) * stride .. +K]), j < len.
+ * Replaces cuda_backend_vec_dot_rows_ring (cuda_backend.h:28). */
+int mxh_host_vec_dot_rows_ring(const float *vec, const float *ring, size_t head, size_t seq_max, size_t len,
+                               size_t K, size_t stride, float *out);
+
+/* out[c] = sum_r vec[r] * rows[r * stride + c].
+ * Replaces cuda_backend_vec_mul_rows_cols (cuda_backend.h:29). */
+int mxh_host_vec_mul_rows_cols(const float *vec, const float *rows, float *out, size_t nrows, size_t ncols,
+                               size_t stride);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MINXFMR_HIP_H */

@@ -1,0 +1,324 @@
+// mxh_abi.hip — the extern "C" surface declared in include/minxfmr_hip.h.
+//
+// Holds the per-process device context (device, stream, timing events, the
+// weight cache of the per-op interface) and validates every request on the
+// host before any kernel sees it: a launch that reaches the device has shapes
+// the kernel's indexing assumes.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "mxh_internal.h"
+
+namespace mxh {
+namespace {
+
+struct Context {
+    bool ready = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // per-op interface: weights cached by (host pointer, bytes)
+    std::map<std::pair<const void*, size_t>, void*> weights;
+    // grow-only staging buffers for host-pointer ops
+    void* stage[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t stage_bytes[4] = {0, 0, 0, 0};
+};
+
+Context g_ctx;
+thread_local std::string g_err;
+
+int ensure_ready() {
+    if (g_ctx.ready) return MXH_OK;
+    return mxh_init(0);
+}
+
+int stage(int slot, size_t bytes, void** out) {
+    if (bytes == 0) bytes = 4;
+    if (g_ctx.stage_bytes[slot] < bytes) {
+        if (g_ctx.stage[slot]) (void)hipFree(g_ctx.stage[slot]);
+        g_ctx.stage[slot] = nullptr;
+        g_ctx.stage_bytes[slot] = 0;
+        size_t want = bytes + (bytes >> 2);
+        if (hipMalloc(&g_ctx.stage[slot], want) != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(MXH_ERR_OOM, "staging allocation of %zu bytes failed", want);
+        }
+        g_ctx.stage_bytes[slot] = want;
+    }
+    *out = g_ctx.stage[slot];
+    return MXH_OK;
+}
+
+// device copy of a host weight, uploading on first use
+int device_weight(const void* host, size_t bytes, const void** dev) {
+    auto key = std::make_pair(host, bytes);
+    auto it = g_ctx.weights.find(key);
+    if (it != g_ctx.weights.end()) {
+        *dev = it->second;
+        return MXH_OK;
+    }
+    void* d = nullptr;
+    if (hipMalloc(&d, bytes + 256) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(MXH_ERR_OOM, "weight upload: allocation of %zu bytes failed", bytes);
+    }
+    int rc = check_hip(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice), "weight upload");
+    if (rc) {
+        (void)hipFree(d);
+        return rc;
+    }
+    g_ctx.weights[key] = d;
+    *dev = d;
+    return MXH_OK;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_weight_ptr(int type, const void* w) {
+    if (!w) return set_error(MXH_ERR_ARG, "null weight pointer");
+    const size_t need = (type == MXH_Q8_0 || type == MXH_Q5_0) ? 4 : 16;
+    if (!aligned(w, need)) return set_error(MXH_ERR_ARG, "weight pointer must be %zu-byte aligned", need);
+    return MXH_OK;
+}
+
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return MXH_OK;
+    return set_error(MXH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t lib_stream() { return g_ctx.stream; }
+
+}  // namespace mxh
+
+using namespace mxh;
+
+extern "C" {
+
+int mxh_init(int device) {
+    if (g_ctx.ready) return device == g_ctx.device ? MXH_OK : set_error(MXH_ERR_ARG, "already bound to device %d", g_ctx.device);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return set_error(MXH_ERR_NODEV, "no HIP device visible");
+    }
+    if (device < 0 || device >= n) return set_error(MXH_ERR_ARG, "device %d out of range (%d visible)", device, n);
+    hipDeviceProp_t prop;
+    if (int rc = check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties")) return rc;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(MXH_ERR_NODEV, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    if (int rc = check_hip(hipSetDevice(device), "hipSetDevice")) return rc;
+    if (int rc = check_hip(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking), "hipStreamCreate")) return rc;
+    if (int rc = check_hip(hipEventCreate(&g_ctx.ev0), "hipEventCreate")) return rc;
+    if (int rc = check_hip(hipEventCreate(&g_ctx.ev1), "hipEventCreate")) return rc;
+    g_ctx.device = device;
+    g_ctx.ready = true;
+    return MXH_OK;
+}
+
+int mxh_is_available(void) { return ensure_ready() == MXH_OK ? 1 : 0; }
+
+const char* mxh_last_error(void) { return g_err.c_str(); }
+
+int mxh_synchronize(void) {
+    if (int rc = ensure_ready()) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "hipStreamSynchronize");
+}
+
+void* mxh_stream(void) { return ensure_ready() == MXH_OK ? (void*)g_ctx.stream : nullptr; }
+
+int mxh_alloc(void** dptr, size_t bytes) {
+    if (!dptr) return set_error(MXH_ERR_ARG, "null output pointer");
+    if (int rc = ensure_ready()) return rc;
+    // 256 bytes of slack: tail loads of the last block never leave the allocation
+    if (hipMalloc(dptr, bytes + 256) != hipSuccess) {
+        (void)hipGetLastError();
+        *dptr = nullptr;
+        return set_error(MXH_ERR_OOM, "hipMalloc(%zu) failed", bytes);
+    }
+    return MXH_OK;
+}
+
+int mxh_free(void* dptr) {
+    if (!dptr) return MXH_OK;
+    return check_hip(hipFree(dptr), "hipFree");
+}
+
+int mxh_upload(void* dst, const void* src, size_t bytes) {
+    if (int rc = ensure_ready()) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.stream), "upload")) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "upload sync");
+}
+
+int mxh_download(void* dst, const void* src, size_t bytes) {
+    if (int rc = ensure_ready()) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream), "download")) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "download sync");
+}
+
+int mxh_memset(void* dptr, int value, size_t bytes) {
+    if (int rc = ensure_ready()) return rc;
+    return check_hip(hipMemsetAsync(dptr, value, bytes, g_ctx.stream), "memset");
+}
+
+int mxh_timer_begin(void) {
+    if (int rc = ensure_ready()) return rc;
+    return check_hip(hipEventRecord(g_ctx.ev0, g_ctx.stream), "hipEventRecord");
+}
+
+int mxh_timer_end(float* ms) {
+    if (int rc = ensure_ready()) return rc;
+    if (int rc = check_hip(hipEventRecord(g_ctx.ev1, g_ctx.stream), "hipEventRecord")) return rc;
+    if (int rc = check_hip(hipEventSynchronize(g_ctx.ev1), "hipEventSynchronize")) return rc;
+    return check_hip(hipEventElapsedTime(ms, g_ctx.ev0, g_ctx.ev1), "hipEventElapsedTime");
+}
+
+int mxh_gemv(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (int rc = check_weight_ptr(type, w)) return rc;
+    if (!x || !y || !aligned(x, 16)) return set_error(MXH_ERR_ARG, "x must be non-null and 16-byte aligned");
+    if (n <= 0 || k <= 0 || row_bytes(type, k) == 0)
+        return set_error(MXH_ERR_ARG, "gemv: k=%lld is not a whole number of type-%d blocks", (long long)k, type);
+    int rc = gemv_launch(type, w, x, y, n, k, form, g_ctx.stream);
+    if (rc == MXH_ERR_ARG) return set_error(rc, "gemv: unsupported shape n=%lld k=%lld", (long long)n, (long long)k);
+    if (rc == MXH_ERR_UNSUPPORTED) return set_error(rc, "gemv: unsupported type %d", type);
+    return check_hip(hipGetLastError(), "gemv launch");
+}
+
+int mxh_matmul_rhs_t(int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k, float* out, int form) {
+    if (m <= 0) return set_error(MXH_ERR_ARG, "matmul: m must be positive");
+    for (int64_t i = 0; i < m; ++i)
+        if (int rc = mxh_gemv(type, w, a + i * k, out + i * n, n, k, form)) return rc;
+    return MXH_OK;
+}
+
+int mxh_dequant(int type, const void* w, float* out, int64_t rows, int64_t cols, int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (!w || !out) return set_error(MXH_ERR_ARG, "dequant: null pointer");
+    int rc = dequant_launch(type, w, out, rows, cols, form, g_ctx.stream);
+    if (rc) return set_error(rc, "dequant: bad type %d or shape %lldx%lld", type, (long long)rows, (long long)cols);
+    return check_hip(hipGetLastError(), "dequant launch");
+}
+
+int mxh_preload(const void* host, size_t bytes) {
+    if (int rc = ensure_ready()) return rc;
+    if (!host || !bytes) return set_error(MXH_ERR_ARG, "preload: empty tensor");
+    const void* d = nullptr;
+    return device_weight(host, bytes, &d);
+}
+
+void mxh_release_resources(void) {
+    if (!g_ctx.ready) return;
+    (void)hipStreamSynchronize(g_ctx.stream);
+    for (auto& kv : g_ctx.weights) (void)hipFree(kv.second);
+    g_ctx.weights.clear();
+    for (int i = 0; i < 4; ++i) {
+        if (g_ctx.stage[i]) (void)hipFree(g_ctx.stage[i]);
+        g_ctx.stage[i] = nullptr;
+        g_ctx.stage_bytes[i] = 0;
+    }
+}
+
+int mxh_host_matmul_rhs_t(int type, const float* a, int64_t m, int64_t k, const void* w, size_t w_bytes, int64_t n,
+                          float* out, int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (!a || !w || !out || m <= 0 || n <= 0 || k <= 0) return set_error(MXH_ERR_ARG, "matmul_rhs_t: bad arguments");
+    const size_t rb = row_bytes(type, k);
+    if (!rb || w_bytes < rb * (size_t)n) return set_error(MXH_ERR_ARG, "matmul_rhs_t: weight bytes too small");
+    const void* dw = nullptr;
+    if (int rc = device_weight(w, rb * (size_t)n, &dw)) return rc;
+    void *da = nullptr, *dout = nullptr;
+    if (int rc = stage(0, sizeof(float) * (size_t)(m * k), &da)) return rc;
+    if (int rc = stage(1, sizeof(float) * (size_t)(m * n), &dout)) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(da, a, sizeof(float) * m * k, hipMemcpyHostToDevice, g_ctx.stream), "H2D"))
+        return rc;
+    if (int rc = mxh_matmul_rhs_t(type, (const float*)da, m, dw, n, k, (float*)dout, form)) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(out, dout, sizeof(float) * m * n, hipMemcpyDeviceToHost, g_ctx.stream), "D2H"))
+        return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "sync");
+}
+
+int mxh_host_matmul_f32(const float* a, const float* b, float* out, int64_t m, int64_t k, int64_t n) {
+    if (int rc = ensure_ready()) return rc;
+    if (!a || !b || !out || m <= 0 || k <= 0 || n <= 0) return set_error(MXH_ERR_ARG, "matmul: bad arguments");
+    void *da, *db, *dout;
+    if (int rc = stage(0, sizeof(float) * m * k, &da)) return rc;
+    if (int rc = stage(2, sizeof(float) * k * n, &db)) return rc;
+    if (int rc = stage(1, sizeof(float) * m * n, &dout)) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(da, a, sizeof(float) * m * k, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(db, b, sizeof(float) * k * n, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    int rc = matmul_f32_launch((const float*)da, (const float*)db, (float*)dout, m, k, n, g_ctx.stream);
+    if (rc) return set_error(rc, "matmul: unsupported shape");
+    if (int rc = check_hip(hipMemcpyAsync(out, dout, sizeof(float) * m * n, hipMemcpyDeviceToHost, g_ctx.stream), "copy")) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "matmul");
+}
+
+int mxh_host_vec_mul_rows_cols(const float* vec, const float* rows, float* out, size_t nrows, size_t ncols,
+                               size_t stride) {
+    if (int rc = ensure_ready()) return rc;
+    if (!vec || !rows || !out || !nrows || !ncols || stride < ncols)
+        return set_error(MXH_ERR_ARG, "vec_mul_rows_cols: bad arguments");
+    const size_t span = (nrows - 1) * stride + ncols;
+    void *dv, *dr, *dout;
+    if (int rc = stage(0, sizeof(float) * nrows, &dv)) return rc;
+    if (int rc = stage(2, sizeof(float) * span, &dr)) return rc;
+    if (int rc = stage(1, sizeof(float) * ncols, &dout)) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(dv, vec, sizeof(float) * nrows, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(dr, rows, sizeof(float) * span, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    if (int rc = vec_mul_rows_cols_launch((const float*)dv, (const float*)dr, (float*)dout, (int64_t)nrows,
+                                          (int64_t)ncols, (int64_t)stride, g_ctx.stream))
+        return set_error(rc, "vec_mul_rows_cols: bad shape");
+    if (int rc = check_hip(hipMemcpyAsync(out, dout, sizeof(float) * ncols, hipMemcpyDeviceToHost, g_ctx.stream), "copy")) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "vec_mul_rows_cols");
+}
+
+int mxh_host_matvec_strided(const float* vec, const float* mat, float* out, size_t K, size_t N, size_t stride) {
+    // out[n] = sum_k vec[k] * mat[k*stride + n]: the same contraction as
+    // vec_mul_rows_cols with K rows of N columns
+    return mxh_host_vec_mul_rows_cols(vec, mat, out, K, N, stride);
+}
+
+int mxh_host_vec_dot_rows_ring(const float* vec, const float* ring, size_t head, size_t seq_max, size_t len, size_t K,
+                               size_t stride, float* out) {
+    if (int rc = ensure_ready()) return rc;
+    if (!vec || !ring || !out || !K || !len || !seq_max || len > seq_max || stride < K)
+        return set_error(MXH_ERR_ARG, "vec_dot_rows_ring: bad arguments");
+    const size_t span = (seq_max - 1) * stride + K;
+    void *dv, *dr, *dout;
+    if (int rc = stage(0, sizeof(float) * K, &dv)) return rc;
+    if (int rc = stage(2, sizeof(float) * span, &dr)) return rc;
+    if (int rc = stage(1, sizeof(float) * len, &dout)) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(dv, vec, sizeof(float) * K, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(dr, ring, sizeof(float) * span, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    if (int rc = vec_dot_rows_launch((const float*)dv, (const float*)dr, (float*)dout, (int64_t)K, (int64_t)len,
+                                     (int64_t)stride, (int64_t)(head % seq_max), (int64_t)seq_max, g_ctx.stream))
+        return set_error(rc, "vec_dot_rows: bad shape");
+    if (int rc = check_hip(hipMemcpyAsync(out, dout, sizeof(float) * len, hipMemcpyDeviceToHost, g_ctx.stream), "copy")) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "vec_dot_rows_ring");
+}
+
+int mxh_host_vec_dot_rows(const float* vec, const float* rows, float* out, size_t K, size_t nrows, size_t stride) {
+    if (!nrows) return set_error(MXH_ERR_ARG, "vec_dot_rows: no rows");
+    // contiguous rows are a ring that never wraps
+    return mxh_host_vec_dot_rows_ring(vec, rows, 0, nrows, nrows, K, stride, out);
+}
+
+}  // extern "C"

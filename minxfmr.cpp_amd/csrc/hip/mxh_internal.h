@@ -1,0 +1,28 @@
+// mxh_internal.h — launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mxh_types.h"
+
+namespace mxh {
+
+// Record a failure message for mxh_last_error(); returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Check a HIP status; on failure record "<what>: <hip error>" and return MXH_ERR_HIP.
+int check_hip(hipError_t e, const char* what);
+
+hipStream_t lib_stream();
+
+int gemv_launch(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int form, hipStream_t st);
+int dequant_launch(int type, const void* w, float* out, int64_t rows, int64_t cols, int form, hipStream_t st);
+
+// small F32 vector ops (attention over host caches, F32 weights)
+int vec_dot_rows_launch(const float* vec, const float* rows, float* out, int64_t K, int64_t nrows, int64_t stride,
+                        int64_t head, int64_t seq_max, hipStream_t st);
+int vec_mul_rows_cols_launch(const float* vec, const float* rows, float* out, int64_t nrows, int64_t ncols,
+                             int64_t stride, hipStream_t st);
+int matmul_f32_launch(const float* a, const float* b, float* out, int64_t m, int64_t k, int64_t n, hipStream_t st);
+
+}  // namespace mxh

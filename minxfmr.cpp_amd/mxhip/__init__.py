@@ -1,0 +1,180 @@
+"""ctypes binding of the gfx950 backend's C ABI (include/minxfmr_hip.h).
+
+The shared library is built in-tree by ``make -C minxfmr.cpp_amd``; importing
+this module loads it and fails loudly if it is missing.  There is no CPU
+fallback: every call runs on the GPU or returns an error.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG_DIR / "lib" / "libminxfmr_hip.so"
+
+F32, F16, Q5_0, Q8_0, Q4_K, Q5_K = 0, 1, 6, 8, 12, 13
+FORM_REF, FORM_GGML = 0, 1
+BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176)}
+TYPE_NAMES = {F32: "F32", F16: "F16", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K"}
+
+
+class MxhError(RuntimeError):
+    pass
+
+
+def row_bytes(type_: int, cols: int) -> int:
+    be, bb = BLOCK[type_]
+    if cols % be:
+        raise ValueError(f"cols={cols} not a multiple of {be}")
+    return cols // be * bb
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH} is not built; run `make -C {PKG_DIR}` (or __graft_entry__.build())")
+    lib = C.CDLL(str(LIB_PATH))
+    vp, i64, sz, fp, ip = C.c_void_p, C.c_int64, C.c_size_t, C.POINTER(C.c_float), C.c_int
+    sig = {
+        "mxh_init": (ip, [ip]),
+        "mxh_is_available": (ip, []),
+        "mxh_last_error": (C.c_char_p, []),
+        "mxh_synchronize": (ip, []),
+        "mxh_stream": (vp, []),
+        "mxh_alloc": (ip, [C.POINTER(vp), sz]),
+        "mxh_free": (ip, [vp]),
+        "mxh_upload": (ip, [vp, vp, sz]),
+        "mxh_download": (ip, [vp, vp, sz]),
+        "mxh_memset": (ip, [vp, ip, sz]),
+        "mxh_timer_begin": (ip, []),
+        "mxh_timer_end": (ip, [fp]),
+        "mxh_gemv": (ip, [ip, vp, vp, vp, i64, i64, ip]),
+        "mxh_matmul_rhs_t": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
+        "mxh_dequant": (ip, [ip, vp, vp, i64, i64, ip]),
+        "mxh_preload": (ip, [vp, sz]),
+        "mxh_release_resources": (None, []),
+        "mxh_host_matmul_rhs_t": (ip, [ip, vp, i64, i64, vp, sz, i64, vp, ip]),
+        "mxh_host_matmul_f32": (ip, [vp, vp, vp, i64, i64, i64]),
+        "mxh_host_matvec_strided": (ip, [vp, vp, vp, sz, sz, sz]),
+        "mxh_host_vec_dot_rows": (ip, [vp, vp, vp, sz, sz, sz]),
+        "mxh_host_vec_dot_rows_ring": (ip, [vp, vp, sz, sz, sz, sz, sz, vp]),
+        "mxh_host_vec_mul_rows_cols": (ip, [vp, vp, vp, sz, sz, sz]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+EXPORTED = (
+    "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
+    "mxh_download mxh_memset mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
+    "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
+    "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols"
+).split()
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib.mxh_last_error().decode(errors="replace")
+        raise MxhError(f"{what or 'mxh call'} failed ({rc}): {msg}")
+
+
+def ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+class DeviceBuffer:
+    """A device allocation owned by Python (freed on close / garbage collection)."""
+
+    def __init__(self, nbytes: int):
+        p = C.c_void_p()
+        check(lib.mxh_alloc(C.byref(p), max(int(nbytes), 1)), "mxh_alloc")
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(a.nbytes)
+        if a.nbytes:
+            check(lib.mxh_upload(buf.ptr, ptr(a), a.nbytes), "upload")
+        return buf
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib.mxh_upload(self.ptr + offset, ptr(a), a.nbytes), "upload")
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        if out.nbytes:
+            check(lib.mxh_download(ptr(out), self.ptr + offset, out.nbytes), "download")
+        return out
+
+    def close(self) -> None:
+        if self.ptr:
+            lib.mxh_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def init(device: int = 0) -> None:
+    check(lib.mxh_init(device), "mxh_init")
+
+
+def available() -> bool:
+    return bool(lib.mxh_is_available())
+
+
+def synchronize() -> None:
+    check(lib.mxh_synchronize(), "synchronize")
+
+
+def gemv(type_: int, w: DeviceBuffer | int, x: DeviceBuffer | int, y: DeviceBuffer | int, n: int, k: int,
+         form: int = FORM_REF) -> None:
+    addr = lambda b: b.ptr if isinstance(b, DeviceBuffer) else int(b)
+    check(lib.mxh_gemv(type_, addr(w), addr(x), addr(y), n, k, form), "mxh_gemv")
+
+
+def dequant(type_: int, w: DeviceBuffer, rows: int, cols: int, form: int = FORM_REF) -> np.ndarray:
+    out = DeviceBuffer(rows * cols * 4)
+    check(lib.mxh_dequant(type_, w.ptr, out.ptr, rows, cols, form), "mxh_dequant")
+    res = out.download(np.float32, rows * cols).reshape(rows, cols)
+    out.close()
+    return res
+
+
+def host_matmul_rhs_t(type_: int, a: np.ndarray, w: np.ndarray, n: int, form: int = FORM_REF) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    m, k = a.shape
+    out = np.empty((m, n), dtype=np.float32)
+    check(lib.mxh_host_matmul_rhs_t(type_, ptr(a), m, k, ptr(w), w.nbytes, n, ptr(out), form), "matmul_rhs_t")
+    return out
+
+
+class Timer:
+    """Elapsed milliseconds of the work enqueued on the library stream."""
+
+    def __enter__(self):
+        check(lib.mxh_timer_begin(), "timer_begin")
+        return self
+
+    def __exit__(self, *exc):
+        ms = C.c_float()
+        check(lib.mxh_timer_end(C.byref(ms)), "timer_end")
+        self.ms = ms.value
+        return False

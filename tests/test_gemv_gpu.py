@@ -1,0 +1,169 @@
+"""Parity of the HIP dequant / GEMV kernels with the CPU oracle (GPU).
+
+Bars: dequantized weights bit-exact; GEMV fp32 output within 1e-3 relative
+(tested as |y - y_ref| <= 1e-3 * |y_ref| + 1e-5 * max|y_ref|, plus a global
+max-error / max-value bound of 1e-4).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mxo
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q4_K": mxo.Q4_K, "Q5_K": mxo.Q5_K, "Q8_0": mxo.Q8_0, "Q5_0": mxo.Q5_0, "F32": mxo.F32}
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return bool(np.all((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))))
+
+
+def random_blocks(rng, t, nblocks):
+    be, bb = mxo.BLOCK[t]
+    raw = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    if t in (mxo.Q4_K, mxo.Q5_K):
+        raw[:, 0:4] = (rng.standard_normal((nblocks, 2)) * 0.01).astype(np.float16).view(np.uint8)
+    elif t in (mxo.Q8_0, mxo.Q5_0):
+        raw[:, 0:2] = (rng.standard_normal((nblocks, 1)) * 0.01).astype(np.float16).view(np.uint8)
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "Q8_0", "Q5_0"])
+@pytest.mark.parametrize("form", [mxo.FORM_REF, mxo.FORM_GGML])
+def test_dequant_bit_exact_random_blocks(mxh, name, form):
+    t = TYPES[name]
+    rng = np.random.default_rng(100 + t + 7 * form)
+    rows, cols = 37, 256 * 6
+    raw = random_blocks(rng, t, rows * cols // mxo.BLOCK[t][0])
+    buf = mxh.DeviceBuffer.from_array(raw)
+    got = mxh.dequant(t, buf, rows, cols, form)
+    want = mxo.dequant(t, raw, rows, cols, form)
+    assert same_bits(got, want)
+
+
+def test_dequant_bit_exact_any_bits_including_nan_inf(mxh):
+    """Unconstrained bytes: fp16 d/dmin may be subnormal, inf or NaN."""
+    rng = np.random.default_rng(5)
+    for t in (mxo.Q4_K, mxo.Q5_K, mxo.Q8_0, mxo.Q5_0):
+        be, bb = mxo.BLOCK[t]
+        raw = rng.integers(0, 256, size=(64 * bb,), dtype=np.uint8)
+        buf = mxh.DeviceBuffer.from_array(raw)
+        for form in (0, 1):
+            assert same_bits(mxh.dequant(t, buf, 1, 64 * be, form), mxo.dequant(t, raw, 1, 64 * be, form))
+
+
+def test_f16_decode_exhaustive(mxh):
+    h = np.arange(65536, dtype=np.uint16)
+    buf = mxh.DeviceBuffer.from_array(h.view(np.uint8))
+    got = mxh.dequant(mxo.F16, buf, 1, 65536)
+    want = mxo.dequant(mxo.F16, h.view(np.uint8), 1, 65536)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))  # NaN payloads too
+
+
+def check_close(got, want, rtol=1e-3):
+    scale = float(np.abs(want).max()) or 1.0
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= rtol * np.abs(want) + 1e-5 * scale), f"max err {err.max()} scale {scale}"
+    assert err.max() / scale <= 1e-4, f"max err / max value = {err.max() / scale}"
+
+
+def run_gemv(mxh, t, w, x, n, k, form=mxo.FORM_REF):
+    wb = mxh.DeviceBuffer.from_array(w)
+    xb = mxh.DeviceBuffer.from_array(x)
+    yb = mxh.DeviceBuffer(n * 4)
+    mxh.gemv(t, wb, xb, yb, n, k, form)
+    return yb.download(np.float32, n)
+
+
+GEMV_CASES = [
+    ("Q4_K", 4096, 4096), ("Q4_K", 12288, 4096), ("Q4_K", 4096, 12288), ("Q4_K", 151936, 4096),
+    ("Q4_K", 1, 256), ("Q4_K", 7, 512), ("Q4_K", 1000, 14336), ("Q4_K", 24, 2816),
+    ("Q5_K", 1024, 4096), ("Q5_K", 4096, 14336), ("Q5_K", 9, 256),
+    ("Q8_0", 151936, 4096), ("Q8_0", 1024, 1024), ("Q8_0", 3, 32), ("Q8_0", 5, 96), ("Q8_0", 1, 3072),
+    ("Q5_0", 256, 512), ("Q5_0", 7, 96), ("F32", 100, 512), ("F32", 3, 32),
+]
+
+
+@pytest.mark.parametrize("name,n,k", GEMV_CASES, ids=[f"{a}-{b}x{c}" for a, b, c in GEMV_CASES])
+def test_gemv_vs_oracle(mxh, name, n, k):
+    t = TYPES[name]
+    rng = np.random.default_rng(n * 31 + k)
+    wf = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+    w = mxo.quantize(t, wf)
+    x = rng.standard_normal(k, dtype=np.float32)
+    for form in ((mxo.FORM_REF, mxo.FORM_GGML) if t in (mxo.Q4_K, mxo.Q5_K) and n * k <= 1 << 24 else (mxo.FORM_REF,)):
+        got = run_gemv(mxh, t, w, x, n, k, form)
+        want = mxo.matmul_rhs_t(t, x, w, n, form)[0]
+        check_close(got, want)
+
+
+def test_gemv_reference_kat_blocks(mxh):
+    """Crafted blocks of the reference parity test, every row the same, x = ones."""
+    import json
+    from pathlib import Path
+    kat = json.loads((Path(__file__).parent / "golden" / "reference_kat.json").read_text())
+    for name in ("Q4_K", "Q5_0", "Q8_0"):
+        t = TYPES[name]
+        be = mxo.BLOCK[t][0]
+        blk = np.frombuffer(bytes.fromhex(kat[name]["block_hex"]), np.uint8)
+        y = run_gemv(mxh, t, np.tile(blk, be), np.ones(be, np.float32), be, be)
+        assert np.all(y == kat[name]["ones_dot"]), (name, y[:4])
+
+
+def test_matmul_rhs_t_multi_row(mxh):
+    rng = np.random.default_rng(77)
+    m, n, k = 5, 300, 1024
+    w = mxo.quantize(mxo.Q4_K, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    got = mxh.host_matmul_rhs_t(mxo.Q4_K, a, w, n)
+    want = mxo.matmul_rhs_t(mxo.Q4_K, a, w, n)
+    check_close(got, want)
+
+
+def test_host_vector_ops(mxh):
+    import ctypes as C
+    lib = mxh.lib
+    rng = np.random.default_rng(3)
+    K, N, stride = 128, 50, 160
+    vec = rng.standard_normal(K).astype(np.float32)
+    rows = rng.standard_normal(N * stride).astype(np.float32)
+    out = np.empty(N, np.float32)
+    mxh.check(lib.mxh_host_vec_dot_rows(mxh.ptr(vec), mxh.ptr(rows), mxh.ptr(out), K, N, stride))
+    want = rows.reshape(N, stride)[:, :K].astype(np.float64) @ vec.astype(np.float64)
+    np.testing.assert_allclose(out, want.astype(np.float32), rtol=1e-6, atol=1e-6)
+    # ring: head 13 of seq_max N, len 40
+    head, ln = 13, 40
+    out2 = np.empty(ln, np.float32)
+    mxh.check(lib.mxh_host_vec_dot_rows_ring(mxh.ptr(vec), mxh.ptr(rows), head, N, ln, K, stride, mxh.ptr(out2)))
+    np.testing.assert_allclose(out2, want[[(head + j) % N for j in range(ln)]].astype(np.float32), rtol=1e-6, atol=1e-6)
+    # rows x cols
+    v2 = rng.standard_normal(N).astype(np.float32)
+    out3 = np.empty(K, np.float32)
+    mxh.check(lib.mxh_host_vec_mul_rows_cols(mxh.ptr(v2), mxh.ptr(rows), mxh.ptr(out3), N, K, stride))
+    want3 = v2.astype(np.float64) @ rows.reshape(N, stride)[:, :K].astype(np.float64)
+    np.testing.assert_allclose(out3, want3.astype(np.float32), rtol=1e-6, atol=1e-6)
+    out4 = np.empty(K, np.float32)
+    mxh.check(lib.mxh_host_matvec_strided(mxh.ptr(v2), mxh.ptr(rows), mxh.ptr(out4), N, K, stride))
+    np.testing.assert_array_equal(out4, out3)
+    # F32 matmul known answer (tests/test_cuda_quantized_matmul.cpp:57-90)
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    c = np.empty((2, 2), np.float32)
+    mxh.check(lib.mxh_host_matmul_f32(mxh.ptr(a), mxh.ptr(b), mxh.ptr(c), 2, 3, 2))
+    assert c.tolist() == [[58, 64], [139, 154]]
+
+
+def test_argument_errors_are_reported_not_launched(mxh):
+    buf = mxh.DeviceBuffer(1 << 16)
+    xb = mxh.DeviceBuffer(4096)
+    yb = mxh.DeviceBuffer(4096)
+    lib = mxh.lib
+    assert lib.mxh_gemv(mxo.Q4_K, buf.ptr, xb.ptr, yb.ptr, 4, 100, 0) == -1      # k not a block multiple
+    assert b"blocks" in lib.mxh_last_error()
+    assert lib.mxh_gemv(mxo.Q4_K, buf.ptr + 4, xb.ptr, yb.ptr, 4, 256, 0) == -1  # misaligned weights
+    assert lib.mxh_gemv(99, buf.ptr, xb.ptr, yb.ptr, 4, 256, 0) == -1            # unknown type
+    assert lib.mxh_gemv(mxo.Q4_K, buf.ptr, xb.ptr, yb.ptr, 0, 256, 0) == -1      # empty
+    assert lib.mxh_dequant(mxo.Q4_K, buf.ptr, yb.ptr, 1, 100, 0) == -1
