@@ -140,6 +140,59 @@ int mxh_host_vec_dot_rows_ring(const float *vec, const float *ring, size_t head,
 int mxh_host_vec_mul_rows_cols(const float *vec, const float *rows, float *out, size_t nrows, size_t ncols,
                                size_t stride);
 
+/* ---- device-resident decoder model ------------------------------------ */
+/* Replaces the runtime's per-token stack walk (run_stack_forward,
+ * src/api/minxfmr.cpp:544-663) and decode loop (src/api/minxfmr.cpp:1849-2390)
+ * for llama-family GGUF models (qwen2/qwen3/llama tensor names): weights,
+ * fp16 KV cache and activations stay in HBM; one token step is one HIP graph
+ * replay with no host round trip. */
+typedef struct mxh_model mxh_model;
+
+typedef struct {
+    int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_ctx;
+    float eps, rope_theta;
+    int has_qk_norm, has_bias, type_wq, type_wv, type_wffn_down, type_output, type_embd;
+    int64_t weight_bytes;      /* HBM bytes of every uploaded tensor */
+    int64_t step_read_bytes;   /* weight bytes one decode step streams (layers + lm-head) */
+} mxh_model_config;
+
+enum {
+    MXH_MODEL_ROPE_NEOX = 1,    /* (i, i + rot/2) pairs; default (2i, 2i+1) as rope.cpp:39-45 */
+    MXH_MODEL_GGML_FORM = 4,    /* ggml Q4_K/Q5_K scale unpacking instead of the reference CPU form */
+    MXH_MODEL_NO_QK_NORM = 8,   /* ignore attn_{q,k}_norm (reference layer semantics) */
+    MXH_MODEL_NO_GRAPH = 16     /* enqueue kernels directly instead of replaying HIP graphs */
+};
+
+/* Load a GGUF file into HBM with room for n_ctx positions.
+ * Replaces minxfmr_open's load path (src/api/minxfmr.cpp:702-1415). */
+int mxh_model_open(const char *gguf_path, int n_ctx, int flags, mxh_model **out);
+int mxh_model_config_get(const mxh_model *m, mxh_model_config *cfg);
+/* Position 0, empty cache.  Replaces kvcache_reset (src/cache/kv_cache.cpp:77-83). */
+int mxh_model_reset(mxh_model *m);
+int mxh_model_position(const mxh_model *m);
+/* Run `token` at the current position and advance.  logits (n_vocab floats)
+ * and trace ((n_layer + 1) * n_embd floats: hidden after each layer, then the
+ * final-normed hidden) are host buffers and may be NULL.  Synchronous. */
+int mxh_model_step(mxh_model *m, int token, float *logits, float *trace);
+/* Greedy generation from position 0: prefill n_prompt ids, then n_gen
+ * decode steps; out receives n_gen ids.  prefill_ms / decode_ms (nullable)
+ * receive the device time of each phase.  Synchronous. */
+int mxh_model_generate(mxh_model *m, const int *prompt, int n_prompt, int n_gen, int *out, float *prefill_ms,
+                       float *decode_ms);
+void mxh_model_close(mxh_model *m);
+
+/* Seeded synthetic GGUF writer (weights N(0, 0.02) quantized per type, norms
+ * F32 near 1), for benchmarks on models that cannot be downloaded.  No
+ * reference counterpart.  Types are GGUF ids; attn_v_type / ffn_down_type
+ * of -1 mean wtype. */
+typedef struct {
+    const char *arch;
+    int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, ctx;
+    float rope_theta, eps;
+    int qk_norm, tied, wtype, out_type, embd_type, attn_v_type, ffn_down_type;
+} mxh_synth_arch;
+int mxh_write_synthetic_gguf(const char *path, const mxh_synth_arch *arch, uint64_t seed, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -197,7 +197,7 @@ int mxh_gemv(int type, const void* w, const float* x, float* y, int64_t n, int64
     if (!x || !y || !aligned(x, 16)) return set_error(MXH_ERR_ARG, "x must be non-null and 16-byte aligned");
     if (n <= 0 || k <= 0 || row_bytes(type, k) == 0)
         return set_error(MXH_ERR_ARG, "gemv: k=%lld is not a whole number of type-%d blocks", (long long)k, type);
-    int rc = gemv_launch(type, w, x, y, n, k, form, g_ctx.stream);
+    int rc = gemv_launch(type, w, x, y, nullptr, n, k, form, g_ctx.stream);
     if (rc == MXH_ERR_ARG) return set_error(rc, "gemv: unsupported shape n=%lld k=%lld", (long long)n, (long long)k);
     if (rc == MXH_ERR_UNSUPPORTED) return set_error(rc, "gemv: unsupported type %d", type);
     return check_hip(hipGetLastError(), "gemv launch");

@@ -275,8 +275,9 @@ struct F32W {
 };
 
 template <template <int> class T, int R>
+// y[row] = W[row] . x (+ res[row] when res is given; res may alias y)
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                        float* __restrict__ y, int n, int k, int form) {
+                                                        float* y, const float* res, int n, int k, int form) {
     extern __shared__ float xs[];
     // stage x (all K values) into padded LDS
     for (int e = threadIdx.x * 4; e < k; e += kThreads * 4)
@@ -298,17 +299,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restric
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float s = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < n) y[row0 + r] = s;
+        if (lane == 0 && row0 + r < n) y[row0 + r] = res ? s + res[row0 + r] : s;
     }
 }
 
 template <template <int> class T, int R>
-void launch_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k, int form, hipStream_t st) {
+void launch_gemv(const void* w, const float* x, float* y, const float* res, int64_t n, int64_t k, int form,
+                 hipStream_t st) {
     const int rows_per_block = kWaves * R;
     const unsigned grid = (unsigned)((n + rows_per_block - 1) / rows_per_block);
     const size_t lds = (size_t)(k + (k >> 4)) * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<T, R>), dim3(grid), dim3(kThreads), lds, st, (const uint8_t*)w, x, y, (int)n,
-                       (int)k, form);
+    hipLaunchKernelGGL((gemv_kernel<T, R>), dim3(grid), dim3(kThreads), lds, st, (const uint8_t*)w, x, y, res,
+                       (int)n, (int)k, form);
 }
 
 }  // namespace
@@ -316,15 +318,15 @@ void launch_gemv(const void* w, const float* x, float* y, int64_t n, int64_t k, 
 // max K whose padded x fits the 64 KiB of LDS one workgroup may use
 constexpr int64_t kGemvMaxK = 15360;
 
-int gemv_launch(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int form,
+int gemv_launch(int type, const void* w, const float* x, float* y, const float* res, int64_t n, int64_t k, int form,
                 hipStream_t st) {
     if (k % 32 || k > kGemvMaxK || n <= 0 || n > INT32_MAX) return MXH_ERR_ARG;
     switch (type) {
-    case MXH_Q4_K: launch_gemv<Q4K, 2>(w, x, y, n, k, form, st); break;
-    case MXH_Q5_K: launch_gemv<Q5K, 2>(w, x, y, n, k, form, st); break;
-    case MXH_Q8_0: launch_gemv<Q80, 2>(w, x, y, n, k, form, st); break;
-    case MXH_Q5_0: launch_gemv<Q50, 2>(w, x, y, n, k, form, st); break;
-    case MXH_F32: launch_gemv<F32W, 2>(w, x, y, n, k, form, st); break;
+    case MXH_Q4_K: launch_gemv<Q4K, 2>(w, x, y, res, n, k, form, st); break;
+    case MXH_Q5_K: launch_gemv<Q5K, 2>(w, x, y, res, n, k, form, st); break;
+    case MXH_Q8_0: launch_gemv<Q80, 2>(w, x, y, res, n, k, form, st); break;
+    case MXH_Q5_0: launch_gemv<Q50, 2>(w, x, y, res, n, k, form, st); break;
+    case MXH_F32: launch_gemv<F32W, 2>(w, x, y, res, n, k, form, st); break;
     default: return MXH_ERR_UNSUPPORTED;
     }
     return MXH_OK;

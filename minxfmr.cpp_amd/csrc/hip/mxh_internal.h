@@ -1,6 +1,7 @@
 // mxh_internal.h — launchers shared between the kernel files and the C ABI.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -15,7 +16,8 @@ int check_hip(hipError_t e, const char* what);
 
 hipStream_t lib_stream();
 
-int gemv_launch(int type, const void* w, const float* x, float* y, int64_t n, int64_t k, int form, hipStream_t st);
+int gemv_launch(int type, const void* w, const float* x, float* y, const float* res, int64_t n, int64_t k, int form,
+                hipStream_t st);
 int dequant_launch(int type, const void* w, float* out, int64_t rows, int64_t cols, int form, hipStream_t st);
 
 // small F32 vector ops (attention over host caches, F32 weights)
@@ -24,5 +26,19 @@ int vec_dot_rows_launch(const float* vec, const float* rows, float* out, int64_t
 int vec_mul_rows_cols_launch(const float* vec, const float* rows, float* out, int64_t nrows, int64_t ncols,
                              int64_t stride, hipStream_t st);
 int matmul_f32_launch(const float* a, const float* b, float* out, int64_t m, int64_t k, int64_t n, hipStream_t st);
+
+// decoder-step kernels (mxh_layer.hip)
+int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, hipStream_t st);
+int qkv_post_launch(float* qkv, const float* bias, const float* qn, const float* kn, const double* rope_cs,
+                    const int* pos, __half* kc, __half* vc, int nh, int nkv, int hd, float eps, int neox,
+                    int rope_half, hipStream_t st);
+int attention_launch(const float* q, const __half* kc, const __half* vc, const int* pos, float* part, float* out,
+                     int nh, int nkv, int hd, int n_ctx, hipStream_t st);
+size_t attention_scratch_floats(int nh, int hd, int n_ctx);
+int silu_mul_launch(const float* gu, float* h, int n, hipStream_t st);
+int embed_launch(int type, const void* w, const int* tokens, const int* pos, float* x, int cols, int form,
+                 hipStream_t st);
+int argmax_launch(const float* logits, int n, int* tokens, const int* pos, hipStream_t st);
+int add_int_launch(int* p, int v, hipStream_t st);
 
 }  // namespace mxh

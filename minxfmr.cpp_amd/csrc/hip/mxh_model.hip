@@ -1,0 +1,505 @@
+// mxh_model.hip — a GGUF decoder model resident in HBM and its decode step.
+//
+// One token step runs entirely on the device with no host round trip:
+//   embed -> n_layer x [rmsnorm, fused QKV GEMV, bias/QK-norm/RoPE/KV-append,
+//   split-K attention, Wo GEMV + residual, rmsnorm, fused gate|up GEMV,
+//   SiLU*up, down GEMV + residual] -> final rmsnorm -> lm-head GEMV -> argmax.
+// The token and position live in device memory, so the step is captured once
+// into a HIP graph and replayed per token; generated ids accumulate in a
+// device token array.  Reference path being replaced: run_stack_forward +
+// the generate loop (src/api/minxfmr.cpp:544-663, 1417-2171) over
+// transformer_forward_single_layer (src/transformer/transformer.cpp:330-755).
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../host/mxh_gguf.h"
+#include "mxh_internal.h"
+
+using namespace mxh;
+
+namespace {
+
+struct DevW {
+    const void* p = nullptr;
+    int type = -1;
+    int64_t rows = 0, cols = 0;
+};
+
+struct Layer {
+    DevW qkv;         // fused [Wq; Wk; Wv] when all three share a type
+    DevW q, k, v;     // otherwise separate
+    bool qkv_fused = false;
+    DevW o, gu, g, u, down;
+    bool gu_fused = false;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    const float* bias = nullptr;  // [bq | bk | bv] or null
+    __half *kc = nullptr, *vc = nullptr;
+};
+
+}  // namespace
+
+struct mxh_model {
+    mxh_model_config cfg{};
+    int form = MXH_FORM_REF;
+    int neox = 0;
+    std::vector<Layer> layers;
+    DevW embd, out;
+    const float* out_norm = nullptr;
+    // device memory
+    uint8_t* blob = nullptr;  // weights + norms
+    size_t blob_bytes = 0;
+    __half* kv = nullptr;
+    double* rope_cs = nullptr;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *h = nullptr, *logits = nullptr,
+          *part = nullptr, *trace = nullptr;
+    int* tokens = nullptr;  // [n_ctx + 1]: prompt then generated ids
+    int* pos = nullptr;     // current position
+    int host_pos = 0;
+    bool trace_on = false;
+    hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
+};
+
+namespace {
+
+int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hipStream_t st) {
+    return gemv_launch(w.type, w.p, x, y, res, w.rows, w.cols, form, st);
+}
+
+// Enqueue one token step at the device position.  with_head: run the final
+// norm, lm-head and argmax (writing tokens[pos+1]); without: prompt step.
+int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
+    const mxh_model_config& c = m->cfg;
+    const int d = c.n_embd, hd = c.head_dim, nh = c.n_head, nkv = c.n_head_kv;
+    const int qd = nh * hd, kvd = nkv * hd;
+    int rc = MXH_OK;
+    // embedding of tokens[pos]: the position counter indexes the token array
+    rc |= embed_launch(m->embd.type, m->embd.p, m->tokens, m->pos, m->x, d, m->form, st);
+    for (int l = 0; l < c.n_layer; ++l) {
+        const Layer& L = m->layers[(size_t)l];
+        rc |= rmsnorm_launch(m->x, L.attn_norm, m->xn, d, c.eps, st);
+        if (L.qkv_fused) {
+            rc |= gemv(L.qkv, m->xn, m->qkv, nullptr, m->form, st);
+        } else {
+            rc |= gemv(L.q, m->xn, m->qkv, nullptr, m->form, st);
+            rc |= gemv(L.k, m->xn, m->qkv + qd, nullptr, m->form, st);
+            rc |= gemv(L.v, m->xn, m->qkv + qd + kvd, nullptr, m->form, st);
+        }
+        rc |= qkv_post_launch(m->qkv, L.bias, L.q_norm, L.k_norm, m->rope_cs, m->pos, L.kc, L.vc, nh, nkv, hd, c.eps,
+                              m->neox, hd / 2, st);
+        rc |= attention_launch(m->qkv, L.kc, L.vc, m->pos, m->part, m->att, nh, nkv, hd, c.n_ctx, st);
+        rc |= gemv(L.o, m->att, m->x, m->x, m->form, st);
+        rc |= rmsnorm_launch(m->x, L.ffn_norm, m->xn, d, c.eps, st);
+        if (L.gu_fused) {
+            rc |= gemv(L.gu, m->xn, m->gu, nullptr, m->form, st);
+        } else {
+            rc |= gemv(L.g, m->xn, m->gu, nullptr, m->form, st);
+            rc |= gemv(L.u, m->xn, m->gu + c.n_ff, nullptr, m->form, st);
+        }
+        rc |= silu_mul_launch(m->gu, m->h, c.n_ff, st);
+        rc |= gemv(L.down, m->h, m->x, m->x, m->form, st);
+        if (m->trace_on) rc |= check_hip(hipMemcpyAsync(m->trace + (size_t)l * d, m->x, sizeof(float) * d,
+                                                        hipMemcpyDeviceToDevice, st), "trace copy");
+    }
+    if (with_head) {
+        rc |= rmsnorm_launch(m->x, m->out_norm, m->xn, d, c.eps, st);
+        if (m->trace_on) rc |= check_hip(hipMemcpyAsync(m->trace + (size_t)c.n_layer * d, m->xn, sizeof(float) * d,
+                                                        hipMemcpyDeviceToDevice, st), "trace copy");
+        rc |= gemv(m->out, m->xn, m->logits, nullptr, m->form, st);
+        rc |= argmax_launch(m->logits, (int)m->out.rows, m->tokens, m->pos, st);
+    }
+    rc |= add_int_launch(m->pos, 1, st);
+    return rc ? set_error(MXH_ERR_HIP, "step enqueue failed") : MXH_OK;
+}
+
+int capture(mxh_model* m, bool with_head, hipGraphExec_t* out) {
+    hipStream_t st = lib_stream();
+    hipGraph_t g = nullptr;
+    if (int rc = check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture")) return rc;
+    const int rc = enqueue_step(m, with_head, st);
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc) return rc;
+    if (int r2 = check_hip(e, "end capture")) return r2;
+    const hipError_t ie = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    return check_hip(ie, "graph instantiate");
+}
+
+}  // namespace
+
+namespace {
+
+struct Placement {
+    const GgufTensor* t;
+    size_t off;
+};
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int free_model(mxh_model* m) {
+    if (!m) return MXH_OK;
+    (void)hipStreamSynchronize(lib_stream());
+    if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
+    if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
+    void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
+                    m->trace, m->tokens, m->pos};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    delete m;
+    return MXH_OK;
+}
+
+template <typename T>
+int dalloc(T** p, size_t count) {
+    if (hipMalloc((void**)p, sizeof(T) * count + 256) != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return set_error(MXH_ERR_OOM, "device allocation of %zu bytes failed", sizeof(T) * count);
+    }
+    return MXH_OK;
+}
+
+bool gemv_type_ok(int t) { return t == MXH_Q4_K || t == MXH_Q5_K || t == MXH_Q8_0 || t == MXH_Q5_0 || t == MXH_F32; }
+
+}  // namespace
+
+extern "C" {
+
+int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out) {
+    if (!gguf_path || !out || n_ctx <= 0) return set_error(MXH_ERR_ARG, "model_open: bad arguments");
+    *out = nullptr;
+    if (int rc = mxh_init(0)) return rc;
+    GgufFile f;
+    std::string err;
+    if (!f.open(gguf_path, &err)) return set_error(MXH_ERR_ARG, "model_open: %s", err.c_str());
+
+    mxh_model* m = new mxh_model();
+    mxh_model_config& c = m->cfg;
+    c.n_layer = (int)f.arch_num("block_count", 0);
+    c.n_embd = (int)f.arch_num("embedding_length", 0);
+    c.n_head = (int)f.arch_num("attention.head_count", 0);
+    c.n_head_kv = (int)f.arch_num("attention.head_count_kv", c.n_head);
+    c.n_ff = (int)f.arch_num("feed_forward_length", 0);
+    c.eps = (float)f.arch_num("attention.layer_norm_rms_epsilon", 1e-6);
+    c.rope_theta = (float)f.arch_num("rope.freq_base", 10000.0);
+    c.n_ctx = n_ctx;
+    // head width from key_length when present (the reference
+    // derives it from n_embd / n_head, wrong for Qwen3-0.6B)
+    c.head_dim = (int)f.arch_num("attention.key_length", c.n_head > 0 ? c.n_embd / c.n_head : 0);
+    m->form = (flags & MXH_MODEL_GGML_FORM) ? MXH_FORM_GGML : MXH_FORM_REF;
+    m->neox = (flags & MXH_MODEL_ROPE_NEOX) ? 1 : 0;
+    auto fail = [&](int code, const std::string& msg) {
+        free_model(m);
+        return set_error(code, "model_open: %s", msg.c_str());
+    };
+    if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_head <= 0 || c.n_head_kv <= 0 || c.n_ff <= 0 || c.head_dim <= 0)
+        return fail(MXH_ERR_ARG, "missing architecture metadata");
+    if (c.n_head % c.n_head_kv || c.n_head / c.n_head_kv > 8 || c.head_dim > 128 || c.head_dim % 2)
+        return fail(MXH_ERR_UNSUPPORTED, "unsupported head layout");
+    const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+
+    // --- place every tensor in one HBM blob ---
+    std::vector<Placement> place;
+    size_t off = 0;
+    auto put = [&](const GgufTensor* t) -> size_t {
+        off = align_up(off, 256);
+        const size_t o = off;
+        place.push_back({t, o});
+        off += t->nbytes;
+        return o;
+    };
+    // contiguous run of same-typed matrices sharing cols -> one fused matrix
+    auto put_run = [&](std::vector<const GgufTensor*> ts) -> size_t {
+        off = align_up(off, 256);
+        const size_t o = off;
+        for (const GgufTensor* t : ts) {
+            place.push_back({t, off});
+            off += t->nbytes;
+        }
+        return o;
+    };
+    auto need = [&](const std::string& n, int64_t rows, int64_t cols) -> const GgufTensor* {
+        const GgufTensor* t = f.find(n);
+        if (!t || !t->data || t->rows() != rows || t->cols() != cols) return nullptr;
+        return t;
+    };
+    const GgufTensor* te = f.find("token_embd.weight");
+    if (!te || !te->data || te->cols() != c.n_embd) return fail(MXH_ERR_ARG, "token_embd.weight missing or misshaped");
+    const GgufTensor* to = f.find("output.weight");
+    if (to && (!to->data || to->cols() != c.n_embd)) return fail(MXH_ERR_ARG, "output.weight misshaped");
+    const GgufTensor* tn = f.find("output_norm.weight");
+    if (!tn || tn->type != MXH_F32 || tn->cols() != c.n_embd) return fail(MXH_ERR_ARG, "output_norm.weight missing");
+    c.n_vocab = (int)(to ? to->rows() : te->rows());
+    // every id the head can produce must index the embedding table
+    if (c.n_vocab > te->rows()) return fail(MXH_ERR_ARG, "output vocabulary larger than the embedding table");
+    const size_t o_embd = put(te);
+    const size_t o_out = to ? put(to) : o_embd;
+    const size_t o_onorm = put(tn);
+
+    struct LOff {
+        size_t qkv, q, k, v, o, gu, g, u, down, an, fn, qn, kn, bias;
+        const GgufTensor *tq, *tk, *tv, *to, *tg, *tu, *td, *bq, *bk, *bv;
+        bool fq, fgu;
+    };
+    std::vector<LOff> lo((size_t)c.n_layer);
+    for (int l = 0; l < c.n_layer; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        LOff& L = lo[(size_t)l];
+        L.tq = need(p + "attn_q.weight", qd, c.n_embd);
+        L.tk = need(p + "attn_k.weight", kvd, c.n_embd);
+        L.tv = need(p + "attn_v.weight", kvd, c.n_embd);
+        L.to = need(p + "attn_output.weight", c.n_embd, qd);
+        L.tg = need(p + "ffn_gate.weight", c.n_ff, c.n_embd);
+        L.tu = need(p + "ffn_up.weight", c.n_ff, c.n_embd);
+        L.td = need(p + "ffn_down.weight", c.n_embd, c.n_ff);
+        if (!L.tq || !L.tk || !L.tv || !L.to || !L.tg || !L.tu || !L.td)
+            return fail(MXH_ERR_ARG, "layer " + std::to_string(l) + ": projection weight missing or misshaped");
+        for (const GgufTensor* t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
+            if (!gemv_type_ok(t->type)) return fail(MXH_ERR_UNSUPPORTED, t->name + ": unsupported type " + std::to_string(t->type));
+        L.fq = L.tq->type == L.tk->type && L.tk->type == L.tv->type;
+        if (L.fq) {
+            L.qkv = put_run({L.tq, L.tk, L.tv});
+        } else {
+            L.q = put(L.tq);
+            L.k = put(L.tk);
+            L.v = put(L.tv);
+        }
+        L.o = put(L.to);
+        L.fgu = L.tg->type == L.tu->type;
+        if (L.fgu) {
+            L.gu = put_run({L.tg, L.tu});
+        } else {
+            L.g = put(L.tg);
+            L.u = put(L.tu);
+        }
+        L.down = put(L.td);
+        auto norm = [&](const std::string& n, int64_t len, bool required, size_t* o) -> bool {
+            const GgufTensor* t = f.find(n);
+            if (!t) { *o = SIZE_MAX; return !required; }
+            if (t->type != MXH_F32 || t->cols() != len) return false;
+            *o = put(t);
+            return true;
+        };
+        if (!norm(p + "attn_norm.weight", c.n_embd, true, &L.an) || !norm(p + "ffn_norm.weight", c.n_embd, true, &L.fn))
+            return fail(MXH_ERR_ARG, "layer " + std::to_string(l) + ": norm weights missing");
+        if (flags & MXH_MODEL_NO_QK_NORM) {
+            L.qn = L.kn = SIZE_MAX;
+        } else if (!norm(p + "attn_q_norm.weight", c.head_dim, false, &L.qn) ||
+                   !norm(p + "attn_k_norm.weight", c.head_dim, false, &L.kn)) {
+            return fail(MXH_ERR_ARG, "layer " + std::to_string(l) + ": QK-norm weights misshaped");
+        }
+        L.bq = f.find(p + "attn_q.bias");
+        L.bk = f.find(p + "attn_k.bias");
+        L.bv = f.find(p + "attn_v.bias");
+        L.bias = SIZE_MAX;
+        if (L.bq || L.bk || L.bv) {
+            if (!L.bq || !L.bk || !L.bv || L.bq->type != MXH_F32 || L.bk->type != MXH_F32 || L.bv->type != MXH_F32 ||
+                L.bq->cols() != qd || L.bk->cols() != kvd || L.bv->cols() != kvd)
+                return fail(MXH_ERR_UNSUPPORTED, "layer " + std::to_string(l) + ": partial or misshaped q/k/v bias");
+            L.bias = put_run({L.bq, L.bk, L.bv});
+        }
+    }
+    m->blob_bytes = align_up(off, 256);
+    c.weight_bytes = (int64_t)m->blob_bytes;
+    if (int rc = dalloc(&m->blob, m->blob_bytes)) { free_model(m); return rc; }
+    for (const Placement& p : place)
+        if (int rc = check_hip(hipMemcpy(m->blob + p.off, p.t->data, p.t->nbytes, hipMemcpyHostToDevice), "weight upload")) {
+            free_model(m);
+            return rc;
+        }
+
+    auto dw = [&](size_t o, int type, int64_t rows, int64_t cols) { return DevW{m->blob + o, type, rows, cols}; };
+    auto fptr = [&](size_t o) -> const float* { return o == SIZE_MAX ? nullptr : (const float*)(m->blob + o); };
+    m->embd = dw(o_embd, te->type, te->rows(), te->cols());
+    m->out = to ? dw(o_out, to->type, to->rows(), to->cols()) : m->embd;
+    if (!gemv_type_ok(m->out.type)) return fail(MXH_ERR_UNSUPPORTED, "output projection type unsupported");
+    m->out_norm = fptr(o_onorm);
+    int64_t step_bytes = (int64_t)tensor_bytes(m->out.type, m->out.rows, m->out.cols);
+    m->layers.resize((size_t)c.n_layer);
+    for (int l = 0; l < c.n_layer; ++l) {
+        const LOff& L = lo[(size_t)l];
+        Layer& D = m->layers[(size_t)l];
+        D.qkv_fused = L.fq;
+        if (L.fq) D.qkv = dw(L.qkv, L.tq->type, qd + 2 * kvd, c.n_embd);
+        else {
+            D.q = dw(L.q, L.tq->type, qd, c.n_embd);
+            D.k = dw(L.k, L.tk->type, kvd, c.n_embd);
+            D.v = dw(L.v, L.tv->type, kvd, c.n_embd);
+        }
+        D.o = dw(L.o, L.to->type, c.n_embd, qd);
+        D.gu_fused = L.fgu;
+        if (L.fgu) D.gu = dw(L.gu, L.tg->type, 2 * (int64_t)c.n_ff, c.n_embd);
+        else {
+            D.g = dw(L.g, L.tg->type, c.n_ff, c.n_embd);
+            D.u = dw(L.u, L.tu->type, c.n_ff, c.n_embd);
+        }
+        D.down = dw(L.down, L.td->type, c.n_embd, c.n_ff);
+        D.attn_norm = fptr(L.an);
+        D.ffn_norm = fptr(L.fn);
+        D.q_norm = fptr(L.qn);
+        D.k_norm = fptr(L.kn);
+        D.bias = fptr(L.bias);
+        for (const GgufTensor* t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td}) step_bytes += (int64_t)t->nbytes;
+    }
+    c.step_read_bytes = step_bytes;
+    c.has_qk_norm = m->layers[0].q_norm != nullptr;
+    c.has_bias = m->layers[0].bias != nullptr;
+    c.type_wq = lo[0].tq->type;
+    c.type_wv = lo[0].tv->type;
+    c.type_wffn_down = lo[0].td->type;
+    c.type_output = m->out.type;
+    c.type_embd = m->embd.type;
+
+    // --- caches, RoPE table, activations ---
+    const size_t kv_per_layer = (size_t)n_ctx * kvd;
+    int rc = dalloc(&m->kv, 2 * kv_per_layer * (size_t)c.n_layer);
+    for (int l = 0; l < c.n_layer && !rc; ++l) {
+        m->layers[(size_t)l].kc = m->kv + (size_t)(2 * l) * kv_per_layer;
+        m->layers[(size_t)l].vc = m->kv + (size_t)(2 * l + 1) * kv_per_layer;
+    }
+    const int half = c.head_dim / 2;
+    if (!rc) {
+        // cos/sin of pos * theta^(-2i/rot) in double, as rope.cpp:26-31 computes them
+        std::vector<double> cs((size_t)n_ctx * half * 2);
+        for (int i = 0; i < half; ++i) {
+            const double inv_freq = 1.0 / std::pow((double)c.rope_theta, (2.0 * (double)i) / (double)c.head_dim);
+            for (int p = 0; p < n_ctx; ++p) {
+                const double ang = (double)p * inv_freq;
+                cs[((size_t)p * half + i) * 2] = std::cos(ang);
+                cs[((size_t)p * half + i) * 2 + 1] = std::sin(ang);
+            }
+        }
+        rc = dalloc(&m->rope_cs, cs.size());
+        if (!rc) rc = check_hip(hipMemcpy(m->rope_cs, cs.data(), cs.size() * sizeof(double), hipMemcpyHostToDevice), "rope table");
+    }
+    if (!rc) rc = dalloc(&m->x, (size_t)c.n_embd);
+    if (!rc) rc = dalloc(&m->xn, (size_t)std::max(c.n_embd, c.n_ff));
+    if (!rc) rc = dalloc(&m->qkv, (size_t)(qd + 2 * kvd));
+    if (!rc) rc = dalloc(&m->att, (size_t)qd);
+    if (!rc) rc = dalloc(&m->gu, 2 * (size_t)c.n_ff);
+    if (!rc) rc = dalloc(&m->h, (size_t)c.n_ff);
+    if (!rc) rc = dalloc(&m->logits, (size_t)c.n_vocab);
+    if (!rc) rc = dalloc(&m->part, attention_scratch_floats(c.n_head, c.head_dim, n_ctx));
+    if (!rc) rc = dalloc(&m->trace, (size_t)(c.n_layer + 1) * c.n_embd);
+    if (!rc) rc = dalloc(&m->tokens, (size_t)n_ctx + 1);
+    if (!rc) rc = dalloc(&m->pos, 1);
+    if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * ((size_t)n_ctx + 1)), "token init");
+    if (!rc) rc = check_hip(hipMemset(m->pos, 0, sizeof(int)), "position init");
+    if (!rc) rc = check_hip(hipDeviceSynchronize(), "model init");
+    if (rc) {
+        free_model(m);
+        return rc;
+    }
+    if (!(flags & MXH_MODEL_NO_GRAPH)) {
+        if ((rc = capture(m, false, &m->g_prefill)) || (rc = capture(m, true, &m->g_decode))) {
+            free_model(m);
+            return rc;
+        }
+    }
+    *out = m;
+    return MXH_OK;
+}
+
+int mxh_model_config_get(const mxh_model* m, mxh_model_config* cfg) {
+    if (!m || !cfg) return set_error(MXH_ERR_ARG, "config_get: null argument");
+    *cfg = m->cfg;
+    return MXH_OK;
+}
+
+int mxh_model_reset(mxh_model* m) {
+    if (!m) return set_error(MXH_ERR_ARG, "reset: null model");
+    m->host_pos = 0;
+    const int zero = 0;
+    if (int rc = check_hip(hipMemcpyAsync(m->pos, &zero, sizeof(int), hipMemcpyHostToDevice, lib_stream()), "reset"))
+        return rc;
+    return check_hip(hipStreamSynchronize(lib_stream()), "reset");
+}
+
+int mxh_model_position(const mxh_model* m) { return m ? m->host_pos : -1; }
+
+namespace {
+
+int run_step(mxh_model* m, bool with_head) {
+    hipStream_t st = lib_stream();
+    if (m->trace_on || !(with_head ? m->g_decode : m->g_prefill)) return enqueue_step(m, with_head, st);
+    return check_hip(hipGraphLaunch(with_head ? m->g_decode : m->g_prefill, st), "graph launch");
+}
+
+}  // namespace
+
+int mxh_model_step(mxh_model* m, int token, float* logits, float* trace) {
+    if (!m) return set_error(MXH_ERR_ARG, "step: null model");
+    if (token < 0 || token >= m->embd.rows) return set_error(MXH_ERR_ARG, "step: token %d out of range", token);
+    if (m->host_pos >= m->cfg.n_ctx) return set_error(MXH_ERR_ARG, "step: context of %d positions is full", m->cfg.n_ctx);
+    hipStream_t st = lib_stream();
+    if (int rc = check_hip(hipMemcpyAsync(m->tokens + m->host_pos, &token, sizeof(int), hipMemcpyHostToDevice, st), "token"))
+        return rc;
+    m->trace_on = trace != nullptr;
+    int rc = run_step(m, true);
+    m->trace_on = false;
+    if (rc) return rc;
+    m->host_pos++;
+    if (logits && (rc = check_hip(hipMemcpyAsync(logits, m->logits, sizeof(float) * m->cfg.n_vocab, hipMemcpyDeviceToHost, st), "logits")))
+        return rc;
+    if (trace && (rc = check_hip(hipMemcpyAsync(trace, m->trace, sizeof(float) * (m->cfg.n_layer + 1) * m->cfg.n_embd,
+                                                hipMemcpyDeviceToHost, st), "trace")))
+        return rc;
+    return check_hip(hipStreamSynchronize(st), "step");
+}
+
+int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen, int* out, float* prefill_ms,
+                       float* decode_ms) {
+    if (!m || !prompt || n_prompt <= 0 || n_gen <= 0 || !out) return set_error(MXH_ERR_ARG, "generate: bad arguments");
+    if (n_prompt + n_gen - 1 > m->cfg.n_ctx)
+        return set_error(MXH_ERR_ARG, "generate: %d + %d tokens exceed the context of %d", n_prompt, n_gen, m->cfg.n_ctx);
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= m->embd.rows) return set_error(MXH_ERR_ARG, "generate: prompt id %d out of range", prompt[i]);
+    if (int rc = mxh_model_reset(m)) return rc;
+    hipStream_t st = lib_stream();
+    hipEvent_t e0, e1, e2;
+    if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
+    (void)hipEventCreate(&e1);
+    (void)hipEventCreate(&e2);
+    int rc = check_hip(hipMemcpyAsync(m->tokens, prompt, sizeof(int) * n_prompt, hipMemcpyHostToDevice, st), "prompt");
+    if (!rc) rc = check_hip(hipEventRecord(e0, st), "event");
+    // prompt positions 0 .. n_prompt-2 need no logits; the last prompt token
+    // runs with the head and yields the first generated id (minxfmr.cpp:1860)
+    for (int i = 0; i < n_prompt - 1 && !rc; ++i) rc = run_step(m, false);
+    if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
+    for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true);
+    if (!rc) rc = check_hip(hipEventRecord(e2, st), "event");
+    if (!rc) rc = check_hip(hipMemcpyAsync(out, m->tokens + n_prompt, sizeof(int) * n_gen, hipMemcpyDeviceToHost, st), "ids");
+    if (!rc) rc = check_hip(hipStreamSynchronize(st), "generate");
+    if (!rc) {
+        m->host_pos = n_prompt + n_gen - 1;
+        float ms = 0.f;
+        if (prefill_ms) { (void)hipEventElapsedTime(&ms, e0, e1); *prefill_ms = ms; }
+        if (decode_ms) { (void)hipEventElapsedTime(&ms, e1, e2); *decode_ms = ms; }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipEventDestroy(e2);
+    return rc;
+}
+
+void mxh_model_close(mxh_model* m) { free_model(m); }
+
+int mxh_write_synthetic_gguf(const char* path, const mxh_synth_arch* a, uint64_t seed, int threads) {
+    if (!path || !a || !a->arch) return set_error(MXH_ERR_ARG, "write_synthetic_gguf: null argument");
+    SynthArch s;
+    s.arch = a->arch;
+    s.n_layer = a->n_layer; s.n_embd = a->n_embd; s.n_head = a->n_head; s.n_head_kv = a->n_head_kv;
+    s.head_dim = a->head_dim; s.n_ff = a->n_ff; s.n_vocab = a->n_vocab; s.ctx = a->ctx;
+    s.rope_theta = a->rope_theta; s.eps = a->eps; s.qk_norm = a->qk_norm; s.tied = a->tied;
+    s.wtype = a->wtype; s.out_type = a->out_type; s.embd_type = a->embd_type;
+    s.attn_v_type = a->attn_v_type; s.ffn_down_type = a->ffn_down_type;
+    std::string err;
+    if (!write_synthetic_gguf(path, s, seed, threads, &err)) return set_error(MXH_ERR_ARG, "%s", err.c_str());
+    return MXH_OK;
+}
+
+}  // extern "C"

@@ -32,6 +32,27 @@ def row_bytes(type_: int, cols: int) -> int:
     return cols // be * bb
 
 
+class ModelConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
+                                       "n_ctx")] + \
+               [("eps", C.c_float), ("rope_theta", C.c_float)] + \
+               [(n, C.c_int) for n in ("has_qk_norm", "has_bias", "type_wq", "type_wv", "type_wffn_down",
+                                       "type_output", "type_embd")] + \
+               [("weight_bytes", C.c_int64), ("step_read_bytes", C.c_int64)]
+
+
+class SynthArch(C.Structure):
+    _fields_ = [("arch", C.c_char_p)] + \
+               [(n, C.c_int) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff", "n_vocab",
+                                       "ctx")] + \
+               [("rope_theta", C.c_float), ("eps", C.c_float)] + \
+               [(n, C.c_int) for n in ("qk_norm", "tied", "wtype", "out_type", "embd_type", "attn_v_type",
+                                       "ffn_down_type")]
+
+
+MODEL_ROPE_NEOX, MODEL_GGML_FORM, MODEL_NO_QK_NORM, MODEL_NO_GRAPH = 1, 4, 8, 16
+
+
 def _load() -> C.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(f"{LIB_PATH} is not built; run `make -C {PKG_DIR}` (or __graft_entry__.build())")
@@ -61,6 +82,14 @@ def _load() -> C.CDLL:
         "mxh_host_vec_dot_rows": (ip, [vp, vp, vp, sz, sz, sz]),
         "mxh_host_vec_dot_rows_ring": (ip, [vp, vp, sz, sz, sz, sz, sz, vp]),
         "mxh_host_vec_mul_rows_cols": (ip, [vp, vp, vp, sz, sz, sz]),
+        "mxh_model_open": (ip, [C.c_char_p, ip, ip, C.POINTER(vp)]),
+        "mxh_model_config_get": (ip, [vp, C.POINTER(ModelConfig)]),
+        "mxh_model_reset": (ip, [vp]),
+        "mxh_model_position": (ip, [vp]),
+        "mxh_model_step": (ip, [vp, ip, vp, vp]),
+        "mxh_model_generate": (ip, [vp, vp, ip, ip, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+        "mxh_model_close": (None, [vp]),
+        "mxh_write_synthetic_gguf": (ip, [C.c_char_p, C.POINTER(SynthArch), C.c_uint64, ip]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -74,7 +103,9 @@ EXPORTED = (
     "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
     "mxh_download mxh_memset mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
-    "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols"
+    "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
+    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_generate mxh_model_close "
+    "mxh_write_synthetic_gguf"
 ).split()
 
 
@@ -178,3 +209,58 @@ class Timer:
         check(lib.mxh_timer_end(C.byref(ms)), "timer_end")
         self.ms = ms.value
         return False
+
+
+def write_synthetic_gguf(path, arch: str = "qwen3", *, n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab,
+                         ctx=4096, rope_theta=1e6, eps=1e-6, qk_norm=True, tied=False, wtype=Q4_K, out_type=Q8_0,
+                         embd_type=Q8_0, attn_v_type=-1, ffn_down_type=-1, seed=0, threads=0) -> None:
+    """Seeded synthetic GGUF written by the library's C++ writer (host only)."""
+    a = SynthArch(arch.encode(), n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, ctx, rope_theta, eps,
+                  int(qk_norm), int(tied), wtype, out_type, embd_type, attn_v_type, ffn_down_type)
+    check(lib.mxh_write_synthetic_gguf(str(path).encode(), C.byref(a), seed, threads), "write_synthetic_gguf")
+
+
+class Model:
+    """A GGUF decoder model resident in HBM (device-side decode step)."""
+
+    def __init__(self, path, n_ctx: int, flags: int = 0):
+        h = C.c_void_p()
+        check(lib.mxh_model_open(str(path).encode(), n_ctx, flags, C.byref(h)), "mxh_model_open")
+        self.h = h.value
+        cfg = ModelConfig()
+        check(lib.mxh_model_config_get(self.h, C.byref(cfg)), "config")
+        self.cfg = cfg
+
+    def reset(self) -> None:
+        check(lib.mxh_model_reset(self.h), "reset")
+
+    @property
+    def position(self) -> int:
+        return lib.mxh_model_position(self.h)
+
+    def step(self, token: int, logits: bool = True, trace: bool = False):
+        c = self.cfg
+        lg = np.empty(c.n_vocab, np.float32) if logits else None
+        tr = np.empty((c.n_layer + 1) * c.n_embd, np.float32) if trace else None
+        check(lib.mxh_model_step(self.h, token, ptr(lg) if lg is not None else None,
+                                 ptr(tr) if tr is not None else None), "step")
+        return lg, (tr.reshape(c.n_layer + 1, c.n_embd) if tr is not None else None)
+
+    def generate(self, prompt, n_gen: int):
+        """Greedy ids; returns (ids, prefill_ms, decode_ms)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_gen, np.int32)
+        pm, dm = C.c_float(), C.c_float()
+        check(lib.mxh_model_generate(self.h, ptr(p), p.size, n_gen, ptr(out), C.byref(pm), C.byref(dm)), "generate")
+        return out, pm.value, dm.value
+
+    def close(self) -> None:
+        if self.h:
+            lib.mxh_model_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

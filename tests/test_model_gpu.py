@@ -1,0 +1,132 @@
+"""Device-resident decode step vs the CPU oracle (GPU).
+
+Bars (north star): per-layer activations and logits within max-abs 2e-2 /
+relative 1e-2 of the CPU backend; greedy ids identical for the first 64
+generated tokens.  The oracle runs with an fp16-rounded KV cache for the
+activation comparisons (the GPU cache is fp16) and with the reference's fp32
+cache for the greedy-token comparison.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mxhip
+import mxo
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layer=3, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=300)
+VARIANTS = {
+    "q4k-qknorm": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True),
+    "q8-tied": dict(wtype=mxhip.Q8_0, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True, tied=True),
+    "q4k-mixed-q5k": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K, qk_norm=False,
+                          attn_v_type=mxhip.Q5_K, ffn_down_type=mxhip.Q5_K, arch="llama", rope_theta=5e5),
+    "q5_0-gqa8": dict(wtype=mxhip.Q5_0, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True, n_head=8,
+                      n_head_kv=1, head_dim=32),
+    "f32-hd128": dict(wtype=mxhip.F32, out_type=mxhip.F32, embd_type=mxhip.F32, n_head=2, n_head_kv=2, head_dim=128),
+}
+
+
+def build(tmp_path, name, **over):
+    kw = dict(TINY)
+    kw.update(VARIANTS[name])
+    kw.update(over)
+    arch = kw.pop("arch", "qwen3")
+    p = tmp_path / f"{name}.gguf"
+    mxhip.write_synthetic_gguf(p, arch, seed=11, **kw)
+    return p
+
+
+def close_enough(got, want, atol=2e-2, rtol=1e-2):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    return bool(np.all(err <= atol + rtol * np.abs(want))), float(err.max())
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+@pytest.mark.parametrize("flags", [0, mxhip.MODEL_ROPE_NEOX | mxhip.MODEL_GGML_FORM])
+def test_per_layer_activations_and_logits(mxh, tmp_path, name, flags):
+    p = build(tmp_path, name)
+    oflags = mxo.OPEN_KV_FP16 | (mxo.OPEN_ROPE_NEOX if flags & mxhip.MODEL_ROPE_NEOX else 0) | \
+        (mxo.OPEN_GGML_FORM if flags & mxhip.MODEL_GGML_FORM else 0)
+    gm = mxhip.Model(p, 64, flags)
+    om = mxo.Model(p, 64, oflags)
+    rng = np.random.default_rng(3)
+    worst = 0.0
+    for step in range(20):
+        tok = int(rng.integers(0, TINY["n_vocab"]))
+        lg, tr = gm.step(tok, trace=True)
+        olg, otr = om.step(tok, trace=True)
+        ok, e1 = close_enough(tr, otr)
+        assert ok, f"step {step}: hidden trace error {e1}"
+        ok, e2 = close_enough(lg, olg)
+        assert ok, f"step {step}: logits error {e2}"
+        worst = max(worst, e1 / max(1.0, float(np.abs(otr).max())), e2)
+    # much tighter than the bar: only summation order and fp32 rounding differ
+    assert worst < 1e-3, worst
+    gm.close()
+
+
+@pytest.mark.parametrize("name", ["q4k-qknorm", "q4k-mixed-q5k"])
+def test_graph_generate_matches_eager_steps_and_oracle(mxh, tmp_path, name):
+    p = build(tmp_path, name)
+    prompt = np.random.default_rng(5).integers(0, TINY["n_vocab"], 12).astype(np.int32)
+    gm = mxhip.Model(p, 128)
+    ids, _, _ = gm.generate(prompt, 48)
+    # eager path (no graphs) must give the same ids
+    em = mxhip.Model(p, 128, mxhip.MODEL_NO_GRAPH)
+    ids2, _, _ = em.generate(prompt, 48)
+    assert np.array_equal(ids, ids2)
+    # generating twice (reset) is reproducible
+    ids3, _, _ = gm.generate(prompt, 48)
+    assert np.array_equal(ids, ids3)
+    # oracle with the reference fp32 cache
+    om = mxo.Model(p, 128)
+    want = []
+    lg = None
+    for t in prompt:
+        lg, _ = om.step(int(t))
+    for _ in range(48):
+        nxt = mxo.lib.mxo_argmax(lg.ctypes.data, lg.size)
+        want.append(nxt)
+        lg, _ = om.step(nxt)
+    assert ids.tolist() == want
+
+
+def test_step_errors_are_reported(mxh, tmp_path):
+    p = build(tmp_path, "q8-tied")
+    gm = mxhip.Model(p, 4)
+    with pytest.raises(mxhip.MxhError, match="out of range"):
+        gm.step(TINY["n_vocab"])
+    for t in range(4):
+        gm.step(t, logits=False)
+    with pytest.raises(mxhip.MxhError, match="full"):
+        gm.step(0)
+    with pytest.raises(mxhip.MxhError):
+        mxhip.Model(tmp_path / "missing.gguf", 16)
+
+
+def test_qwen3_06b_config1_greedy_64_tokens(mxh, tmp_path):
+    """Qwen3-0.6B architecture, Q8_0 weights, tied
+    embeddings, 32-token seeded prompt (ids uniform in [0, 151936)); the first
+    64 greedy ids match the CPU oracle (fp32 cache, as the reference)."""
+    p = tmp_path / "qwen3-0.6b-q8.gguf"
+    mxhip.write_synthetic_gguf(p, "qwen3", n_layer=28, n_embd=1024, n_head=16, n_head_kv=8, head_dim=128, n_ff=3072,
+                               n_vocab=151936, ctx=40960, qk_norm=True, tied=True, wtype=mxhip.Q8_0,
+                               out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, seed=0x0C0F1, threads=16)
+    prompt = np.random.default_rng(0xC0F1).integers(0, 151936, 32).astype(np.int32)
+    gm = mxhip.Model(p, 256)
+    ids, _, _ = gm.generate(prompt, 64)
+    om = mxo.Model(p, 256, threads=16)
+    lg = None
+    for t in prompt:
+        lg, _ = om.step(int(t))
+    want, margins = [], []
+    for _ in range(64):
+        top2 = np.sort(lg)[-2:]
+        margins.append(float(top2[1] - top2[0]))
+        nxt = mxo.lib.mxo_argmax(lg.ctypes.data, lg.size)
+        want.append(nxt)
+        lg, _ = om.step(nxt)
+    mism = [i for i, (a, b) in enumerate(zip(ids.tolist(), want)) if a != b]
+    assert not mism, f"first mismatch at {mism[0]}, top-2 margin there {margins[mism[0]]:.3g}"
