@@ -1,0 +1,168 @@
+"""Headline benchmark: Qwen3-8B-shape Q4_K decode at batch 1 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--prompt P] [--no-cpu-baseline]
+
+Workload: a seeded synthetic GGUF with the
+Qwen3-8B architecture (36 layers, hidden 4096, 32/8 heads of 128, FFN 12288,
+vocab 151936, QK-norm), every 2D weight Q4_K, the lm-head Q8_0.  A P-token
+seeded prompt (default 512) is prefilled, W decode steps warm up, then
+exactly K greedy decode steps (default 256) are timed.  A step is one token
+through the whole device-resident stack plus the lm-head and argmax.
+
+One JSON line is printed.  `value` is decode tokens/s; `roofline` is for the
+dominant kernel, the Q4_K dequant-GEMV, timed with HIP events over every
+Q4_K GEMV of the model on its own HBM-resident weights; `cpu_baseline` is the
+CPU oracle decoding a bounded sample of the same model on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "minxfmr.cpp_amd", ROOT / "oracle"):
+    sys.path.insert(0, str(p))
+
+METRIC = "decode tok/s Qwen3-8B-shape Q4_K bs=1; Q4_K GEMV HBM GB/s vs ~8 TB/s peak"
+HBM_PEAK_GBS = 8000.0
+ARCH = dict(n_layer=36, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=12288, n_vocab=151936, ctx=40960,
+            rope_theta=1e6, eps=1e-6, qk_norm=True, tied=False)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_path(seed: int) -> Path:
+    d = Path(os.environ.get("MXH_BENCH_DIR", "/tmp"))
+    return d / f"mxh_bench_qwen3_8b_q4k_seed{seed}.gguf"
+
+
+def ensure_model(mxhip, seed: int) -> Path:
+    p = model_path(seed)
+    if p.exists() and p.stat().st_size > 4_000_000_000:
+        return p
+    t0 = time.time()
+    tmp = p.with_suffix(".tmp")
+    mxhip.write_synthetic_gguf(tmp, "qwen3", wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K, seed=seed,
+                               threads=min(16, os.cpu_count() or 8), **ARCH)
+    tmp.rename(p)
+    log(f"wrote synthetic model {p} ({p.stat().st_size / 1e9:.2f} GB) in {time.time() - t0:.1f}s")
+    return p
+
+
+def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
+    """Oracle decode on the host cores: greedy steps from position 0 until the
+    time budget is spent (a bounded sample of the same workload)."""
+    import numpy as np
+
+    import mxo
+
+    m = mxo.Model(path, n_ctx=64, threads=threads)
+    t0 = time.perf_counter()
+    n = 0
+    tok = int(prompt[0])
+    while True:
+        lg, _ = m.step(tok)
+        tok = int(np.argmax(lg))
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 48:
+            break
+    m.close()
+    return {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps (positions 0..{n - 1}, lm-head included) of the same model "
+                      f"by the C oracle with {threads} OpenMP threads, {el:.1f}s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--seed", type=int, default=8)
+    ap.add_argument("--gemv-reps", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build targets a single MI355X); --gpus {args.gpus} is not "
+              f"supported", file=sys.stderr)
+        return 2
+    import numpy as np
+
+    import mxhip
+
+    mxhip.init(0)
+    path = ensure_model(mxhip, args.seed)
+    n_ctx = args.prompt + args.warmup + args.steps + 8
+    t0 = time.time()
+    model = mxhip.Model(path, n_ctx)
+    cfg = model.cfg
+    log(f"model in HBM: {cfg.weight_bytes / 1e9:.2f} GB, {time.time() - t0:.1f}s; step reads "
+        f"{cfg.step_read_bytes / 1e9:.3f} GB of weights")
+    prompt = np.random.default_rng(args.seed).integers(0, cfg.n_vocab, args.prompt).astype(np.int32)
+
+    # prefill + first token, then untimed warmup steps
+    _, prefill_ms, _ = model.generate(prompt, 1)
+    model.decode(args.warmup)
+    mxhip.synchronize()
+    # timed region: exactly K decode steps, synchronized on both sides
+    t_start = time.perf_counter()
+    ids, dev_ms = model.decode(args.steps)
+    mxhip.synchronize()
+    wall_s = time.perf_counter() - t_start
+    tok_s = args.steps / wall_s
+    log(f"decode: {args.steps} steps in {wall_s * 1e3:.1f} ms wall ({dev_ms:.1f} ms device) -> {tok_s:.1f} tok/s; "
+        f"prefill {args.prompt} tokens {prefill_ms:.1f} ms")
+
+    # dominant kernel: Q4_K GEMV over the model's own weights
+    model.bench_gemv(mxhip.Q4_K, 1)
+    g_ms, g_launch, g_bytes = model.bench_gemv(mxhip.Q4_K, args.gemv_reps)
+    g_avg_us = g_ms * 1e3 / g_launch
+    g_bytes_launch = g_bytes / g_launch
+    gemv_gbs = g_bytes_launch / (g_avg_us * 1e-6) / 1e9
+    h_ms, h_launch, h_bytes = model.bench_gemv(mxhip.Q8_0, args.gemv_reps)
+    log(f"Q4_K GEMV: {g_launch} launches, avg {g_avg_us:.2f} us, {g_bytes_launch / 1e6:.2f} MB/launch -> "
+        f"{gemv_gbs:.0f} GB/s; Q8_0 lm-head {h_ms * 1e3 / h_launch:.1f} us -> "
+        f"{h_bytes / h_launch / (h_ms * 1e-3 / h_launch) / 1e9:.0f} GB/s")
+    step_bytes = cfg.step_read_bytes
+    model.close()
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_s * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"qwen3-8b-shape, Q4_K weights + Q8_0 lm-head, bs=1: {args.prompt}-token seeded "
+                               f"prompt prefill, then {args.steps} timed greedy decode steps",
+                   "global_batch": 1, "seq_len": args.prompt + args.warmup + args.steps},
+        "decode_weight_gbs": round(step_bytes / (wall_s / args.steps) / 1e9, 1),
+        "decode_hbm_frac": round(step_bytes / (wall_s / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "prefill_tok_s": round(args.prompt / (prefill_ms * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "Q4_K dequant-GEMV (gemv_kernel<Q4K>)",
+                     "per_launch_bytes": int(g_bytes_launch), "avg_launch_us": round(g_avg_us, 3)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(path, prompt, args.cpu_seconds, min(16, os.cpu_count() or 8))
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -179,6 +179,15 @@ int mxh_model_step(mxh_model *m, int token, float *logits, float *trace);
  * receive the device time of each phase.  Synchronous. */
 int mxh_model_generate(mxh_model *m, const int *prompt, int n_prompt, int n_gen, int *out, float *prefill_ms,
                        float *decode_ms);
+/* Continue greedy decoding for n_gen steps from the current position (the id
+ * at the position is the input); out (nullable) receives n_gen ids. */
+int mxh_model_decode(mxh_model *m, int n_gen, int *out, float *decode_ms);
+/* Enqueue every GEMV of the model whose weights have `type` (in layer order,
+ * then the lm-head) `reps` times on the library stream, on the model's own
+ * HBM-resident weights; reports device time, launch count and algorithmic
+ * bytes (weights + fp32 x and y).  Benchmark support, no reference
+ * counterpart. */
+int mxh_model_bench_gemv(mxh_model *m, int type, int reps, float *ms, int64_t *launches, int64_t *bytes);
 void mxh_model_close(mxh_model *m);
 
 /* Seeded synthetic GGUF writer (weights N(0, 0.02) quantized per type, norms

@@ -486,6 +486,63 @@ int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen,
     return rc;
 }
 
+int mxh_model_decode(mxh_model* m, int n_gen, int* out, float* decode_ms) {
+    if (!m || n_gen <= 0) return set_error(MXH_ERR_ARG, "decode: bad arguments");
+    const int p0 = m->host_pos;
+    if (p0 + n_gen > m->cfg.n_ctx)
+        return set_error(MXH_ERR_ARG, "decode: position %d + %d exceeds the context of %d", p0, n_gen, m->cfg.n_ctx);
+    hipStream_t st = lib_stream();
+    hipEvent_t e0, e1;
+    if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
+    (void)hipEventCreate(&e1);
+    int rc = check_hip(hipEventRecord(e0, st), "event");
+    for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true);
+    if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
+    if (!rc && out) rc = check_hip(hipMemcpyAsync(out, m->tokens + p0 + 1, sizeof(int) * n_gen, hipMemcpyDeviceToHost, st), "ids");
+    if (!rc) rc = check_hip(hipStreamSynchronize(st), "decode");
+    if (!rc) {
+        m->host_pos = p0 + n_gen;
+        if (decode_ms) (void)hipEventElapsedTime(decode_ms, e0, e1);
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
+int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* launches, int64_t* bytes) {
+    if (!m || reps <= 0 || !ms) return set_error(MXH_ERR_ARG, "bench_gemv: bad arguments");
+    hipStream_t st = lib_stream();
+    std::vector<const DevW*> ws;
+    for (const Layer& L : m->layers)
+        for (const DevW* w : {&L.qkv, &L.q, &L.k, &L.v, &L.o, &L.gu, &L.g, &L.u, &L.down})
+            if (w->p && w->type == type) ws.push_back(w);
+    if (m->out.type == type) ws.push_back(&m->out);
+    if (ws.empty()) return set_error(MXH_ERR_ARG, "bench_gemv: model has no matrices of type %d", type);
+    int64_t b = 0;
+    for (const DevW* w : ws) b += (int64_t)tensor_bytes(w->type, w->rows, w->cols) + 4 * (w->rows + w->cols);
+    hipEvent_t e0, e1;
+    if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
+    (void)hipEventCreate(&e1);
+    int rc = check_hip(hipEventRecord(e0, st), "event");
+    for (int r = 0; r < reps && !rc; ++r)
+        for (const DevW* w : ws) {
+            // x: a K-long activation buffer (xn holds max(n_embd, n_ff)); y: scratch wide enough for any row count
+            float* y = w->rows <= 2 * (int64_t)m->cfg.n_ff ? m->gu : m->logits;
+            rc = gemv(*w, m->xn, y, nullptr, m->form, st);
+            if (rc) break;
+        }
+    if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
+    if (!rc) rc = check_hip(hipEventSynchronize(e1), "bench_gemv");
+    if (!rc) {
+        (void)hipEventElapsedTime(ms, e0, e1);
+        if (launches) *launches = (int64_t)ws.size() * reps;
+        if (bytes) *bytes = b * reps;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
 void mxh_model_close(mxh_model* m) { free_model(m); }
 
 int mxh_write_synthetic_gguf(const char* path, const mxh_synth_arch* a, uint64_t seed, int threads) {

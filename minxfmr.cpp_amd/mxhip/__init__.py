@@ -89,6 +89,8 @@ def _load() -> C.CDLL:
         "mxh_model_step": (ip, [vp, ip, vp, vp]),
         "mxh_model_generate": (ip, [vp, vp, ip, ip, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mxh_model_close": (None, [vp]),
+        "mxh_model_decode": (ip, [vp, ip, vp, C.POINTER(C.c_float)]),
+        "mxh_model_bench_gemv": (ip, [vp, ip, ip, C.POINTER(C.c_float), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
         "mxh_write_synthetic_gguf": (ip, [C.c_char_p, C.POINTER(SynthArch), C.c_uint64, ip]),
     }
     for name, (res, args) in sig.items():
@@ -105,7 +107,7 @@ EXPORTED = (
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_generate mxh_model_close "
-    "mxh_write_synthetic_gguf"
+    "mxh_write_synthetic_gguf mxh_model_decode mxh_model_bench_gemv"
 ).split()
 
 
@@ -253,6 +255,19 @@ class Model:
         pm, dm = C.c_float(), C.c_float()
         check(lib.mxh_model_generate(self.h, ptr(p), p.size, n_gen, ptr(out), C.byref(pm), C.byref(dm)), "generate")
         return out, pm.value, dm.value
+
+    def decode(self, n_gen: int):
+        """Continue greedy decoding; returns (ids, decode_ms)."""
+        out = np.empty(n_gen, np.int32)
+        ms = C.c_float()
+        check(lib.mxh_model_decode(self.h, n_gen, ptr(out), C.byref(ms)), "decode")
+        return out, ms.value
+
+    def bench_gemv(self, type_: int, reps: int = 1):
+        """(device ms, launches, algorithmic bytes) of every `type_` GEMV of the model."""
+        ms, n, b = C.c_float(), C.c_int64(), C.c_int64()
+        check(lib.mxh_model_bench_gemv(self.h, type_, reps, C.byref(ms), C.byref(n), C.byref(b)), "bench_gemv")
+        return ms.value, n.value, b.value
 
     def close(self) -> None:
         if self.h:
