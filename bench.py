@@ -89,6 +89,7 @@ def main() -> int:
     ap.add_argument("--gemv-reps", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="enqueue kernels directly instead of replaying HIP graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build targets a single MI355X); --gpus {args.gpus} is not "
@@ -102,7 +103,7 @@ def main() -> int:
     path = ensure_model(mxhip, args.seed)
     n_ctx = args.prompt + args.warmup + args.steps + 8
     t0 = time.time()
-    model = mxhip.Model(path, n_ctx)
+    model = mxhip.Model(path, n_ctx, mxhip.MODEL_NO_GRAPH if args.eager else 0)
     cfg = model.cfg
     log(f"model in HBM: {cfg.weight_bytes / 1e9:.2f} GB, {time.time() - t0:.1f}s; step reads "
         f"{cfg.step_read_bytes / 1e9:.3f} GB of weights")

@@ -274,43 +274,164 @@ struct F32W {
     }
 };
 
-template <template <int> class T, int R>
-// y[row] = W[row] . x (+ res[row] when res is given; res may alias y)
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                        float* y, const float* res, int n, int k, int form) {
-    extern __shared__ float xs[];
-    // stage x (all K values) into padded LDS
-    for (int e = threadIdx.x * 4; e < k; e += kThreads * 4)
-        *reinterpret_cast<float4*>(xs + xpad(e)) = *reinterpret_cast<const float4*>(x + e);
+// Stage x into padded LDS.  With a norm weight, x is replaced by the
+// reference rmsnorm float(x / sqrt(mean(x^2) + eps)) * w (rmsnorm.cpp:5-26,
+// transformer.cpp:189-214); the sum of squares is a double block reduction
+// in a fixed order, so every workgroup computes identical inputs.
+__device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, const float* __restrict__ nw,
+                                        int k, float eps, double* red) {
+    if (!nw) {
+        for (int e = threadIdx.x * 4; e < k; e += kThreads * 4)
+            *reinterpret_cast<float4*>(xs + xpad(e)) = *reinterpret_cast<const float4*>(x + e);
+        __syncthreads();
+        return;
+    }
+    double ss = 0.0;
+    for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + e);
+        ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
+    const double inv = 1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps);
+    for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x + e);
+        const float4 g = *reinterpret_cast<const float4*>(nw + e);
+        float4 o;
+        o.x = (float)((double)v.x * inv) * g.x;
+        o.y = (float)((double)v.y * inv) * g.y;
+        o.z = (float)((double)v.z * inv) * g.z;
+        o.w = (float)((double)v.w * inv) * g.w;
+        *reinterpret_cast<float4*>(xs + xpad(e)) = o;
+    }
+    __syncthreads();
+}
+
+// Output modes (epilogues) of one GEMV launch.
+//  GEMV_PLAIN : y[r] = W[r].x (+ res[r])
+//  GEMV_SILU  : W = [gate; up] with n = 2F rows; y[i] = silu(gate_i) * up_i
+//               (transformer.cpp:183-185, 696-704) for i < F
+//  GEMV_ARGMAX: y = logits; additionally the greedy id (largest logit, lowest
+//               index on ties) goes to tokens[*pos + 1] and *pos advances —
+//               done by the last workgroup to finish (minxfmr.cpp:2091-2115)
+template <template <int> class T, int R, int MODE>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+    extern __shared__ float xs[];
+    __shared__ double red[kWaves];
+    __shared__ float wmax[kWaves];
+    __shared__ int widx[kWaves];
+    __shared__ int last;
+    stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * kWaves + wave) * R;
-    if (row0 >= n) return;
-    int rows[R];
+    const int n = a.n;
+    // rows this wave accumulates; in SILU mode rows [j] and [R/2 + j] are the
+    // gate and up rows of output i0 + j
+    constexpr int kOut = MODE == GEMV_SILU ? R / 2 : R;
+    const int out0 = (blockIdx.x * kWaves + wave) * kOut;
+    const int n_out = MODE == GEMV_SILU ? n / 2 : n;
+    float best = -INFINITY;
+    int best_i = 0x7fffffff;
+    if (out0 < n_out) {
+        int rows[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = min(row0 + r, n - 1);  // clamp loads in bounds
-    float acc[R];
+        for (int r = 0; r < kOut; ++r) {
+            const int o = min(out0 + r, n_out - 1);  // clamp loads in bounds
+            rows[r] = o;
+            if (MODE == GEMV_SILU) rows[kOut + r] = o + n_out;
+        }
+        float acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    const size_t rbytes = row_bytes(T<R>::kType, k);
-    const int nchunks = k >> 5;  // every chunk covers 32 elements
-    for (int c = lane; c < nchunks; c += 64) T<R>::run(w, rbytes, rows, c, xs, form, acc);
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        const size_t rbytes = row_bytes(T<R>::kType, a.k);
+        const int nchunks = a.k >> 5;  // every chunk covers 32 elements
+        for (int c = lane; c < nchunks; c += 64) T<R>::run(a.w, rbytes, rows, c, xs, a.form, acc);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const float s = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < n) y[row0 + r] = res ? s + res[row0 + r] : s;
+        for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < kOut; ++r) {
+                const int o = out0 + r;
+                if (o >= n_out) break;
+                float v;
+                if (MODE == GEMV_SILU) {
+                    const float g = acc[r];
+                    v = g / (1.0f + expf(-g)) * acc[kOut + r];
+                } else {
+                    v = a.res ? acc[r] + a.res[o] : acc[r];
+                }
+                a.y[o] = v;
+                if (MODE == GEMV_ARGMAX && (v > best || (v == best && o < best_i))) {
+                    best = v;
+                    best_i = o;
+                }
+            }
+        }
+    }
+    if constexpr (MODE == GEMV_ARGMAX) {
+        if (lane == 0) {
+            wmax[wave] = best;
+            widx[wave] = best_i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w2 = 1; w2 < kWaves; ++w2)
+                if (wmax[w2] > best || (wmax[w2] == best && widx[w2] < best_i)) {
+                    best = wmax[w2];
+                    best_i = widx[w2];
+                }
+            a.red_val[blockIdx.x] = best;
+            a.red_idx[blockIdx.x] = best_i;
+            __threadfence();
+            last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+        }
+        __syncthreads();
+        if (last) {
+            __threadfence();
+            // the last workgroup reduces the per-workgroup winners in index order
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int b = threadIdx.x; b < (int)gridDim.x; b += kThreads) {
+                const float v = __builtin_nontemporal_load(a.red_val + b);
+                const int i = __builtin_nontemporal_load(a.red_idx + b);
+                if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) { wmax[wave] = bv; widx[wave] = bi; }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                for (int w2 = 1; w2 < kWaves; ++w2)
+                    if (wmax[w2] > bv || (wmax[w2] == bv && widx[w2] < bi)) { bv = wmax[w2]; bi = widx[w2]; }
+                if (bi == 0x7fffffff) bi = 0;  // all-NaN logits
+                const int p = *a.pos;
+                a.tokens[p + 1] = bi;
+                *a.pos = p + 1;
+                *a.counter = 0;  // ready for the next launch
+            }
+        }
     }
 }
 
 template <template <int> class T, int R>
-void launch_gemv(const void* w, const float* x, float* y, const float* res, int64_t n, int64_t k, int form,
-                 hipStream_t st) {
-    const int rows_per_block = kWaves * R;
-    const unsigned grid = (unsigned)((n + rows_per_block - 1) / rows_per_block);
-    const size_t lds = (size_t)(k + (k >> 4)) * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<T, R>), dim3(grid), dim3(kThreads), lds, st, (const uint8_t*)w, x, y, res,
-                       (int)n, (int)k, form);
+int launch_gemv(const GemvArgs& a, int mode, hipStream_t st) {
+    const int rows_per_block = kWaves * (mode == GEMV_SILU ? R / 2 : R);
+    const int64_t n_out = mode == GEMV_SILU ? a.n / 2 : a.n;
+    const unsigned grid = (unsigned)((n_out + rows_per_block - 1) / rows_per_block);
+    const size_t lds = (size_t)(a.k + (a.k >> 4)) * sizeof(float);
+    if (mode == GEMV_PLAIN) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN>), dim3(grid), dim3(kThreads), lds, st, a);
+    else if (mode == GEMV_SILU) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU>), dim3(grid), dim3(kThreads), lds, st, a);
+    else {
+        if (grid > (unsigned)a.red_cap) return MXH_ERR_ARG;
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX>), dim3(grid), dim3(kThreads), lds, st, a);
+    }
+    return MXH_OK;
 }
 
 }  // namespace
@@ -318,18 +439,31 @@ void launch_gemv(const void* w, const float* x, float* y, const float* res, int6
 // max K whose padded x fits the 64 KiB of LDS one workgroup may use
 constexpr int64_t kGemvMaxK = 15360;
 
+int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
+    if (a.k % 32 || a.k > kGemvMaxK || a.n <= 0 || (mode == GEMV_SILU && a.n % 2)) return MXH_ERR_ARG;
+    if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.counter || !a.tokens || !a.pos)) return MXH_ERR_ARG;
+    switch (type) {
+    case MXH_Q4_K: return launch_gemv<Q4K, 2>(a, mode, st);
+    case MXH_Q5_K: return launch_gemv<Q5K, 2>(a, mode, st);
+    case MXH_Q8_0: return launch_gemv<Q80, 2>(a, mode, st);
+    case MXH_Q5_0: return launch_gemv<Q50, 2>(a, mode, st);
+    case MXH_F32: return launch_gemv<F32W, 2>(a, mode, st);
+    }
+    return MXH_ERR_UNSUPPORTED;
+}
+
 int gemv_launch(int type, const void* w, const float* x, float* y, const float* res, int64_t n, int64_t k, int form,
                 hipStream_t st) {
-    if (k % 32 || k > kGemvMaxK || n <= 0 || n > INT32_MAX) return MXH_ERR_ARG;
-    switch (type) {
-    case MXH_Q4_K: launch_gemv<Q4K, 2>(w, x, y, res, n, k, form, st); break;
-    case MXH_Q5_K: launch_gemv<Q5K, 2>(w, x, y, res, n, k, form, st); break;
-    case MXH_Q8_0: launch_gemv<Q80, 2>(w, x, y, res, n, k, form, st); break;
-    case MXH_Q5_0: launch_gemv<Q50, 2>(w, x, y, res, n, k, form, st); break;
-    case MXH_F32: launch_gemv<F32W, 2>(w, x, y, res, n, k, form, st); break;
-    default: return MXH_ERR_UNSUPPORTED;
-    }
-    return MXH_OK;
+    if (n <= 0 || n > INT32_MAX) return MXH_ERR_ARG;
+    GemvArgs a{};
+    a.w = (const uint8_t*)w;
+    a.x = x;
+    a.y = y;
+    a.res = res;
+    a.n = (int)n;
+    a.k = (int)k;
+    a.form = form;
+    return gemv_run(type, a, GEMV_PLAIN, st);
 }
 
 }  // namespace mxh

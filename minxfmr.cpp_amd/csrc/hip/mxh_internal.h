@@ -18,6 +18,27 @@ hipStream_t lib_stream();
 
 int gemv_launch(int type, const void* w, const float* x, float* y, const float* res, int64_t n, int64_t k, int form,
                 hipStream_t st);
+
+// Fused GEMV launch (see mxh_gemv.hip for the epilogues).
+enum { GEMV_PLAIN = 0, GEMV_SILU = 1, GEMV_ARGMAX = 2 };
+struct GemvArgs {
+    const uint8_t* w;
+    const float* x;
+    float* y;
+    const float* res;     // residual added to y (PLAIN); may alias y
+    const float* norm_w;  // when set, x is rmsnorm(x) * norm_w
+    float eps;
+    int n, k, form;
+    // ARGMAX: per-workgroup winners, completion counter (zero between
+    // launches), token array and device position
+    float* red_val;
+    int* red_idx;
+    int red_cap;
+    int* counter;
+    int* tokens;
+    int* pos;
+};
+int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st);
 int dequant_launch(int type, const void* w, float* out, int64_t rows, int64_t cols, int form, hipStream_t st);
 
 // small F32 vector ops (attention over host caches, F32 weights)
@@ -29,11 +50,25 @@ int matmul_f32_launch(const float* a, const float* b, float* out, int64_t m, int
 
 // decoder-step kernels (mxh_layer.hip)
 int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, hipStream_t st);
-int qkv_post_launch(float* qkv, const float* bias, const float* qn, const float* kn, const double* rope_cs,
-                    const int* pos, __half* kc, __half* vc, int nh, int nkv, int hd, float eps, int neox,
-                    int rope_half, hipStream_t st);
-int attention_launch(const float* q, const __half* kc, const __half* vc, const int* pos, float* part, float* out,
-                     int nh, int nkv, int hd, int n_ctx, hipStream_t st);
+// Fused decode attention: QK-norm, RoPE, fp16 KV append, split-K softmax*V
+// and the split merge (mxh_layer.hip).
+struct AttnArgs {
+    const float* qkv;     // [q | k | v] raw projections of the current token
+    const float* bias;    // [bq | bk | bv] or null
+    const float* q_norm;  // per-head rmsnorm weights or null
+    const float* k_norm;
+    const double* rope_cs;  // [n_ctx][hd/2][cos, sin]
+    const int* pos;       // current position (device)
+    __half* kc;           // this layer's K cache [n_ctx][nkv*hd]
+    __half* vc;
+    float* part;          // split partials
+    int* counter;         // per kv head, zero between launches
+    float* att;           // [nh*hd] output
+    int nh, nkv, hd, neox;
+    float eps, scale;
+};
+int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st);
+int attention_splits(int n_ctx);
 size_t attention_scratch_floats(int nh, int hd, int n_ctx);
 int silu_mul_launch(const float* gu, float* h, int n, hipStream_t st);
 int embed_launch(int type, const void* w, const int* tokens, const int* pos, float* x, int cols, int form,

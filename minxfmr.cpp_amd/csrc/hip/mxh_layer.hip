@@ -50,162 +50,223 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     }
 }
 
-// One wave per head.  Heads [0, nh) are q, [nh, nh+nkv) are k, [nh+nkv,
-// nh+2nkv) are v, all in the fused qkv buffer [q | k | v].  q and k get
-// optional bias, optional per-head rmsnorm (QK-norm), then RoPE at `pos`
-// from the double cos/sin table; k and v are written to the fp16 cache.
-__global__ void qkv_post_kernel(float* __restrict__ qkv, const float* __restrict__ bias, const float* __restrict__ qn,
-                                const float* __restrict__ kn, const double* __restrict__ rope_cs,
-                                const int* __restrict__ pos_p, __half* __restrict__ kc, __half* __restrict__ vc,
-                                int nh, int nkv, int hd, float eps, int neox, int rope_half) {
-    const int head = blockIdx.x;
-    const int lane = threadIdx.x;
-    const int pos = *pos_p;
-    const int kvd = nkv * hd;
-    float* v = qkv + (size_t)head * hd;  // head slices are contiguous in [q | k | v]
-    const bool is_q = head < nh, is_k = !is_q && head < nh + nkv;
-    if (bias)
-        for (int t = lane; t < hd; t += 64) v[t] += bias[(size_t)head * hd + t];
-    if (is_q || is_k) {
-        const float* nw = is_q ? qn : kn;
-        if (nw) {
-            double ss = 0.0;
-            for (int t = lane; t < hd; t += 64) ss += (double)v[t] * (double)v[t];
-            ss = wave_sum_d(ss);
-            const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
-            for (int t = lane; t < hd; t += 64) v[t] = (float)((double)v[t] * inv) * nw[t];
-        }
-        // RoPE: pair i rotates by pos * theta^(-2i/rot), cos/sin from the table
-        const double* cs = rope_cs + (size_t)pos * rope_half * 2;
-        for (int i = lane; i < rope_half; i += 64) {
-            const int a = neox ? i : 2 * i;
-            const int b = neox ? i + rope_half : 2 * i + 1;
-            const double c = cs[2 * i], s = cs[2 * i + 1];
-            const double x0 = v[a], x1 = v[b];
-            v[a] = (float)(x0 * c - x1 * s);
-            v[b] = (float)(x0 * s + x1 * c);
+constexpr int kAttnMaxGroup = 8;    // q heads per kv head
+constexpr int kAttnMaxPos = 512;    // positions one workgroup may cover
+
+// Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice held by a
+// wave; result written to dst (LDS or global), `src` is the raw projection.
+__device__ void head_prep(const float* __restrict__ src, const float* __restrict__ bias,
+                          const float* __restrict__ nw, const double* __restrict__ cs, float* dst, int hd, float eps,
+                          int neox) {
+    const int lane = threadIdx.x & 63;
+    float v[2] = {0.f, 0.f};  // hd <= 128: elements lane and lane + 64
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int t = lane + 64 * r;
+        if (t < hd) v[r] = src[t] + (bias ? bias[t] : 0.f);
+    }
+    if (nw) {
+        double ss = (double)v[0] * v[0] + (double)v[1] * v[1];
+        ss = wave_sum_d(ss);
+        const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int t = lane + 64 * r;
+            if (t < hd) v[r] = (float)((double)v[r] * inv) * nw[t];
         }
     }
-    if (!is_q) {
-        // round through fp16 into the cache; the current token is read back
-        // from the cache by attention like every earlier one
-        const int kvh = is_k ? head - nh : head - nh - nkv;
-        __half* dst = (is_k ? kc : vc) + (size_t)pos * kvd + (size_t)kvh * hd;
-        for (int t = lane; t < hd; t += 64) dst[t] = __float2half_rn(v[t]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int t = lane + 64 * r;
+        if (t < hd) dst[t] = v[r];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    // RoPE (rope.cpp:6-57): pair i = (2i, 2i+1), or (i, i + hd/2) for NeoX
+    const int half = hd / 2;
+    float a0 = 0.f, a1 = 0.f;
+    const int i = lane;
+    if (i < half) {
+        const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
+        const double c = cs[2 * i], s = cs[2 * i + 1];
+        const double x0 = dst[ia], x1 = dst[ib];
+        a0 = (float)(x0 * c - x1 * s);
+        a1 = (float)(x0 * s + x1 * c);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (i < half) {
+        dst[neox ? i : 2 * i] = a0;
+        dst[neox ? i + half : 2 * i + 1] = a1;
     }
 }
 
-constexpr int kAttnChunk = 256;   // positions per split
-constexpr int kAttnMaxGroup = 8;  // q heads per kv head handled by one workgroup
-
-// Split-K decode attention, partial pass.  Workgroup (kv head g, split s)
-// covers positions [s*C, min(L, s*C + C)) for the `group` q heads of g and
-// writes, per q head, the running max m, the sum l of exp(score - m) and the
-// unnormalised sum of exp(score - m) * V.
-__global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
-                                                           const __half* __restrict__ vc, const int* __restrict__ pos_p,
-                                                           float* __restrict__ part, int nh, int nkv, int hd,
-                                                           float scale, int max_splits) {
-    __shared__ float qs[kAttnMaxGroup * 256];
-    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
-    __shared__ float accs[2][kAttnMaxGroup][256];
-    const int g = blockIdx.x, s = blockIdx.y;
-    const int group = nh / nkv;
-    const int L = *pos_p + 1;
-    const int j0 = s * kAttnChunk;
-    const int jn = min(L - j0, kAttnChunk);
-    const int kvd = nkv * hd;
+// Decode attention for one kv head g and one split s of the L = pos+1
+// positions (transformer.cpp:529-629): q heads of the group are normed and
+// rotated in LDS; the split holding position pos also prepares k and v of
+// the current token and appends them (fp16) to the cache.  Each split writes
+// (max, sum of exp, unnormalised exp-weighted V) per q head; the last split
+// to finish merges the partials in split order into att.
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+    __shared__ float qs[kAttnMaxGroup * 128];
+    __shared__ float sc[kAttnMaxGroup][kAttnMaxPos];
+    __shared__ float kv_tmp[2][128];
+    __shared__ float vacc[4][kAttnMaxGroup][128];
+    __shared__ int last;
+    const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    const int hd = a.hd, group = a.nh / a.nkv, kvd = a.nkv * hd, qd = a.nh * hd;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (jn <= 0) {
-        // empty split: neutral partial
-        if (tid < group) {
-            float* p = part + ((size_t)(g * group + tid) * max_splits + s) * (hd + 2);
+    const int pos = *a.pos, L = pos + 1;
+    const int j0 = (int)(((long long)s * L) / S), j1 = (int)(((long long)(s + 1) * L) / S);
+    const int nj = j1 - j0;
+    const double* cs = a.rope_cs + (size_t)pos * hd;  // (hd/2) pairs of (cos, sin)
+    __half* kc = a.kc;
+    __half* vc = a.vc;
+
+    if (nj > 0) {
+        for (int h = wave; h < group; h += 4) {
+            const int qh = g * group + h;
+            head_prep(a.qkv + (size_t)qh * hd, a.bias ? a.bias + (size_t)qh * hd : nullptr, a.q_norm, cs,
+                      qs + h * hd, hd, a.eps, a.neox);
+        }
+        if (j1 == L) {
+            // this split owns the current position: k and v of kv head g
+            if (wave == 0)
+                head_prep(a.qkv + qd + (size_t)g * hd, a.bias ? a.bias + qd + (size_t)g * hd : nullptr, a.k_norm,
+                          cs, kv_tmp[0], hd, a.eps, a.neox);
+            if (wave == 1)
+                for (int t = lane; t < hd; t += 64)
+                    kv_tmp[1][t] = a.qkv[qd + kvd + (size_t)g * hd + t] +
+                                   (a.bias ? a.bias[qd + kvd + (size_t)g * hd + t] : 0.f);
+            __syncthreads();
+            for (int t = tid; t < 2 * hd; t += 256) {
+                const int which = t / hd, tt = t % hd;
+                (which ? vc : kc)[(size_t)pos * kvd + (size_t)g * hd + tt] = __float2half_rn(kv_tmp[which][tt]);
+            }
+        }
+        __syncthreads();
+
+        // scores: LPP lanes per position, 8 dims (one 16-byte load) each
+        const int lpp = hd / 8, ppw = 64 / lpp;
+        const int sub = lane % lpp, slot = lane / lpp;
+        float qreg[kAttnMaxGroup][8];
+#pragma unroll
+        for (int h = 0; h < kAttnMaxGroup; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qreg[h][e] = h < group ? qs[h * hd + sub * 8 + e] : 0.f;
+        for (int jb = wave * ppw; jb < nj; jb += 4 * ppw) {
+            const int jj = jb + slot;
+            float dot[kAttnMaxGroup];
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h) dot[h] = 0.f;
+            if (jj < nj) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(kc + (size_t)(j0 + jj) * kvd + (size_t)g * hd + sub * 8);
+                const __half2* hv = reinterpret_cast<const __half2*>(&raw);
+                float kf[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float2 f = __half22float2(hv[e]);
+                    kf[2 * e] = f.x;
+                    kf[2 * e + 1] = f.y;
+                }
+#pragma unroll
+                for (int h = 0; h < kAttnMaxGroup; ++h)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) dot[h] = fmaf(qreg[h][e], kf[e], dot[h]);
+            }
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h) {
+                if (h >= group) break;
+                float d = dot[h];
+                for (int off = 1; off < lpp; off <<= 1) d += __shfl_xor(d, off, 64);
+                if (sub == 0 && jj < nj) sc[h][jj] = d * a.scale;
+            }
+        }
+        __syncthreads();
+        // per-head max and exp (softmax.cpp:4-18 up to the final division)
+        for (int h = wave; h < group; h += 4) {
+            float m = -INFINITY;
+            for (int jj = lane; jj < nj; jj += 64) m = fmaxf(m, sc[h][jj]);
+            m = wave_max(m);
+            float l = 0.f;
+            for (int jj = lane; jj < nj; jj += 64) {
+                const float e = expf(sc[h][jj] - m);
+                sc[h][jj] = e;
+                l += e;
+            }
+            l = wave_sum(l);
+            if (lane == 0) {
+                float* p = a.part + ((size_t)(g * group + h) * S + s) * (hd + 2);
+                p[0] = m;
+                p[1] = l;
+            }
+        }
+        __syncthreads();
+        // exp-weighted V: thread = (dim pair, one of four position phases)
+        const int npair = hd / 2, phase = tid / npair, t2 = tid % npair;
+        if (phase < 4) {
+            float acc[kAttnMaxGroup][2];
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h) acc[h][0] = acc[h][1] = 0.f;
+            for (int jj = phase; jj < nj; jj += 4) {
+                const float2 v = __half22float2(
+                    *reinterpret_cast<const __half2*>(vc + (size_t)(j0 + jj) * kvd + (size_t)g * hd + 2 * t2));
+#pragma unroll
+                for (int h = 0; h < kAttnMaxGroup; ++h) {
+                    if (h >= group) break;
+                    const float pr = sc[h][jj];
+                    acc[h][0] = fmaf(pr, v.x, acc[h][0]);
+                    acc[h][1] = fmaf(pr, v.y, acc[h][1]);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h) {
+                if (h >= group) break;
+                vacc[phase][h][2 * t2] = acc[h][0];
+                vacc[phase][h][2 * t2 + 1] = acc[h][1];
+            }
+        }
+        __syncthreads();
+        const int nphase = min(4, 256 / npair);
+        for (int i = tid; i < group * hd; i += 256) {
+            const int h = i / hd, t = i % hd;
+            float v = 0.f;
+            for (int ph = 0; ph < nphase; ++ph) v += vacc[ph][h][t];
+            a.part[((size_t)(g * group + h) * S + s) * (hd + 2) + 2 + t] = v;
+        }
+    } else {
+        for (int h = tid; h < group; h += 256) {
+            float* p = a.part + ((size_t)(g * group + h) * S + s) * (hd + 2);
             p[0] = -INFINITY;
             p[1] = 0.f;
         }
-        return;
+        for (int i = tid; i < group * hd; i += 256)
+            a.part[((size_t)(g * group + i / hd) * S + s) * (hd + 2) + 2 + i % hd] = 0.f;
     }
-    for (int i = tid; i < group * hd; i += 256) qs[i] = q[(size_t)(g * group) * hd + i];
+    // last split of kv head g to finish merges the partials
+    __threadfence();
     __syncthreads();
-    // scores: one wave per position, lanes split the head dimension
-    for (int jj = wave; jj < jn; jj += 4) {
-        const __half* kr = kc + (size_t)(j0 + jj) * kvd + (size_t)g * hd;
-        float dot[kAttnMaxGroup];
-#pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) dot[h] = 0.f;
-        for (int t = lane; t < hd; t += 64) {
-            const float kv = __half2float(kr[t]);
-#pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h)
-                if (h < group) dot[h] = fmaf(qs[h * hd + t], kv, dot[h]);
-        }
-#pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h)
-            if (h < group) {
-                const float d = wave_sum(dot[h]);
-                if (lane == 0) sc[h][jj] = d * scale;
-            }
-    }
+    if (tid == 0) last = atomicAdd(a.counter + g, 1) == S - 1;
     __syncthreads();
-    // per-head max and exp
+    if (!last) return;
+    __threadfence();
     for (int h = wave; h < group; h += 4) {
-        float m = -INFINITY;
-        for (int jj = lane; jj < jn; jj += 64) m = fmaxf(m, sc[h][jj]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int jj = lane; jj < jn; jj += 64) {
-            const float e = expf(sc[h][jj] - m);
-            sc[h][jj] = e;
-            l += e;
+        const float* p = a.part + (size_t)(g * group + h) * S * (hd + 2);
+        float M = -INFINITY;
+        for (int i = 0; i < S; ++i) M = fmaxf(M, __builtin_nontemporal_load(p + (size_t)i * (hd + 2)));
+        float den = 0.f;
+        for (int i = 0; i < S; ++i)
+            den += expf(__builtin_nontemporal_load(p + (size_t)i * (hd + 2)) - M) *
+                   __builtin_nontemporal_load(p + (size_t)i * (hd + 2) + 1);
+        for (int t = lane; t < hd; t += 64) {
+            float num = 0.f;
+            for (int i = 0; i < S; ++i)
+                num += expf(__builtin_nontemporal_load(p + (size_t)i * (hd + 2)) - M) *
+                       __builtin_nontemporal_load(p + (size_t)i * (hd + 2) + 2 + t);
+            a.att[(size_t)(g * group + h) * hd + t] = num / den;
         }
-        l = wave_sum(l);
-        if (lane == 0) {
-            float* p = part + ((size_t)(g * group + h) * max_splits + s) * (hd + 2);
-            p[0] = m;
-            p[1] = l;
-        }
     }
-    __syncthreads();
-    // weighted V: threads [0, hd) take even positions, [hd, 2hd) odd ones
-    const int t = tid % hd, half = tid / hd;
-    if (half < 2 && tid < 2 * hd) {
-        float acc[kAttnMaxGroup];
-#pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) acc[h] = 0.f;
-        for (int jj = half; jj < jn; jj += 2) {
-            const float vv = __half2float(vc[(size_t)(j0 + jj) * kvd + (size_t)g * hd + t]);
-#pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h)
-                if (h < group) acc[h] = fmaf(sc[h][jj], vv, acc[h]);
-        }
-#pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h)
-            if (h < group) accs[half][h][t] = acc[h];
-    }
-    __syncthreads();
-    for (int i = tid; i < group * hd; i += 256) {
-        const int h = i / hd, tt = i % hd;
-        float* p = part + ((size_t)(g * group + h) * max_splits + s) * (hd + 2);
-        p[2 + tt] = accs[0][h][tt] + (2 * hd <= 256 ? accs[1][h][tt] : 0.f);
-    }
-}
-
-// Merge the splits of one q head: out = sum_s e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s.
-__global__ void attn_combine_kernel(const float* __restrict__ part, const int* __restrict__ pos_p,
-                                    float* __restrict__ out, int hd, int max_splits) {
-    const int h = blockIdx.x;
-    const int L = *pos_p + 1;
-    const int ns = (L + kAttnChunk - 1) / kAttnChunk;
-    const float* p = part + (size_t)h * max_splits * (hd + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, p[(size_t)s * (hd + 2)]);
-    float den = 0.f;
-    for (int s = 0; s < ns; ++s) den += expf(p[(size_t)s * (hd + 2)] - M) * p[(size_t)s * (hd + 2) + 1];
-    for (int t = threadIdx.x; t < hd; t += blockDim.x) {
-        float num = 0.f;
-        for (int s = 0; s < ns; ++s) num += expf(p[(size_t)s * (hd + 2)] - M) * p[(size_t)s * (hd + 2) + 2 + t];
-        out[(size_t)h * hd + t] = num / den;
-    }
+    if (tid == 0) a.counter[g] = 0;
 }
 
 // h[i] = silu(g[i]) * u[i], gu = [g | u]
@@ -288,31 +349,27 @@ __global__ void add_int_kernel(int* p, int v) {
 }  // namespace
 
 int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, hipStream_t st) {
+    if (n <= 0) return MXH_ERR_ARG;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, st, x, w, y, n, eps);
     return MXH_OK;
 }
 
-int qkv_post_launch(float* qkv, const float* bias, const float* qn, const float* kn, const double* rope_cs,
-                    const int* pos, __half* kc, __half* vc, int nh, int nkv, int hd, float eps, int neox,
-                    int rope_half, hipStream_t st) {
-    hipLaunchKernelGGL(qkv_post_kernel, dim3(nh + 2 * nkv), dim3(64), 0, st, qkv, bias, qn, kn, rope_cs, pos, kc, vc,
-                       nh, nkv, hd, eps, neox, rope_half);
-    return MXH_OK;
+int attention_splits(int n_ctx) {
+    int S = n_ctx / 64;
+    S = S < 8 ? 8 : (S > 64 ? 64 : S);
+    while ((n_ctx + S - 1) / S > kAttnMaxPos) ++S;
+    return S;
 }
 
-int attention_launch(const float* q, const __half* kc, const __half* vc, const int* pos, float* part, float* out,
-                     int nh, int nkv, int hd, int n_ctx, hipStream_t st) {
-    if (nh % nkv || nh / nkv > kAttnMaxGroup || hd > 128 || hd % 2) return MXH_ERR_UNSUPPORTED;
-    const int max_splits = (n_ctx + kAttnChunk - 1) / kAttnChunk;
-    const float scale = 1.0f / sqrtf((float)hd);
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(nkv, max_splits), dim3(256), 0, st, q, kc, vc, pos, part, nh, nkv, hd,
-                       scale, max_splits);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(nh), dim3(128), 0, st, part, pos, out, hd, max_splits);
+int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
+    if (a.nh % a.nkv || a.nh / a.nkv > kAttnMaxGroup || a.hd > 128 || a.hd % 8 || a.hd < 16) return MXH_ERR_UNSUPPORTED;
+    const int S = attention_splits(n_ctx);
+    hipLaunchKernelGGL(attention_kernel, dim3(a.nkv, S), dim3(256), 0, st, a);
     return MXH_OK;
 }
 
 size_t attention_scratch_floats(int nh, int hd, int n_ctx) {
-    return (size_t)nh * ((n_ctx + kAttnChunk - 1) / kAttnChunk) * (hd + 2);
+    return (size_t)nh * attention_splits(n_ctx) * (hd + 2);
 }
 
 int silu_mul_launch(const float* gu, float* h, int n, hipStream_t st) {

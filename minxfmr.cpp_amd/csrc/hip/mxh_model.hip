@@ -56,7 +56,10 @@ struct mxh_model {
     __half* kv = nullptr;
     double* rope_cs = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *h = nullptr, *logits = nullptr,
-          *part = nullptr, *trace = nullptr;
+          *part = nullptr, *trace = nullptr, *red_val = nullptr;
+    int* red_idx = nullptr;
+    int red_cap = 0;
+    int* counters = nullptr;  // [0]: lm-head argmax, [1 ..]: attention per kv head
     int* tokens = nullptr;  // [n_ctx + 1]: prompt then generated ids
     int* pos = nullptr;     // current position
     int host_pos = 0;
@@ -66,12 +69,32 @@ struct mxh_model {
 
 namespace {
 
-int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hipStream_t st) {
-    return gemv_launch(w.type, w.p, x, y, res, w.rows, w.cols, form, st);
+int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hipStream_t st,
+         const float* norm_w = nullptr, float eps = 0.f, int mode = GEMV_PLAIN, mxh_model* m = nullptr) {
+    GemvArgs a{};
+    a.w = (const uint8_t*)w.p;
+    a.x = x;
+    a.y = y;
+    a.res = res;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.n = (int)w.rows;
+    a.k = (int)w.cols;
+    a.form = form;
+    if (mode == GEMV_ARGMAX) {
+        a.red_val = m->red_val;
+        a.red_idx = m->red_idx;
+        a.red_cap = m->red_cap;
+        a.counter = m->counters;
+        a.tokens = m->tokens;
+        a.pos = m->pos;
+    }
+    return gemv_run(w.type, a, mode, st);
 }
 
-// Enqueue one token step at the device position.  with_head: run the final
-// norm, lm-head and argmax (writing tokens[pos+1]); without: prompt step.
+// Enqueue one token step at the device position.  with_head: the final
+// norm, lm-head and argmax (writing tokens[pos+1]) and the position advance
+// are fused into the head GEMV; without: a prompt step.
 int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
     const mxh_model_config& c = m->cfg;
     const int d = c.n_embd, hd = c.head_dim, nh = c.n_head, nkv = c.n_head_kv;
@@ -81,38 +104,51 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
     rc |= embed_launch(m->embd.type, m->embd.p, m->tokens, m->pos, m->x, d, m->form, st);
     for (int l = 0; l < c.n_layer; ++l) {
         const Layer& L = m->layers[(size_t)l];
-        rc |= rmsnorm_launch(m->x, L.attn_norm, m->xn, d, c.eps, st);
+        // attention rmsnorm is fused into the projection GEMVs
         if (L.qkv_fused) {
-            rc |= gemv(L.qkv, m->xn, m->qkv, nullptr, m->form, st);
+            rc |= gemv(L.qkv, m->x, m->qkv, nullptr, m->form, st, L.attn_norm, c.eps);
         } else {
-            rc |= gemv(L.q, m->xn, m->qkv, nullptr, m->form, st);
-            rc |= gemv(L.k, m->xn, m->qkv + qd, nullptr, m->form, st);
-            rc |= gemv(L.v, m->xn, m->qkv + qd + kvd, nullptr, m->form, st);
+            rc |= gemv(L.q, m->x, m->qkv, nullptr, m->form, st, L.attn_norm, c.eps);
+            rc |= gemv(L.k, m->x, m->qkv + qd, nullptr, m->form, st, L.attn_norm, c.eps);
+            rc |= gemv(L.v, m->x, m->qkv + qd + kvd, nullptr, m->form, st, L.attn_norm, c.eps);
         }
-        rc |= qkv_post_launch(m->qkv, L.bias, L.q_norm, L.k_norm, m->rope_cs, m->pos, L.kc, L.vc, nh, nkv, hd, c.eps,
-                              m->neox, hd / 2, st);
-        rc |= attention_launch(m->qkv, L.kc, L.vc, m->pos, m->part, m->att, nh, nkv, hd, c.n_ctx, st);
+        AttnArgs aa{};
+        aa.qkv = m->qkv;
+        aa.bias = L.bias;
+        aa.q_norm = L.q_norm;
+        aa.k_norm = L.k_norm;
+        aa.rope_cs = m->rope_cs;
+        aa.pos = m->pos;
+        aa.kc = L.kc;
+        aa.vc = L.vc;
+        aa.part = m->part;
+        aa.counter = m->counters + 1;
+        aa.att = m->att;
+        aa.nh = nh;
+        aa.nkv = nkv;
+        aa.hd = hd;
+        aa.neox = m->neox;
+        aa.eps = c.eps;
+        aa.scale = 1.0f / sqrtf((float)hd);
+        rc |= attention_run(aa, c.n_ctx, st);
         rc |= gemv(L.o, m->att, m->x, m->x, m->form, st);
-        rc |= rmsnorm_launch(m->x, L.ffn_norm, m->xn, d, c.eps, st);
         if (L.gu_fused) {
-            rc |= gemv(L.gu, m->xn, m->gu, nullptr, m->form, st);
+            rc |= gemv(L.gu, m->x, m->h, nullptr, m->form, st, L.ffn_norm, c.eps, GEMV_SILU);
         } else {
-            rc |= gemv(L.g, m->xn, m->gu, nullptr, m->form, st);
-            rc |= gemv(L.u, m->xn, m->gu + c.n_ff, nullptr, m->form, st);
+            rc |= gemv(L.g, m->x, m->gu, nullptr, m->form, st, L.ffn_norm, c.eps);
+            rc |= gemv(L.u, m->x, m->gu + c.n_ff, nullptr, m->form, st, L.ffn_norm, c.eps);
+            rc |= silu_mul_launch(m->gu, m->h, c.n_ff, st);
         }
-        rc |= silu_mul_launch(m->gu, m->h, c.n_ff, st);
         rc |= gemv(L.down, m->h, m->x, m->x, m->form, st);
         if (m->trace_on) rc |= check_hip(hipMemcpyAsync(m->trace + (size_t)l * d, m->x, sizeof(float) * d,
                                                         hipMemcpyDeviceToDevice, st), "trace copy");
     }
     if (with_head) {
-        rc |= rmsnorm_launch(m->x, m->out_norm, m->xn, d, c.eps, st);
-        if (m->trace_on) rc |= check_hip(hipMemcpyAsync(m->trace + (size_t)c.n_layer * d, m->xn, sizeof(float) * d,
-                                                        hipMemcpyDeviceToDevice, st), "trace copy");
-        rc |= gemv(m->out, m->xn, m->logits, nullptr, m->form, st);
-        rc |= argmax_launch(m->logits, (int)m->out.rows, m->tokens, m->pos, st);
+        if (m->trace_on) rc |= rmsnorm_launch(m->x, m->out_norm, m->trace + (size_t)c.n_layer * d, d, c.eps, st);
+        rc |= gemv(m->out, m->x, m->logits, nullptr, m->form, st, m->out_norm, c.eps, GEMV_ARGMAX, m);
+    } else {
+        rc |= add_int_launch(m->pos, 1, st);
     }
-    rc |= add_int_launch(m->pos, 1, st);
     return rc ? set_error(MXH_ERR_HIP, "step enqueue failed") : MXH_OK;
 }
 
@@ -146,7 +182,7 @@ int free_model(mxh_model* m) {
     if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
-                    m->trace, m->tokens, m->pos};
+                    m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -387,6 +423,11 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     if (!rc) rc = dalloc(&m->trace, (size_t)(c.n_layer + 1) * c.n_embd);
     if (!rc) rc = dalloc(&m->tokens, (size_t)n_ctx + 1);
     if (!rc) rc = dalloc(&m->pos, 1);
+    m->red_cap = (c.n_vocab + 7) / 8 + 1;  // workgroups of the head GEMV (8 rows each)
+    if (!rc) rc = dalloc(&m->red_val, (size_t)m->red_cap);
+    if (!rc) rc = dalloc(&m->red_idx, (size_t)m->red_cap);
+    if (!rc) rc = dalloc(&m->counters, (size_t)c.n_head_kv + 1);
+    if (!rc) rc = check_hip(hipMemset(m->counters, 0, sizeof(int) * ((size_t)c.n_head_kv + 1)), "counter init");
     if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * ((size_t)n_ctx + 1)), "token init");
     if (!rc) rc = check_hip(hipMemset(m->pos, 0, sizeof(int)), "position init");
     if (!rc) rc = check_hip(hipDeviceSynchronize(), "model init");
