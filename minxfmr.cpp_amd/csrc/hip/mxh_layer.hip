@@ -52,6 +52,7 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
 
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
 constexpr int kAttnMaxPos = 512;    // positions one workgroup may cover
+constexpr int kAttnMaxSplits = 64;  // splits per kv head (one lane each in the merge)
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice held by a
 // wave; result written to dst (LDS or global), `src` is the raw projection.
@@ -250,19 +251,23 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     __syncthreads();
     if (!last) return;
     __threadfence();
+    // merge: lane i holds split i's (max, sum); weights e^(m_i - M) go through
+    // LDS so every lane can scale its dims of the partial sums
     for (int h = wave; h < group; h += 4) {
         const float* p = a.part + (size_t)(g * group + h) * S * (hd + 2);
-        float M = -INFINITY;
-        for (int i = 0; i < S; ++i) M = fmaxf(M, __builtin_nontemporal_load(p + (size_t)i * (hd + 2)));
-        float den = 0.f;
-        for (int i = 0; i < S; ++i)
-            den += expf(__builtin_nontemporal_load(p + (size_t)i * (hd + 2)) - M) *
-                   __builtin_nontemporal_load(p + (size_t)i * (hd + 2) + 1);
+        const float mi = lane < S ? __builtin_nontemporal_load(p + (size_t)lane * (hd + 2)) : -INFINITY;
+        const float li = lane < S ? __builtin_nontemporal_load(p + (size_t)lane * (hd + 2) + 1) : 0.f;
+        const float M = wave_max(mi);
+        const float wi = lane < S ? expf(mi - M) : 0.f;
+        const float den = wave_sum(wi * li);
+        sc[h][lane] = wi;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         for (int t = lane; t < hd; t += 64) {
             float num = 0.f;
+#pragma unroll 8
             for (int i = 0; i < S; ++i)
-                num += expf(__builtin_nontemporal_load(p + (size_t)i * (hd + 2)) - M) *
-                       __builtin_nontemporal_load(p + (size_t)i * (hd + 2) + 2 + t);
+                num = fmaf(sc[h][i], __builtin_nontemporal_load(p + (size_t)i * (hd + 2) + 2 + t), num);
             a.att[(size_t)(g * group + h) * hd + t] = num / den;
         }
     }
@@ -364,6 +369,7 @@ int attention_splits(int n_ctx) {
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (a.nh % a.nkv || a.nh / a.nkv > kAttnMaxGroup || a.hd > 128 || a.hd % 8 || a.hd < 16) return MXH_ERR_UNSUPPORTED;
     const int S = attention_splits(n_ctx);
+    if (S > kAttnMaxSplits) return MXH_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(attention_kernel, dim3(a.nkv, S), dim3(256), 0, st, a);
     return MXH_OK;
 }
