@@ -8,16 +8,24 @@
 // 16 qs bytes covering half of two sub-blocks; Q5_K: the same plus their 16
 // qh bytes; Q8_0/Q5_0: one block; F32: 128 bytes).  Lane l of a wave64 owns
 // chunks l, l+64, ... of every row, so one x slice serves all R rows the
-// wave handles at a time.  x sits in LDS, staged once per workgroup (padded
-// so the 64-byte x runs read together land in distinct banks); workgroups
-// are persistent over row groups so that staging, and the optional fused
-// rmsnorm, are paid once per workgroup rather than once per few rows.  Each
-// wave walks its (row group, chunk) sequence with the next step's weight
-// loads issued before the current step's arithmetic (register double
-// buffer), so 128-bit loads of raw block bytes stay in flight while decoding
-// happens in registers.  Per sub-block the inner product is factored as
-//   sum_i x_i (d*sc*q_i - dmin*m) = d*sc * sum_i x_i q_i - dmin*m * sum_i x_i.
-// A row's 64 lane partials are reduced with cross-lane shuffles.
+// wave handles at a time.  x is staged in LDS once per workgroup;
+// workgroups are persistent over row groups so that staging, and the
+// optional fused rmsnorm, are paid once per workgroup rather than once per
+// few rows.  Each wave walks its (row group, chunk) sequence with the next
+// step's weight loads issued before the current step's arithmetic (register
+// double buffer), so 128-bit loads of raw block bytes stay in flight while
+// decoding happens in registers.  A row's 64 lane partials are reduced with
+// cross-lane shuffles.
+//
+// Integer inner products.  For the quantized formats x is staged as 16-bit
+// block fixed point: per 32-element sub-block j, X_i = rint(x_i / s_j) with
+// s_j = max|x| / 32512, split into two signed bytes X = 256*hi + lo.  The
+// codes q are small integers, so sum_i X_i q_i is exact in int32 and costs
+// two v_dot4_i32_i8 per four elements (no per-element conversion).  With
+//   sum_i x_i (d*sc*q_i - dmin*m) = d*sc*s_j * sum_i X_i q_i - dmin*m * s_j * sum_i X_i
+// the only approximation is x's 16-bit rounding (relative 2^-16 of the
+// sub-block maximum); the weights are used exactly.
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include "mxh_device.h"
@@ -88,13 +96,77 @@ __device__ __forceinline__ void load_block_2aligned(const uint8_t* base, size_t 
     bd[n] = ub;
 }
 
-// ---- per-type chunk load / compute ---------------------------------------
+// ---- staged x in LDS ------------------------------------------------------
+// Quantized formats: lo/hi limb bytes (K each), per-32 scales (K/32) and
+// per-16 scaled sums s_j * sum X_i (K/16).
+struct XQ {
+    const uint32_t* lo;
+    const uint32_t* hi;
+    const float* scale;
+    const float* sum16;
+};
+
+__device__ __forceinline__ XQ xq_view(const float* smem, int k) {
+    const uint32_t* lo = reinterpret_cast<const uint32_t*>(smem);
+    return XQ{lo, lo + k / 4, reinterpret_cast<const float*>(lo + k / 2),
+              reinterpret_cast<const float*>(lo + k / 2) + k / 32};
+}
+
+__device__ __forceinline__ uint4 lds16(const uint32_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// sum over 16 elements of X_i q_i given the four dwords of lo/hi limbs and q bytes
+__device__ __forceinline__ float dot16(uint4 xl, uint4 xh, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3) {
+    int l = sdot4(xl.x, q0, 0);
+    l = sdot4(xl.y, q1, l);
+    l = sdot4(xl.z, q2, l);
+    l = sdot4(xl.w, q3, l);
+    int h = sdot4(xh.x, q0, 0);
+    h = sdot4(xh.y, q1, h);
+    h = sdot4(xh.z, q2, h);
+    h = sdot4(xh.w, q3, h);
+    return (float)(h * 256 + l);  // |result| < 2^24: exact
+}
+
+// 6-bit (scale, min) of sub-blocks 2g and 2g+1 as byte pairs, without
+// branches (tensor.cpp:395-403 reference form; ggml form for form != 0)
+__device__ __forceinline__ void k4_pair(uint32_t s0, uint32_t s1, uint32_t s2, int g, int form, uint32_t& sc,
+                                        uint32_t& mn) {
+    const int sh = (g & 1) * 16;
+    const uint32_t A = s0 >> sh, B = s1 >> sh, C = s2 >> sh;
+    if (g >= 2) {
+        sc = (C & 0x0f0fu) | (((form ? A : B) >> 2) & 0x3030u);
+        mn = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    } else {
+        sc = A & 0x3f3fu;
+        mn = B & 0x3f3fu;
+    }
+}
+
+__device__ __forceinline__ float2 h2f2(uint32_t v) {
+    __half2 h;
+    __builtin_memcpy(&h, &v, 4);
+    return __half22float2(h);
+}
+
+__device__ __forceinline__ float h2f(uint32_t v) {
+    __half h;
+    const uint16_t b = (uint16_t)v;
+    __builtin_memcpy(&h, &b, 2);
+    return __half2float(h);
+}
+
+// ---- per-type chunk load / compute -----------------------------------------
 // load(): raw bytes of chunk c of R rows into a register buffer.
 // compute(): add the chunk's contribution to acc[r].
 
 template <int R>
 struct Q4K {
     static constexpr int kType = MXH_Q4_K;
+    static constexpr bool kIntX = true;
     struct Buf {
         uint4 hd[R], qs[R];
     };
@@ -107,36 +179,27 @@ struct Q4K {
             b.qs[r] = ldg16(bp + 16 + 16 * p);
         }
     }
-    static __device__ __forceinline__ void compute(const Buf& b, int c, const float* xs, int form, float (&acc)[R]) {
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int form, float (&acc)[R]) {
         const int blk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
-        const int e0 = 256 * blk + 64 * g + 16 * h;
-        const float4 xl0 = lds4(xs, e0), xl1 = lds4(xs, e0 + 4), xl2 = lds4(xs, e0 + 8), xl3 = lds4(xs, e0 + 12);
-        const float4 xh0 = lds4(xs, e0 + 32), xh1 = lds4(xs, e0 + 36), xh2 = lds4(xs, e0 + 40),
-                     xh3 = lds4(xs, e0 + 44);
-        const float sl = (sum4(xl0) + sum4(xl1)) + (sum4(xl2) + sum4(xl3));
-        const float sh = (sum4(xh0) + sum4(xh1)) + (sum4(xh2) + sum4(xh3));
+        const int e0 = 256 * blk + 64 * g + 16 * h;  // low-nibble elements e0..e0+15 (sub-block 2g)
+        const uint4 xla = lds16(x.lo + e0 / 4), xha = lds16(x.hi + e0 / 4);
+        const uint4 xlb = lds16(x.lo + e0 / 4 + 8), xhb = lds16(x.hi + e0 / 4 + 8);
+        const float sa = x.scale[e0 >> 5], sb = x.scale[(e0 >> 5) + 1];
+        const float ta = x.sum16[e0 >> 4], tb = x.sum16[(e0 >> 4) + 2];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float d = half_bits_to_float(b.hd[r].x & 0xffffu);
-            const float dm = half_bits_to_float(b.hd[r].x >> 16);
-            uint32_t sa, ma, sb, mb;
-            k4_scale_min(b.hd[r].y, b.hd[r].z, b.hd[r].w, 2 * g, form, sa, ma);
-            k4_scale_min(b.hd[r].y, b.hd[r].z, b.hd[r].w, 2 * g + 1, form, sb, mb);
+            const float2 dd = h2f2(b.hd[r].x);  // d, dmin
+            uint32_t scp, mnp;
+            k4_pair(b.hd[r].y, b.hd[r].z, b.hd[r].w, g, form, scp, mnp);
             const uint32_t q0 = b.qs[r].x, q1 = b.qs[r].y, q2 = b.qs[r].z, q3 = b.qs[r].w;
-            float dl = 0.f, dh = 0.f;
-            dl = dot4_ubyte(xl0, q0 & 0x0f0f0f0fu, dl);
-            dl = dot4_ubyte(xl1, q1 & 0x0f0f0f0fu, dl);
-            dl = dot4_ubyte(xl2, q2 & 0x0f0f0f0fu, dl);
-            dl = dot4_ubyte(xl3, q3 & 0x0f0f0f0fu, dl);
-            dh = dot4_ubyte(xh0, (q0 >> 4) & 0x0f0f0f0fu, dh);
-            dh = dot4_ubyte(xh1, (q1 >> 4) & 0x0f0f0f0fu, dh);
-            dh = dot4_ubyte(xh2, (q2 >> 4) & 0x0f0f0f0fu, dh);
-            dh = dot4_ubyte(xh3, (q3 >> 4) & 0x0f0f0f0fu, dh);
+            const float da = dot16(xla, xha, q0 & 0x0f0f0f0fu, q1 & 0x0f0f0f0fu, q2 & 0x0f0f0f0fu, q3 & 0x0f0f0f0fu);
+            const float db = dot16(xlb, xhb, (q0 >> 4) & 0x0f0f0f0fu, (q1 >> 4) & 0x0f0f0f0fu,
+                                   (q2 >> 4) & 0x0f0f0f0fu, (q3 >> 4) & 0x0f0f0f0fu);
             float a = acc[r];
-            a = fmaf(d * (float)sa, dl, a);
-            a = fmaf(-(dm * (float)ma), sl, a);
-            a = fmaf(d * (float)sb, dh, a);
-            a = fmaf(-(dm * (float)mb), sh, a);
+            a = fmaf(dd.x * (float)(scp & 0xffu) * sa, da, a);
+            a = fmaf(-(dd.y * (float)(mnp & 0xffu)), ta, a);
+            a = fmaf(dd.x * (float)((scp >> 8) & 0xffu) * sb, db, a);
+            a = fmaf(-(dd.y * (float)((mnp >> 8) & 0xffu)), tb, a);
             acc[r] = a;
         }
     }
@@ -145,6 +208,7 @@ struct Q4K {
 template <int R>
 struct Q5K {
     static constexpr int kType = MXH_Q5_K;
+    static constexpr bool kIntX = true;
     struct Buf {
         uint4 hd[R], qh[R], qs[R];
     };
@@ -158,35 +222,33 @@ struct Q5K {
             b.qs[r] = ldg16(bp + 48 + 16 * p);
         }
     }
-    static __device__ __forceinline__ void compute(const Buf& b, int c, const float* xs, int form, float (&acc)[R]) {
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int form, float (&acc)[R]) {
         const int blk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
         const int e0 = 256 * blk + 64 * g + 16 * h;
-        const float4 xl[4] = {lds4(xs, e0), lds4(xs, e0 + 4), lds4(xs, e0 + 8), lds4(xs, e0 + 12)};
-        const float4 xh[4] = {lds4(xs, e0 + 32), lds4(xs, e0 + 36), lds4(xs, e0 + 40), lds4(xs, e0 + 44)};
-        const float sl = (sum4(xl[0]) + sum4(xl[1])) + (sum4(xl[2]) + sum4(xl[3]));
-        const float sh = (sum4(xh[0]) + sum4(xh[1])) + (sum4(xh[2]) + sum4(xh[3]));
+        const uint4 xla = lds16(x.lo + e0 / 4), xha = lds16(x.hi + e0 / 4);
+        const uint4 xlb = lds16(x.lo + e0 / 4 + 8), xhb = lds16(x.hi + e0 / 4 + 8);
+        const float sa = x.scale[e0 >> 5], sb = x.scale[(e0 >> 5) + 1];
+        const float ta = x.sum16[e0 >> 4], tb = x.sum16[(e0 >> 4) + 2];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float d = half_bits_to_float(b.hd[r].x & 0xffffu);
-            const float dm = half_bits_to_float(b.hd[r].x >> 16);
-            uint32_t sa, ma, sb, mb;
-            k4_scale_min(b.hd[r].y, b.hd[r].z, b.hd[r].w, 2 * g, form, sa, ma);
-            k4_scale_min(b.hd[r].y, b.hd[r].z, b.hd[r].w, 2 * g + 1, form, sb, mb);
+            const float2 dd = h2f2(b.hd[r].x);
+            uint32_t scp, mnp;
+            k4_pair(b.hd[r].y, b.hd[r].z, b.hd[r].w, g, form, scp, mnp);
             const uint32_t q[4] = {b.qs[r].x, b.qs[r].y, b.qs[r].z, b.qs[r].w};
             const uint32_t hb[4] = {b.qh[r].x, b.qh[r].y, b.qh[r].z, b.qh[r].w};
-            float dl = 0.f, dh = 0.f;
+            uint32_t lo[4], hi[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t lo = (q[i] & 0x0f0f0f0fu) | (((hb[i] >> (2 * g)) & 0x01010101u) << 4);
-                const uint32_t hi = ((q[i] >> 4) & 0x0f0f0f0fu) | (((hb[i] >> (2 * g + 1)) & 0x01010101u) << 4);
-                dl = dot4_ubyte(xl[i], lo, dl);
-                dh = dot4_ubyte(xh[i], hi, dh);
+                lo[i] = (q[i] & 0x0f0f0f0fu) | (((hb[i] >> (2 * g)) & 0x01010101u) << 4);
+                hi[i] = ((q[i] >> 4) & 0x0f0f0f0fu) | (((hb[i] >> (2 * g + 1)) & 0x01010101u) << 4);
             }
+            const float da = dot16(xla, xha, lo[0], lo[1], lo[2], lo[3]);
+            const float db = dot16(xlb, xhb, hi[0], hi[1], hi[2], hi[3]);
             float a = acc[r];
-            a = fmaf(d * (float)sa, dl, a);
-            a = fmaf(-(dm * (float)ma), sl, a);
-            a = fmaf(d * (float)sb, dh, a);
-            a = fmaf(-(dm * (float)mb), sh, a);
+            a = fmaf(dd.x * (float)(scp & 0xffu) * sa, da, a);
+            a = fmaf(-(dd.y * (float)(mnp & 0xffu)), ta, a);
+            a = fmaf(dd.x * (float)((scp >> 8) & 0xffu) * sb, db, a);
+            a = fmaf(-(dd.y * (float)((mnp >> 8) & 0xffu)), tb, a);
             acc[r] = a;
         }
     }
@@ -195,6 +257,7 @@ struct Q5K {
 template <int R>
 struct Q80 {
     static constexpr int kType = MXH_Q8_0;
+    static constexpr bool kIntX = true;
     struct Buf {
         uint32_t bd[R][9];
     };
@@ -202,19 +265,20 @@ struct Q80 {
 #pragma unroll
         for (int r = 0; r < R; ++r) load_block_2aligned<34>(w, (size_t)rows[r] * rb + (size_t)c * 34, b.bd[r]);
     }
-    static __device__ __forceinline__ void compute(const Buf& b, int c, const float* xs, int, float (&acc)[R]) {
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        float4 x[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = lds4(xs, e0 + 4 * i);
+        const uint4 xl0 = lds16(x.lo + e0 / 4), xh0 = lds16(x.hi + e0 / 4);
+        const uint4 xl1 = lds16(x.lo + e0 / 4 + 4), xh1 = lds16(x.hi + e0 / 4 + 4);
+        const float s = x.scale[c];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            // block bytes: d = bytes 0-1, q = bytes 2..33
-            const float d = half_bits_to_float(b.bd[r][0] & 0xffffu);
-            float s = 0.f;
+            // block bytes: d = bytes 0-1, q = bytes 2..33 (signed)
+            const float d = h2f(b.bd[r][0]);
+            uint32_t q[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s = dot4_sbyte(x[i], (b.bd[r][i] >> 16) | (b.bd[r][i + 1] << 16), s);
-            acc[r] = fmaf(d, s, acc[r]);
+            for (int i = 0; i < 8; ++i) q[i] = (b.bd[r][i] >> 16) | (b.bd[r][i + 1] << 16);
+            const float v = dot16(xl0, xh0, q[0], q[1], q[2], q[3]) + dot16(xl1, xh1, q[4], q[5], q[6], q[7]);
+            acc[r] = fmaf(d * s, v, acc[r]);
         }
     }
 };
@@ -222,6 +286,7 @@ struct Q80 {
 template <int R>
 struct Q50 {
     static constexpr int kType = MXH_Q5_0;
+    static constexpr bool kIntX = true;
     struct Buf {
         uint32_t bd[R][6];
     };
@@ -229,30 +294,30 @@ struct Q50 {
 #pragma unroll
         for (int r = 0; r < R; ++r) load_block_2aligned<22>(w, (size_t)rows[r] * rb + (size_t)c * 22, b.bd[r]);
     }
-    static __device__ __forceinline__ void compute(const Buf& b, int c, const float* xs, int, float (&acc)[R]) {
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        float4 x[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = lds4(xs, e0 + 4 * i);
-        const float sx = ((sum4(x[0]) + sum4(x[1])) + (sum4(x[2]) + sum4(x[3]))) +
-                         ((sum4(x[4]) + sum4(x[5])) + (sum4(x[6]) + sum4(x[7])));
+        const uint4 xl0 = lds16(x.lo + e0 / 4), xh0 = lds16(x.hi + e0 / 4);
+        const uint4 xl1 = lds16(x.lo + e0 / 4 + 4), xh1 = lds16(x.hi + e0 / 4 + 4);
+        const float s = x.scale[c];
+        const float t = x.sum16[2 * c] + x.sum16[2 * c + 1];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            // bytes: d 0-1, qh 2-5, qs 6-21
-            const float d = half_bits_to_float(b.bd[r][0] & 0xffffu);
+            // bytes: d 0-1, qh 2-5, qs 6-21; code q = nibble | bit << 4, value d*(q-16)
+            const float d = h2f(b.bd[r][0]);
             const uint32_t qh = (b.bd[r][0] >> 16) | (b.bd[r][1] << 16);
-            float s = 0.f;
+            uint32_t lo[4], hi[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t qd = (b.bd[r][1 + i] >> 16) | (b.bd[r][2 + i] << 16);  // qs bytes 4i..4i+3
                 const uint32_t hlo = (qh >> (4 * i)) & 15u, hhi = (qh >> (16 + 4 * i)) & 15u;
                 const uint32_t spread_lo = (hlo & 1u) | ((hlo & 2u) << 7) | ((hlo & 4u) << 14) | ((hlo & 8u) << 21);
                 const uint32_t spread_hi = (hhi & 1u) | ((hhi & 2u) << 7) | ((hhi & 4u) << 14) | ((hhi & 8u) << 21);
-                s = dot4_ubyte(x[i], (qd & 0x0f0f0f0fu) | (spread_lo << 4), s);
-                s = dot4_ubyte(x[4 + i], ((qd >> 4) & 0x0f0f0f0fu) | (spread_hi << 4), s);
+                lo[i] = (qd & 0x0f0f0f0fu) | (spread_lo << 4);
+                hi[i] = ((qd >> 4) & 0x0f0f0f0fu) | (spread_hi << 4);
             }
-            // d * (q - 16) summed: d * (sum x q - 16 sum x)
-            acc[r] = fmaf(d, fmaf(-16.f, sx, s), acc[r]);
+            // elements 0..15 are the low nibbles, 16..31 the high nibbles
+            const float v = dot16(xl0, xh0, lo[0], lo[1], lo[2], lo[3]) + dot16(xl1, xh1, hi[0], hi[1], hi[2], hi[3]);
+            acc[r] = fmaf(d, fmaf(s, v, -16.f * t), acc[r]);
         }
     }
 };
@@ -260,6 +325,7 @@ struct Q50 {
 template <int R>
 struct F32W {
     static constexpr int kType = MXH_F32;
+    static constexpr bool kIntX = false;
     struct Buf {
         f32x4 v[R][8];
     };
@@ -323,6 +389,69 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
     __syncthreads();
 }
 
+// Stage x as 16-bit block fixed point (see the file comment).  Each thread
+// handles 4 consecutive elements; the 8 threads of a 32-element sub-block
+// share its maximum through shuffles.  With a norm weight x is first
+// replaced by the reference rmsnorm, as in stage_x.
+__device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
+                                         int k, float eps, double* red) {
+    uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
+    uint32_t* hi = lo + k / 4;
+    float* scale = reinterpret_cast<float*>(lo + k / 2);
+    float* sum16 = scale + k / 32;
+    double inv = 1.0;
+    if (nw) {
+        double ss = 0.0;
+        for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(x + e);
+            ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        inv = 1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps);
+    }
+    for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
+        float4 v = *reinterpret_cast<const float4*>(x + e);
+        if (nw) {
+            const float4 g = *reinterpret_cast<const float4*>(nw + e);
+            v.x = (float)((double)v.x * inv) * g.x;
+            v.y = (float)((double)v.y * inv) * g.y;
+            v.z = (float)((double)v.z * inv) * g.z;
+            v.w = (float)((double)v.w * inv) * g.w;
+        }
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite)
+        const bool live = m > 1e-30f;
+        const float sc = live ? m / 32512.0f : 0.f;
+        const float is = live ? 32512.0f / m : 0.f;
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t plo = 0, phi = 0;
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int X = (int)rintf(vv[i] * is);
+            X = X > 32512 ? 32512 : (X < -32512 ? -32512 : X);
+            const int l = ((X + 128) & 255) - 128;
+            const int h = (X - l) >> 8;
+            plo |= (uint32_t)(l & 255) << (8 * i);
+            phi |= (uint32_t)(h & 255) << (8 * i);
+            sum += X;
+        }
+        lo[e >> 2] = plo;
+        hi[e >> 2] = phi;
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * (float)sum;
+        if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
+    }
+    __syncthreads();
+}
+
 // Output modes (epilogues) of one GEMV launch.
 //  GEMV_PLAIN : y[r] = W[r].x (+ res[r])
 //  GEMV_SILU  : W = [gate; up] with n = 2F rows; y[i] = silu(gate_i) * up_i
@@ -337,7 +466,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __shared__ double red[kWaves];
     __shared__ float wmax[kWaves];
     __shared__ int widx[kWaves];
-    stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
+    if constexpr (Ty::kIntX) stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red);
+    else stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
+    const auto xview = [&] {
+        if constexpr (Ty::kIntX) return xq_view(xs, a.k);
+        else return (const float*)xs;
+    }();
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // rows a wave accumulates at once; in SILU mode rows [j] and [R/2 + j]
@@ -383,7 +517,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             const int cn = chunk_of(it + 1);
             if (cn < nchunks) Ty::load(a.w, rbytes, rows, cn, nxt);
         }
-        if (c < nchunks) Ty::compute(cur, c, xs, a.form, acc);
+        if (c < nchunks) Ty::compute(cur, c, xview, a.form, acc);
         cur = nxt;
         if (it % cpl == cpl - 1) {
             // row group complete: reduce across lanes and write
@@ -478,7 +612,9 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st) {
     const int64_t n_out = mode == GEMV_SILU ? a.n / 2 : a.n;
     const int64_t n_groups = (n_out + kout - 1) / kout;
     const unsigned grid = (unsigned)gemv_grid((n_groups + kWaves - 1) / kWaves);
-    const size_t lds = (size_t)(a.k + (a.k >> 4)) * sizeof(float);
+    // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
+    const size_t lds = T<R>::kIntX ? (size_t)a.k * 2 + (size_t)(a.k / 32 + a.k / 16) * 4
+                                   : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
     if (mode == GEMV_PLAIN) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN>), dim3(grid), dim3(kThreads), lds, st, a);
     else if (mode == GEMV_SILU) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU>), dim3(grid), dim3(kThreads), lds, st, a);
     else {
