@@ -1,8 +1,12 @@
 """Parity of the HIP dequant / GEMV kernels with the CPU oracle (GPU).
 
 Bars: dequantized weights bit-exact; GEMV fp32 output within 1e-3 relative
-(tested as |y - y_ref| <= 1e-3 * |y_ref| + 1e-5 * max|y_ref|, plus a global
-max-error / max-value bound of 1e-4).
+of the CPU kernel, tested per element as |y - y_ref| <= 1e-3 * |y_ref| +
+1e-4 * max|y_ref| (the floor keeps outputs that cancel to ~0 from demanding
+unbounded relative accuracy), plus a global max-error / max-value bound of
+1e-4.  The quantized kernels stage x as 16-bit block fixed point, which
+bounds their deviation at about 2^-16 of each 32-element sub-block's largest
+|x|; the weights themselves are used exactly.
 """
 from __future__ import annotations
 
@@ -66,7 +70,7 @@ def test_f16_decode_exhaustive(mxh):
 def check_close(got, want, rtol=1e-3):
     scale = float(np.abs(want).max()) or 1.0
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    assert np.all(err <= rtol * np.abs(want) + 1e-5 * scale), f"max err {err.max()} scale {scale}"
+    assert np.all(err <= rtol * np.abs(want) + 1e-4 * scale), f"max err {err.max()} scale {scale}"
     assert err.max() / scale <= 1e-4, f"max err / max value = {err.max() / scale}"
 
 
