@@ -96,6 +96,23 @@ __device__ __forceinline__ void load_block_2aligned(const uint8_t* base, size_t 
     bd[n] = ub;
 }
 
+// Wave64 sum with DPP row operations; the total lands in lane 63
+// (quad swaps, half-row and row mirrors, then row broadcasts 15 and 31).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v += dpp_f<0xb1>(v);        // quad_perm [1,0,3,2]
+    v += dpp_f<0x4e>(v);        // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);       // row_half_mirror
+    v += dpp_f<0x140>(v);       // row_mirror
+    v += dpp_f<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 // ---- staged x in LDS ------------------------------------------------------
 // Quantized formats: lo/hi limb bytes (K each), per-32 scales (K/32) and
 // per-16 scaled sums s_j * sum X_i (K/16).
@@ -488,43 +505,40 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     float best = -INFINITY;
     int best_i = 0x7fffffff;
 
-    auto rows_of = [&](int it, int (&rows)[R]) {
-        const int grp = wave_id + (it / cpl) * n_waves;
+    // (chunk step j, row-group ordinal g) cursors: one issues weight loads two
+    // steps ahead, one consumes; the loop is unrolled by three so the three
+    // register buffers keep fixed names (no copies, no dynamic indexing)
+    struct Cursor {
+        int j, g;
+    };
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    auto issue = [&](Cursor& cu, Buf& b) {
+        const int grp = wave_id + cu.g * n_waves;
+        int rows[R];
 #pragma unroll
         for (int r = 0; r < kOut; ++r) {
             const int o = min(grp * kOut + r, n_out - 1);  // clamp loads in bounds
             rows[r] = o;
             if (MODE == GEMV_SILU) rows[kOut + r] = o + n_out;
         }
-    };
-    auto chunk_of = [&](int it) { return lane + 64 * (it % cpl); };
-
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    Buf cur, nxt;
-    if (total > 0) {
-        int rows[R];
-        rows_of(0, rows);
-        const int c0 = chunk_of(0);
-        if (c0 < nchunks) Ty::load(a.w, rbytes, rows, c0, cur);
-    }
-    for (int it = 0; it < total; ++it) {
-        const int c = chunk_of(it);
-        if (it + 1 < total) {
-            int rows[R];
-            rows_of(it + 1, rows);
-            const int cn = chunk_of(it + 1);
-            if (cn < nchunks) Ty::load(a.w, rbytes, rows, cn, nxt);
+        const int c = lane + 64 * cu.j;
+        if (c < nchunks) Ty::load(a.w, rbytes, rows, c, b);
+        if (++cu.j == cpl) {
+            cu.j = 0;
+            ++cu.g;
         }
-        if (c < nchunks) Ty::compute(cur, c, xview, a.form, acc);
-        cur = nxt;
-        if (it % cpl == cpl - 1) {
-            // row group complete: reduce across lanes and write
-            const int grp = wave_id + (it / cpl) * n_waves;
+    };
+    auto consume = [&](Cursor& cu, const Buf& b) {
+        const int c = lane + 64 * cu.j;
+        if (c < nchunks) Ty::compute(b, c, xview, a.form, acc);
+        if (cu.j == cpl - 1) {
+            // row group complete: reduce across lanes (total lands in lane 63) and write
+            const int grp = wave_id + cu.g * n_waves;
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-            if (lane == 0) {
+            for (int r = 0; r < R; ++r) acc[r] = wave_sum_lane63(acc[r]);
+            if (lane == 63) {
 #pragma unroll
                 for (int r = 0; r < kOut; ++r) {
                     const int o = grp * kOut + r;
@@ -547,9 +561,27 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = 0.f;
         }
+        if (++cu.j == cpl) {
+            cu.j = 0;
+            ++cu.g;
+        }
+    };
+    Cursor ci{0, 0}, cc{0, 0};
+    Buf b0, b1, b2;
+    if (total > 0) issue(ci, b0);
+    if (total > 1) issue(ci, b1);
+    for (int it = 0; it < total; it += 3) {
+        if (it + 2 < total) issue(ci, b2);
+        consume(cc, b0);
+        if (it + 1 >= total) break;
+        if (it + 3 < total) issue(ci, b0);
+        consume(cc, b1);
+        if (it + 2 >= total) break;
+        if (it + 4 < total) issue(ci, b1);
+        consume(cc, b2);
     }
     if constexpr (MODE == GEMV_ARGMAX) {
-        if (lane == 0) {
+        if (lane == 63) {
             wmax[wave] = best;
             widx[wave] = best_i;
         }
@@ -599,19 +631,17 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* __rest
     }
 }
 
-// Persistent grid: enough workgroups to fill the chip, never more than there
-// are row groups.
-int gemv_grid(int64_t wgs_needed) {
-    const int64_t cap = 1024;  // 4 workgroups (16 waves) per CU on 256 CUs
-    return (int)(wgs_needed < cap ? wgs_needed : cap);
-}
+// Persistent grid: enough workgroups to fill the chip (default 4 per CU on
+// 256 CUs), never more than there are row groups.
+constexpr int kGridCap = 1024;
 
 template <template <int> class T, int R>
-int launch_gemv(const GemvArgs& a, int mode, hipStream_t st) {
+int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = kGridCap) {
     const int kout = mode == GEMV_SILU ? R / 2 : R;
     const int64_t n_out = mode == GEMV_SILU ? a.n / 2 : a.n;
     const int64_t n_groups = (n_out + kout - 1) / kout;
-    const unsigned grid = (unsigned)gemv_grid((n_groups + kWaves - 1) / kWaves);
+    const int64_t need = (n_groups + kWaves - 1) / kWaves;
+    const unsigned grid = (unsigned)(need < grid_cap ? need : grid_cap);
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
     const size_t lds = T<R>::kIntX ? (size_t)a.k * 2 + (size_t)(a.k / 32 + a.k / 16) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
@@ -635,10 +665,10 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     if (a.k % 32 || a.k > kGemvMaxK || a.n <= 0 || (mode == GEMV_SILU && a.n % 2)) return MXH_ERR_ARG;
     if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.tokens || !a.pos)) return MXH_ERR_ARG;
     switch (type) {
-    case MXH_Q4_K: return launch_gemv<Q4K, 2>(a, mode, st);
-    case MXH_Q5_K: return launch_gemv<Q5K, 2>(a, mode, st);
-    case MXH_Q8_0: return launch_gemv<Q80, 2>(a, mode, st);
-    case MXH_Q5_0: return launch_gemv<Q50, 2>(a, mode, st);
+    case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);
+    case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
+    case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
+    case MXH_Q5_0: return launch_gemv<Q50, 4>(a, mode, st);
     case MXH_F32: return launch_gemv<F32W, 2>(a, mode, st);
     }
     return MXH_ERR_UNSUPPORTED;
