@@ -483,12 +483,6 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __shared__ double red[kWaves];
     __shared__ float wmax[kWaves];
     __shared__ int widx[kWaves];
-    if constexpr (Ty::kIntX) stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red);
-    else stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
-    const auto xview = [&] {
-        if constexpr (Ty::kIntX) return xq_view(xs, a.k);
-        else return (const float*)xs;
-    }();
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     // rows a wave accumulates at once; in SILU mode rows [j] and [R/2 + j]
@@ -511,6 +505,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     struct Cursor {
         int j, g;
     };
+    const auto xview = [&] {  // layout of the staged x (filled below)
+        if constexpr (Ty::kIntX) return xq_view(xs, a.k);
+        else return (const float*)xs;
+    }();
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -568,8 +566,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     };
     Cursor ci{0, 0}, cc{0, 0};
     Buf b0, b1, b2;
+    // the first two steps' weight loads do not depend on x: issue them before
+    // staging x so both latencies overlap
     if (total > 0) issue(ci, b0);
     if (total > 1) issue(ci, b1);
+    if constexpr (Ty::kIntX) stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red);
+    else stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
     for (int it = 0; it < total; it += 3) {
         if (it + 2 < total) issue(ci, b2);
         consume(cc, b0);
@@ -587,13 +589,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         }
         __syncthreads();
         if (threadIdx.x == 0) {
+            float bv = wmax[0];
+            int bi = widx[0];
             for (int w2 = 1; w2 < kWaves; ++w2)
-                if (wmax[w2] > best || (wmax[w2] == best && widx[w2] < best_i)) {
-                    best = wmax[w2];
-                    best_i = widx[w2];
+                if (wmax[w2] > bv || (wmax[w2] == bv && widx[w2] < bi)) {
+                    bv = wmax[w2];
+                    bi = widx[w2];
                 }
-            a.red_val[blockIdx.x] = best;
-            a.red_idx[blockIdx.x] = best_i;
+            a.red_val[blockIdx.x] = bv;
+            a.red_idx[blockIdx.x] = bi;
         }
     }
 }
