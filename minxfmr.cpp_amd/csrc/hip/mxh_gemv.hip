@@ -377,6 +377,7 @@ struct F32W {
 __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, const float* __restrict__ nw,
                                         int k, float eps, double* red) {
     if (!nw) {
+#pragma unroll 4
         for (int e = threadIdx.x * 4; e < k; e += kThreads * 4)
             *reinterpret_cast<float4*>(xs + xpad(e)) = *reinterpret_cast<const float4*>(x + e);
         __syncthreads();
@@ -410,61 +411,123 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // handles 4 consecutive elements; the 8 threads of a 32-element sub-block
 // share its maximum through shuffles.  With a norm weight x is first
 // replaced by the reference rmsnorm, as in stage_x.
+// DPP reductions inside groups of 4 / 8 lanes and across the wave (double).
+__device__ __forceinline__ float max8_dpp(float v) {
+    v = fmaxf(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
+    return fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of the 8
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+__device__ __forceinline__ int sum4_dpp(int v) {
+    v += dpp_i<0xb1>(v);
+    return v + dpp_i<0x4e>(v);
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROW_MASK, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// wave sum of doubles; the total lands in lane 63
+__device__ __forceinline__ double wave_sum_d_lane63(double v) {
+    v += dpp_d<0xb1>(v);
+    v += dpp_d<0x4e>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
+    v += dpp_d<0x142, 0xa>(v);
+    v += dpp_d<0x143, 0xc>(v);
+    return v;
+}
+
+// Stage x as 16-bit block fixed point (see the file comment).  Each thread
+// handles groups of 4 consecutive elements; the 8 threads of a 32-element
+// sub-block share its maximum through DPP.  With a norm weight x is first
+// replaced by the reference rmsnorm, as in stage_x.
 __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
                                          int k, float eps, double* red) {
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
     uint32_t* hi = lo + k / 4;
     float* scale = reinterpret_cast<float*>(lo + k / 2);
     float* sum16 = scale + k / 32;
+    // x loads are issued in batches of kB per thread so their latencies
+    // overlap (the DPP steps below are convergent, which blocks automatic
+    // unrolling of a loop with a runtime trip count)
+    constexpr int kB = 4;
+    constexpr int kStep = kThreads * 4;
     double inv = 1.0;
     if (nw) {
         double ss = 0.0;
-        for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
-            const float4 v = *reinterpret_cast<const float4*>(x + e);
-            ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-        }
+        for (int base = threadIdx.x * 4; base < k; base += kB * kStep) {
+            float4 v[kB];
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+            for (int u = 0; u < kB; ++u) {
+                const int e = base + u * kStep;
+                v[u] = e < k ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u)
+                ss += (double)v[u].x * v[u].x + (double)v[u].y * v[u].y + (double)v[u].z * v[u].z +
+                      (double)v[u].w * v[u].w;
+        }
+        ss = wave_sum_d_lane63(ss);
+        if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
         inv = 1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps);
     }
-    for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
-        float4 v = *reinterpret_cast<const float4*>(x + e);
-        if (nw) {
-            const float4 g = *reinterpret_cast<const float4*>(nw + e);
-            v.x = (float)((double)v.x * inv) * g.x;
-            v.y = (float)((double)v.y * inv) * g.y;
-            v.z = (float)((double)v.z * inv) * g.z;
-            v.w = (float)((double)v.w * inv) * g.w;
-        }
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite)
-        const bool live = m > 1e-30f;
-        const float sc = live ? m / 32512.0f : 0.f;
-        const float is = live ? 32512.0f / m : 0.f;
-        const float vv[4] = {v.x, v.y, v.z, v.w};
-        uint32_t plo = 0, phi = 0;
-        int sum = 0;
+    for (int base = threadIdx.x * 4; base < k; base += kB * kStep) {
+        float4 v[kB], g[kB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int X = (int)rintf(vv[i] * is);
-            X = X > 32512 ? 32512 : (X < -32512 ? -32512 : X);
-            const int l = ((X + 128) & 255) - 128;
-            const int h = (X - l) >> 8;
-            plo |= (uint32_t)(l & 255) << (8 * i);
-            phi |= (uint32_t)(h & 255) << (8 * i);
-            sum += X;
+        for (int u = 0; u < kB; ++u) {
+            const int e = base + u * kStep;
+            const bool in = e < k;
+            v[u] = in ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (nw) g[u] = in ? *reinterpret_cast<const float4*>(nw + e) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        lo[e >> 2] = plo;
-        hi[e >> 2] = phi;
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * (float)sum;
-        if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            const int e = base + u * kStep;
+            float4 w4 = v[u];
+            if (nw) {
+                w4.x = (float)((double)w4.x * inv) * g[u].x;
+                w4.y = (float)((double)w4.y * inv) * g[u].y;
+                w4.z = (float)((double)w4.z * inv) * g[u].z;
+                w4.w = (float)((double)w4.w * inv) * g[u].w;
+            }
+            // groups of 8 threads (one sub-block) are all in or all out of range
+            const float m = max8_dpp(fmaxf(fmaxf(fabsf(w4.x), fabsf(w4.y)), fmaxf(fabsf(w4.z), fabsf(w4.w))));
+            // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite)
+            const bool live = m > 1e-30f;
+            const float sc = live ? m / 32512.0f : 0.f;
+            const float is = live ? 32512.0f / m : 0.f;
+            const float vv[4] = {w4.x, w4.y, w4.z, w4.w};
+            uint32_t plo = 0, phi = 0;
+            int sum = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int X = (int)rintf(vv[i] * is);
+                X = X > 32512 ? 32512 : (X < -32512 ? -32512 : X);
+                const int l = ((X + 128) & 255) - 128;
+                const int h = (X - l) >> 8;
+                plo |= (uint32_t)(l & 255) << (8 * i);
+                phi |= (uint32_t)(h & 255) << (8 * i);
+                sum += X;
+            }
+            sum = sum4_dpp(sum);
+            if (e < k) {
+                lo[e >> 2] = plo;
+                hi[e >> 2] = phi;
+                if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * (float)sum;
+                if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
+            }
+        }
     }
     __syncthreads();
 }
@@ -635,20 +698,47 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* __rest
     }
 }
 
-// Persistent grid: enough workgroups to fill the chip (default 4 per CU on
-// 256 CUs), never more than there are row groups.
-constexpr int kGridCap = 1024;
+// Resident workgroups of a kernel on the whole device (occupancy x CUs),
+// cached per kernel and LDS size: a persistent grid of exactly this size runs
+// in one round, so each resident slot stages x once.
+int resident_grid(const void* kernel, size_t lds) {
+    struct Entry {
+        const void* k;
+        size_t lds;
+        int grid;
+    };
+    static Entry cache[64];
+    static int n_cache = 0;
+    static int n_cu = 0;
+    for (int i = 0; i < n_cache; ++i)
+        if (cache[i].k == kernel && cache[i].lds == lds) return cache[i].grid;
+    if (!n_cu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n_cu = 256;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int grid = per_cu * n_cu;
+    if (n_cache < 64) cache[n_cache++] = Entry{kernel, lds, grid};
+    return grid;
+}
 
 template <template <int> class T, int R>
-int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = kGridCap) {
+int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const int kout = mode == GEMV_SILU ? R / 2 : R;
     const int64_t n_out = mode == GEMV_SILU ? a.n / 2 : a.n;
     const int64_t n_groups = (n_out + kout - 1) / kout;
     const int64_t need = (n_groups + kWaves - 1) / kWaves;
-    const unsigned grid = (unsigned)(need < grid_cap ? need : grid_cap);
+    const void* kern = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN>
+                       : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU>
+                                           : (const void*)gemv_kernel<T, R, GEMV_ARGMAX>;
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
     const size_t lds = T<R>::kIntX ? (size_t)a.k * 2 + (size_t)(a.k / 32 + a.k / 16) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
+    const int cap = grid_cap > 0 ? grid_cap : resident_grid(kern, lds);
+    const unsigned grid = (unsigned)(need < cap ? need : cap);
     if (mode == GEMV_PLAIN) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN>), dim3(grid), dim3(kThreads), lds, st, a);
     else if (mode == GEMV_SILU) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU>), dim3(grid), dim3(kThreads), lds, st, a);
     else {
