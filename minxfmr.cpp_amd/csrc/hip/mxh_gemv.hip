@@ -96,23 +96,6 @@ __device__ __forceinline__ void load_block_2aligned(const uint8_t* base, size_t 
     bd[n] = ub;
 }
 
-// Wave64 sum with DPP row operations; the total lands in lane 63
-// (quad swaps, half-row and row mirrors, then row broadcasts 15 and 31).
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
-}
-
-__device__ __forceinline__ float wave_sum_lane63(float v) {
-    v += dpp_f<0xb1>(v);        // quad_perm [1,0,3,2]
-    v += dpp_f<0x4e>(v);        // quad_perm [2,3,0,1]
-    v += dpp_f<0x141>(v);       // row_half_mirror
-    v += dpp_f<0x140>(v);       // row_mirror
-    v += dpp_f<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-    v += dpp_f<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-    return v;
-}
-
 // ---- staged x in LDS ------------------------------------------------------
 // Quantized formats: lo/hi limb bytes (K each), per-32 scales (K/32) and
 // per-16 scaled sums s_j * sum X_i (K/16).
@@ -411,42 +394,6 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // handles 4 consecutive elements; the 8 threads of a 32-element sub-block
 // share its maximum through shuffles.  With a norm weight x is first
 // replaced by the reference rmsnorm, as in stage_x.
-// DPP reductions inside groups of 4 / 8 lanes and across the wave (double).
-__device__ __forceinline__ float max8_dpp(float v) {
-    v = fmaxf(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
-    return fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror: the other quad of the 8
-}
-
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
-}
-
-__device__ __forceinline__ int sum4_dpp(int v) {
-    v += dpp_i<0xb1>(v);
-    return v + dpp_i<0x4e>(v);
-}
-
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ double dpp_d(double v) {
-    const long long b = __double_as_longlong(v);
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, ROW_MASK, 0xf, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROW_MASK, 0xf, false);
-    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
-}
-
-// wave sum of doubles; the total lands in lane 63
-__device__ __forceinline__ double wave_sum_d_lane63(double v) {
-    v += dpp_d<0xb1>(v);
-    v += dpp_d<0x4e>(v);
-    v += dpp_d<0x141>(v);
-    v += dpp_d<0x140>(v);
-    v += dpp_d<0x142, 0xa>(v);
-    v += dpp_d<0x143, 0xc>(v);
-    return v;
-}
-
 // Stage x as 16-bit block fixed point (see the file comment).  Each thread
 // handles groups of 4 consecutive elements; the 8 threads of a 32-element
 // sub-block share its maximum through DPP.  With a norm weight x is first

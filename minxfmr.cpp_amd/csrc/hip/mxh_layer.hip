@@ -51,11 +51,11 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
 }
 
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
-constexpr int kAttnMaxPos = 512;    // positions one workgroup may cover
+constexpr int kAttnMaxPos = 1024;   // positions one workgroup may cover
 constexpr int kAttnMaxSplits = 64;  // splits per kv head (one lane each in the merge)
 
-// Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice held by a
-// wave; result written to dst (LDS or global), `src` is the raw projection.
+// Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
+// wave; `src` is the raw projection, the result goes to dst (LDS).
 __device__ void head_prep(const float* __restrict__ src, const float* __restrict__ bias,
                           const float* __restrict__ nw, const double* __restrict__ cs, float* dst, int hd, float eps,
                           int neox) {
@@ -67,8 +67,7 @@ __device__ void head_prep(const float* __restrict__ src, const float* __restrict
         if (t < hd) v[r] = src[t] + (bias ? bias[t] : 0.f);
     }
     if (nw) {
-        double ss = (double)v[0] * v[0] + (double)v[1] * v[1];
-        ss = wave_sum_d(ss);
+        const double ss = wave_sum_d_all((double)v[0] * v[0] + (double)v[1] * v[1]);
         const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
@@ -82,37 +81,43 @@ __device__ void head_prep(const float* __restrict__ src, const float* __restrict
         if (t < hd) dst[t] = v[r];
     }
     __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    // RoPE (rope.cpp:6-57): pair i = (2i, 2i+1), or (i, i + hd/2) for NeoX
-    const int half = hd / 2;
-    float a0 = 0.f, a1 = 0.f;
-    const int i = lane;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // RoPE (rope.cpp:6-57): pair i = (2i, 2i+1), or (i, i + hd/2) for NeoX;
+    // each lane reads and rewrites only its own pair
+    const int half = hd / 2, i = lane;
     if (i < half) {
         const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
         const double c = cs[2 * i], s = cs[2 * i + 1];
         const double x0 = dst[ia], x1 = dst[ib];
-        a0 = (float)(x0 * c - x1 * s);
-        a1 = (float)(x0 * s + x1 * c);
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (i < half) {
-        dst[neox ? i : 2 * i] = a0;
-        dst[neox ? i + half : 2 * i + 1] = a1;
+        dst[ia] = (float)(x0 * c - x1 * s);
+        dst[ib] = (float)(x0 * s + x1 * c);
     }
 }
 
-// Decode attention for one kv head g and one split s of the L = pos+1
-// positions (transformer.cpp:529-629): q heads of the group are normed and
-// rotated in LDS; the split holding position pos also prepares k and v of
-// the current token and appends them (fp16) to the cache.  Each split writes
-// (max, sum of exp, unnormalised exp-weighted V) per q head; the last split
-// to finish merges the partials in split order into att.
+// sum over aligned groups of `lpp` lanes (a power of two <= 16); every lane of
+// the group ends with the group sum
+__device__ __forceinline__ float lane_group_sum(float v, int lpp) {
+    if (lpp >= 2) v += dpp_f<0xb1>(v);
+    if (lpp >= 4) v += dpp_f<0x4e>(v);
+    if (lpp >= 8) v += dpp_f<0x141>(v);
+    if (lpp >= 16) v += dpp_f<0x140>(v);
+    return v;
+}
+
+// Decode attention for kv head g and split s of the L = pos+1 positions
+// (transformer.cpp:529-629).  The group's q heads are normed and rotated in
+// LDS.  The split holding position pos also prepares k and v of the current
+// token: it appends them (fp16) to the cache and uses its own fp16-rounded
+// copies for position pos, so no workgroup reads a cache row written in the
+// same launch.  With one split the normalised output goes straight to att;
+// with several, each split writes (max, sum of exp, exp-weighted V) per q
+// head and the last split to finish merges them in split order.
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     __shared__ float qs[kAttnMaxGroup * 128];
     __shared__ float sc[kAttnMaxGroup][kAttnMaxPos];
-    __shared__ float kv_tmp[2][128];
+    __shared__ float kvt[2][128];
     __shared__ float vacc[4][kAttnMaxGroup][128];
+    __shared__ float ml[kAttnMaxGroup][2];
     __shared__ int last;
     const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
     const int hd = a.hd, group = a.nh / a.nkv, kvd = a.nkv * hd, qd = a.nh * hd;
@@ -120,9 +125,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     const int pos = *a.pos, L = pos + 1;
     const int j0 = (int)(((long long)s * L) / S), j1 = (int)(((long long)(s + 1) * L) / S);
     const int nj = j1 - j0;
+    const bool owns = nj > 0 && j1 == L;
+    const int ncache = owns ? nj - 1 : nj;  // positions read from the cache
     const double* cs = a.rope_cs + (size_t)pos * hd;  // (hd/2) pairs of (cos, sin)
-    __half* kc = a.kc;
-    __half* vc = a.vc;
 
     if (nj > 0) {
         for (int h = wave; h < group; h += 4) {
@@ -130,24 +135,27 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             head_prep(a.qkv + (size_t)qh * hd, a.bias ? a.bias + (size_t)qh * hd : nullptr, a.q_norm, cs,
                       qs + h * hd, hd, a.eps, a.neox);
         }
-        if (j1 == L) {
-            // this split owns the current position: k and v of kv head g
-            if (wave == 0)
-                head_prep(a.qkv + qd + (size_t)g * hd, a.bias ? a.bias + qd + (size_t)g * hd : nullptr, a.k_norm,
-                          cs, kv_tmp[0], hd, a.eps, a.neox);
-            if (wave == 1)
-                for (int t = lane; t < hd; t += 64)
-                    kv_tmp[1][t] = a.qkv[qd + kvd + (size_t)g * hd + t] +
-                                   (a.bias ? a.bias[qd + kvd + (size_t)g * hd + t] : 0.f);
-            __syncthreads();
-            for (int t = tid; t < 2 * hd; t += 256) {
-                const int which = t / hd, tt = t % hd;
-                (which ? vc : kc)[(size_t)pos * kvd + (size_t)g * hd + tt] = __float2half_rn(kv_tmp[which][tt]);
+        if (owns && wave >= 2) {
+            // k (wave 3) or v (wave 2) of the current token, rounded through
+            // fp16 like every cached position, appended to the cache
+            float* dst = kvt[wave - 2];
+            const size_t off = (wave == 3 ? qd : qd + kvd) + (size_t)g * hd;
+            if (wave == 3) {
+                head_prep(a.qkv + off, a.bias ? a.bias + off : nullptr, a.k_norm, cs, dst, hd, a.eps, a.neox);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            }
+            __half* cache = (wave == 3 ? a.kc : a.vc) + (size_t)pos * kvd + (size_t)g * hd;
+            for (int t = lane; t < hd; t += 64) {
+                const float v = wave == 3 ? dst[t] : a.qkv[off + t] + (a.bias ? a.bias[off + t] : 0.f);
+                const __half hv = __float2half_rn(v);
+                dst[t] = __half2float(hv);
+                cache[t] = hv;
             }
         }
         __syncthreads();
-
-        // scores: LPP lanes per position, 8 dims (one 16-byte load) each
+        // scores of cached positions: lpp lanes per position, 8 dims (one
+        // 16-byte load of fp16 K) per lane
         const int lpp = hd / 8, ppw = 64 / lpp;
         const int sub = lane % lpp, slot = lane / lpp;
         float qreg[kAttnMaxGroup][8];
@@ -155,13 +163,15 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int h = 0; h < kAttnMaxGroup; ++h)
 #pragma unroll
             for (int e = 0; e < 8; ++e) qreg[h][e] = h < group ? qs[h * hd + sub * 8 + e] : 0.f;
-        for (int jb = wave * ppw; jb < nj; jb += 4 * ppw) {
-            const int jj = jb + slot;
-            float dot[kAttnMaxGroup];
+        const __half* kbase = a.kc + (size_t)j0 * kvd + (size_t)g * hd + sub * 8;
+        for (int jb = wave * ppw; jb < ncache; jb += 8 * ppw) {
+            // two positions per lane per iteration: both loads in flight together
+            float dot[2][kAttnMaxGroup];
 #pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) dot[h] = 0.f;
-            if (jj < nj) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(kc + (size_t)(j0 + jj) * kvd + (size_t)g * hd + sub * 8);
+            for (int u = 0; u < 2; ++u) {
+                const int jj = jb + u * 4 * ppw + slot;
+                uint4 raw = make_uint4(0, 0, 0, 0);
+                if (jj < ncache) raw = *reinterpret_cast<const uint4*>(kbase + (size_t)jj * kvd);
                 const __half2* hv = reinterpret_cast<const __half2*>(&raw);
                 float kf[8];
 #pragma unroll
@@ -171,16 +181,30 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
                     kf[2 * e + 1] = f.y;
                 }
 #pragma unroll
-                for (int h = 0; h < kAttnMaxGroup; ++h)
+                for (int h = 0; h < kAttnMaxGroup; ++h) {
+                    float d = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) dot[h] = fmaf(qreg[h][e], kf[e], dot[h]);
+                    for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
+                    dot[u][h] = d;
+                }
             }
 #pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) {
-                if (h >= group) break;
-                float d = dot[h];
-                for (int off = 1; off < lpp; off <<= 1) d += __shfl_xor(d, off, 64);
-                if (sub == 0 && jj < nj) sc[h][jj] = d * a.scale;
+            for (int u = 0; u < 2; ++u) {
+                const int jj = jb + u * 4 * ppw + slot;
+#pragma unroll
+                for (int h = 0; h < kAttnMaxGroup; ++h) {
+                    if (h >= group) break;
+                    const float d = lane_group_sum(dot[u][h], lpp);
+                    if (sub == 0 && jj < ncache) sc[h][jj] = d * a.scale;
+                }
+            }
+        }
+        if (owns && wave == 0) {
+            for (int h = 0; h < group; ++h) {
+                float d = 0.f;
+                for (int t = lane; t < hd; t += 64) d = fmaf(qs[h * hd + t], kvt[0][t], d);
+                d = wave_sum_all(d);
+                if (lane == 0) sc[h][nj - 1] = d * a.scale;
             }
         }
         __syncthreads();
@@ -188,18 +212,17 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int h = wave; h < group; h += 4) {
             float m = -INFINITY;
             for (int jj = lane; jj < nj; jj += 64) m = fmaxf(m, sc[h][jj]);
-            m = wave_max(m);
+            m = wave_max_all(m);
             float l = 0.f;
             for (int jj = lane; jj < nj; jj += 64) {
                 const float e = expf(sc[h][jj] - m);
                 sc[h][jj] = e;
                 l += e;
             }
-            l = wave_sum(l);
+            l = wave_sum_all(l);
             if (lane == 0) {
-                float* p = a.part + ((size_t)(g * group + h) * S + s) * (hd + 2);
-                p[0] = m;
-                p[1] = l;
+                ml[h][0] = m;
+                ml[h][1] = l;
             }
         }
         __syncthreads();
@@ -209,15 +232,27 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             float acc[kAttnMaxGroup][2];
 #pragma unroll
             for (int h = 0; h < kAttnMaxGroup; ++h) acc[h][0] = acc[h][1] = 0.f;
-            for (int jj = phase; jj < nj; jj += 4) {
-                const float2 v = __half22float2(
-                    *reinterpret_cast<const __half2*>(vc + (size_t)(j0 + jj) * kvd + (size_t)g * hd + 2 * t2));
+            const __half* vbase = a.vc + (size_t)j0 * kvd + (size_t)g * hd + 2 * t2;
+            for (int jj = phase; jj < ncache; jj += 8) {
+                const float2 v0 = __half22float2(*reinterpret_cast<const __half2*>(vbase + (size_t)jj * kvd));
+                float2 v1 = make_float2(0.f, 0.f);
+                const bool two = jj + 4 < ncache;
+                if (two) v1 = __half22float2(*reinterpret_cast<const __half2*>(vbase + (size_t)(jj + 4) * kvd));
 #pragma unroll
                 for (int h = 0; h < kAttnMaxGroup; ++h) {
                     if (h >= group) break;
-                    const float pr = sc[h][jj];
-                    acc[h][0] = fmaf(pr, v.x, acc[h][0]);
-                    acc[h][1] = fmaf(pr, v.y, acc[h][1]);
+                    const float p0 = sc[h][jj], p1 = two ? sc[h][jj + 4] : 0.f;
+                    acc[h][0] = fmaf(p1, v1.x, fmaf(p0, v0.x, acc[h][0]));
+                    acc[h][1] = fmaf(p1, v1.y, fmaf(p0, v0.y, acc[h][1]));
+                }
+            }
+            if (owns && phase == 0) {
+#pragma unroll
+                for (int h = 0; h < kAttnMaxGroup; ++h) {
+                    if (h >= group) break;
+                    const float p = sc[h][nj - 1];
+                    acc[h][0] = fmaf(p, kvt[1][2 * t2], acc[h][0]);
+                    acc[h][1] = fmaf(p, kvt[1][2 * t2 + 1], acc[h][1]);
                 }
             }
 #pragma unroll
@@ -233,33 +268,39 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             const int h = i / hd, t = i % hd;
             float v = 0.f;
             for (int ph = 0; ph < nphase; ++ph) v += vacc[ph][h][t];
-            a.part[((size_t)(g * group + h) * S + s) * (hd + 2) + 2 + t] = v;
+            if (S == 1) {
+                a.att[(size_t)(g * group + h) * hd + t] = v / ml[h][1];
+            } else {
+                float* p = a.part + ((size_t)(g * group + h) * S + s) * (hd + 2);
+                p[2 + t] = v;
+                if (t == 0) {
+                    p[0] = ml[h][0];
+                    p[1] = ml[h][1];
+                }
+            }
         }
     } else {
-        for (int h = tid; h < group; h += 256) {
-            float* p = a.part + ((size_t)(g * group + h) * S + s) * (hd + 2);
-            p[0] = -INFINITY;
-            p[1] = 0.f;
+        for (int i = tid; i < group * (hd + 2); i += 256) {
+            const int h = i / (hd + 2), t = i % (hd + 2);
+            a.part[((size_t)(g * group + h) * S + s) * (hd + 2) + t] = t == 0 ? -INFINITY : 0.f;
         }
-        for (int i = tid; i < group * hd; i += 256)
-            a.part[((size_t)(g * group + i / hd) * S + s) * (hd + 2) + 2 + i % hd] = 0.f;
     }
-    // last split of kv head g to finish merges the partials
+    if (S == 1) return;
+    // the last split of kv head g to finish merges the partials
     __threadfence();
     __syncthreads();
     if (tid == 0) last = atomicAdd(a.counter + g, 1) == S - 1;
     __syncthreads();
     if (!last) return;
     __threadfence();
-    // merge: lane i holds split i's (max, sum); weights e^(m_i - M) go through
-    // LDS so every lane can scale its dims of the partial sums
+    // lane i holds split i's (max, sum); weights e^(m_i - M) go through LDS
     for (int h = wave; h < group; h += 4) {
         const float* p = a.part + (size_t)(g * group + h) * S * (hd + 2);
         const float mi = lane < S ? __builtin_nontemporal_load(p + (size_t)lane * (hd + 2)) : -INFINITY;
         const float li = lane < S ? __builtin_nontemporal_load(p + (size_t)lane * (hd + 2) + 1) : 0.f;
-        const float M = wave_max(mi);
+        const float M = wave_max_all(mi);
         const float wi = lane < S ? expf(mi - M) : 0.f;
-        const float den = wave_sum(wi * li);
+        const float den = wave_sum_all(wi * li);
         sc[h][lane] = wi;
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -359,15 +400,21 @@ int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, h
     return MXH_OK;
 }
 
+// Splits per kv head: one (no merge pass) up to 256 positions, then about
+// 256 positions per split up to kAttnMaxSplits splits, and beyond that as
+// many as the LDS score buffer (kAttnMaxPos per split) needs.
 int attention_splits(int n_ctx) {
-    int S = n_ctx / 64;
-    S = S < 8 ? 8 : (S > 64 ? 64 : S);
+    int S = (n_ctx + 255) / 256;
+    S = S < 1 ? 1 : (S > kAttnMaxSplits ? kAttnMaxSplits : S);
     while ((n_ctx + S - 1) / S > kAttnMaxPos) ++S;
     return S;
 }
 
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
-    if (a.nh % a.nkv || a.nh / a.nkv > kAttnMaxGroup || a.hd > 128 || a.hd % 8 || a.hd < 16) return MXH_ERR_UNSUPPORTED;
+    // head_dim: a multiple of 8 with hd/8 a power of two (lanes per position)
+    const int lpp = a.hd / 8;
+    if (a.nh % a.nkv || a.nh / a.nkv > kAttnMaxGroup || a.hd > 128 || a.hd % 8 || a.hd < 16 || (lpp & (lpp - 1)))
+        return MXH_ERR_UNSUPPORTED;
     const int S = attention_splits(n_ctx);
     if (S > kAttnMaxSplits) return MXH_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(attention_kernel, dim3(a.nkv, S), dim3(256), 0, st, a);

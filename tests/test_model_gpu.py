@@ -67,6 +67,32 @@ def test_per_layer_activations_and_logits(mxh, tmp_path, name, flags):
     gm.close()
 
 
+@pytest.mark.parametrize("name,n_ctx,warm", [("q4k-qknorm", 600, 300), ("q5_0-gqa8", 1100, 40),
+                                             ("f32-hd128", 4000, 520)])
+def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
+    """Contexts long enough for several attention splits per kv head (merged
+    by the last split), including positions where some splits are empty."""
+    p = build(tmp_path, name)
+    gm = mxhip.Model(p, n_ctx)
+    om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
+    rng = np.random.default_rng(7)
+    toks = rng.integers(0, TINY["n_vocab"], warm + 6)
+    worst = 0.0
+    for i, tok in enumerate(toks):
+        check = i < 3 or i >= warm
+        lg, tr = gm.step(int(tok), trace=check, logits=check)
+        olg, otr = om.step(int(tok), trace=check)
+        if not check:
+            continue
+        ok, e1 = close_enough(tr, otr)
+        assert ok, f"position {i}: hidden trace error {e1}"
+        ok, e2 = close_enough(lg, olg)
+        assert ok, f"position {i}: logits error {e2}"
+        worst = max(worst, e1 / max(1.0, float(np.abs(otr).max())), e2)
+    assert worst < 1e-3, worst
+    gm.close()
+
+
 @pytest.mark.parametrize("name", ["q4k-qknorm", "q4k-mixed-q5k"])
 def test_graph_generate_matches_eager_steps_and_oracle(mxh, tmp_path, name):
     p = build(tmp_path, name)
