@@ -51,8 +51,8 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
 }
 
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
-constexpr int kAttnMaxPos = 1024;   // positions one workgroup may cover
-constexpr int kAttnMaxSplits = 64;  // splits per kv head (one lane each in the merge)
+constexpr int kAttnChunk = 64;      // positions per pass of a workgroup (one per lane in the softmax)
+constexpr int kAttnMaxSplits = 64;  // workgroups per kv head (one lane each in the merge)
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
 // wave; `src` is the raw projection, the result goes to dst (LDS).
@@ -94,223 +94,273 @@ __device__ void head_prep(const float* __restrict__ src, const float* __restrict
     }
 }
 
-// sum over aligned groups of `lpp` lanes (a power of two <= 16); every lane of
+// sum over aligned groups of LPP lanes (a power of two <= 16); every lane of
 // the group ends with the group sum
-__device__ __forceinline__ float lane_group_sum(float v, int lpp) {
-    if (lpp >= 2) v += dpp_f<0xb1>(v);
-    if (lpp >= 4) v += dpp_f<0x4e>(v);
-    if (lpp >= 8) v += dpp_f<0x141>(v);
-    if (lpp >= 16) v += dpp_f<0x140>(v);
+template <int LPP>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    if (LPP >= 2) v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+    if (LPP >= 4) v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+    if (LPP >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
+    if (LPP >= 16) v += dpp_f<0x140>(v); // row_mirror
     return v;
 }
 
-// Decode attention for kv head g and split s of the L = pos+1 positions
-// (transformer.cpp:529-629).  The group's q heads are normed and rotated in
-// LDS.  The split holding position pos also prepares k and v of the current
-// token: it appends them (fp16) to the cache and uses its own fp16-rounded
-// copies for position pos, so no workgroup reads a cache row written in the
-// same launch.  With one split the normalised output goes straight to att;
-// with several, each split writes (max, sum of exp, exp-weighted V) per q
-// head and the last split to finish merges them in split order.
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-    __shared__ float qs[kAttnMaxGroup * 128];
-    __shared__ float sc[kAttnMaxGroup][kAttnMaxPos];
-    __shared__ float kvt[2][128];
-    __shared__ float vacc[4][kAttnMaxGroup][128];
-    __shared__ float ml[kAttnMaxGroup][2];
-    __shared__ int last;
-    const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
-    const int hd = a.hd, group = a.nh / a.nkv, kvd = a.nkv * hd, qd = a.nh * hd;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int pos = *a.pos, L = pos + 1;
-    const int j0 = (int)(((long long)s * L) / S), j1 = (int)(((long long)(s + 1) * L) / S);
-    const int nj = j1 - j0;
-    const bool owns = nj > 0 && j1 == L;
-    const int ncache = owns ? nj - 1 : nj;  // positions read from the cache
-    const double* cs = a.rope_cs + (size_t)pos * hd;  // (hd/2) pairs of (cos, sin)
+__device__ __forceinline__ void half8_to_float(const uint4& raw, float* f) {
+    const __half2* h = reinterpret_cast<const __half2*>(&raw);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float2 t = __half22float2(h[e]);
+        f[2 * e] = t.x;
+        f[2 * e + 1] = t.y;
+    }
+}
 
-    if (nj > 0) {
-        for (int h = wave; h < group; h += 4) {
-            const int qh = g * group + h;
-            head_prep(a.qkv + (size_t)qh * hd, a.bias ? a.bias + (size_t)qh * hd : nullptr, a.q_norm, cs,
-                      qs + h * hd, hd, a.eps, a.neox);
+// Decode attention for kv head g over the L = pos+1 positions
+// (transformer.cpp:529-629), head_dim = 8 * LPP.
+//
+// Positions are taken in chunks of 64; workgroup s of the S per kv head takes
+// chunks s, s+S, ...  Thread (position group pg, lane sub) holds 8 dims
+// (one 16-byte fp16 load) of NP positions of K and of V, so a chunk's cache
+// rows are read with every load in flight at once.  Scores are reduced over
+// the LPP lanes of a position with DPP; one wave per q head keeps a running
+// softmax (max, sum) across chunks, and the exp-weighted V sums stay in
+// registers, rescaled per chunk.
+//
+// The workgroup holding chunk pos/64 also prepares k and v of the current
+// token: it appends them (fp16) to the cache and uses its LDS copies for
+// position pos, so no workgroup reads a cache row written in this launch.
+// With one active workgroup the normalised output is written directly;
+// otherwise each writes (max, sum, V sums) per q head and the last to finish
+// merges them.
+template <int LPP>
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+    constexpr int HD = LPP * 8, NPG = 256 / LPP, NP = kAttnChunk / NPG;
+    __shared__ float qs[kAttnMaxGroup][HD];
+    __shared__ float kvt[HD];
+    __shared__ __align__(16) __half kvh[2][HD];
+    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
+    __shared__ float run_m[kAttnMaxGroup], run_l[kAttnMaxGroup], alpha[kAttnMaxGroup];
+    __shared__ __align__(16) float red[4][kAttnMaxGroup][HD];
+    __shared__ float wgt[kAttnMaxGroup][kAttnMaxSplits];
+    __shared__ int last;
+
+    const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    const int group = a.nh / a.nkv, kvd = a.nkv * HD, qd = a.nh * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = tid % LPP, pg = tid / LPP;
+    const int pos = *a.pos, L = pos + 1;
+    const int nch = (L + kAttnChunk - 1) / kAttnChunk;
+    const int sact = nch < S ? nch : S;  // workgroups with work
+    if (s >= sact) return;
+    const int own_chunk = pos / kAttnChunk;
+    const bool owns = own_chunk % S == s;
+    const size_t col = (size_t)g * HD + sub * 8;
+
+    uint4 kraw[NP], vraw[NP];
+    // cache rows of this thread's positions in chunk c; positions >= pos are
+    // not read (pos itself comes from LDS)
+    auto load = [&](uint4* raw, const __half* cache, int c) {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int j = c * kAttnChunk + i * NPG + pg;
+            raw[i] = j < pos ? *reinterpret_cast<const uint4*>(cache + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
         }
-        if (owns && wave >= 2) {
-            // k (wave 3) or v (wave 2) of the current token, rounded through
-            // fp16 like every cached position, appended to the cache
-            float* dst = kvt[wave - 2];
-            const size_t off = (wave == 3 ? qd : qd + kvd) + (size_t)g * hd;
-            if (wave == 3) {
-                head_prep(a.qkv + off, a.bias ? a.bias + off : nullptr, a.k_norm, cs, dst, hd, a.eps, a.neox);
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-            }
-            __half* cache = (wave == 3 ? a.kc : a.vc) + (size_t)pos * kvd + (size_t)g * hd;
-            for (int t = lane; t < hd; t += 64) {
-                const float v = wave == 3 ? dst[t] : a.qkv[off + t] + (a.bias ? a.bias[off + t] : 0.f);
-                const __half hv = __float2half_rn(v);
-                dst[t] = __half2float(hv);
-                cache[t] = hv;
-            }
+    };
+    load(kraw, a.kc, s);
+    load(vraw, a.vc, s);
+
+    // q heads (and k, v of the current token) of this kv head
+    const double* cs = a.rope_cs + (size_t)pos * HD;  // (hd/2) pairs of (cos, sin)
+    const int njobs = group + (owns ? 2 : 0);
+    for (int job = wave; job < njobs; job += 4) {
+        if (job < group) {
+            const int qh = g * group + job;
+            head_prep(a.qkv + (size_t)qh * HD, a.bias ? a.bias + (size_t)qh * HD : nullptr, a.q_norm, cs, qs[job], HD,
+                      a.eps, a.neox);
+            continue;
         }
-        __syncthreads();
-        // scores of cached positions: lpp lanes per position, 8 dims (one
-        // 16-byte load of fp16 K) per lane
-        const int lpp = hd / 8, ppw = 64 / lpp;
-        const int sub = lane % lpp, slot = lane / lpp;
-        float qreg[kAttnMaxGroup][8];
-#pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qreg[h][e] = h < group ? qs[h * hd + sub * 8 + e] : 0.f;
-        const __half* kbase = a.kc + (size_t)j0 * kvd + (size_t)g * hd + sub * 8;
-        for (int jb = wave * ppw; jb < ncache; jb += 8 * ppw) {
-            // two positions per lane per iteration: both loads in flight together
-            float dot[2][kAttnMaxGroup];
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int jj = jb + u * 4 * ppw + slot;
-                uint4 raw = make_uint4(0, 0, 0, 0);
-                if (jj < ncache) raw = *reinterpret_cast<const uint4*>(kbase + (size_t)jj * kvd);
-                const __half2* hv = reinterpret_cast<const __half2*>(&raw);
-                float kf[8];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float2 f = __half22float2(hv[e]);
-                    kf[2 * e] = f.x;
-                    kf[2 * e + 1] = f.y;
-                }
-#pragma unroll
-                for (int h = 0; h < kAttnMaxGroup; ++h) {
-                    float d = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
-                    dot[u][h] = d;
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int jj = jb + u * 4 * ppw + slot;
-#pragma unroll
-                for (int h = 0; h < kAttnMaxGroup; ++h) {
-                    if (h >= group) break;
-                    const float d = lane_group_sum(dot[u][h], lpp);
-                    if (sub == 0 && jj < ncache) sc[h][jj] = d * a.scale;
-                }
-            }
+        const bool is_k = job == group;
+        const size_t off = (is_k ? qd : qd + kvd) + (size_t)g * HD;
+        if (is_k) {
+            head_prep(a.qkv + off, a.bias ? a.bias + off : nullptr, a.k_norm, cs, kvt, HD, a.eps, a.neox);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         }
-        if (owns && wave == 0) {
-            for (int h = 0; h < group; ++h) {
-                float d = 0.f;
-                for (int t = lane; t < hd; t += 64) d = fmaf(qs[h * hd + t], kvt[0][t], d);
-                d = wave_sum_all(d);
-                if (lane == 0) sc[h][nj - 1] = d * a.scale;
-            }
+        // rounded through fp16 like every cached position, and appended
+        __half* cache = (is_k ? a.kc : a.vc) + (size_t)pos * kvd + (size_t)g * HD;
+        for (int t = lane; t < HD; t += 64) {
+            const float v = is_k ? kvt[t] : a.qkv[off + t] + (a.bias ? a.bias[off + t] : 0.f);
+            const __half hv = __float2half_rn(v);
+            kvh[is_k ? 0 : 1][t] = hv;
+            cache[t] = hv;
         }
-        __syncthreads();
-        // per-head max and exp (softmax.cpp:4-18 up to the final division)
-        for (int h = wave; h < group; h += 4) {
-            float m = -INFINITY;
-            for (int jj = lane; jj < nj; jj += 64) m = fmaxf(m, sc[h][jj]);
-            m = wave_max_all(m);
-            float l = 0.f;
-            for (int jj = lane; jj < nj; jj += 64) {
-                const float e = expf(sc[h][jj] - m);
-                sc[h][jj] = e;
-                l += e;
-            }
-            l = wave_sum_all(l);
-            if (lane == 0) {
-                ml[h][0] = m;
-                ml[h][1] = l;
-            }
+    }
+    if (tid < kAttnMaxGroup) {
+        run_m[tid] = -INFINITY;
+        run_l[tid] = 0.f;
+    }
+    __syncthreads();
+
+    float qreg[kAttnMaxGroup][8], acc[kAttnMaxGroup][8];
+#pragma unroll
+    for (int h = 0; h < kAttnMaxGroup; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            qreg[h][e] = h < group ? qs[h][sub * 8 + e] : 0.f;
+            acc[h][e] = 0.f;
         }
-        __syncthreads();
-        // exp-weighted V: thread = (dim pair, one of four position phases)
-        const int npair = hd / 2, phase = tid / npair, t2 = tid % npair;
-        if (phase < 4) {
-            float acc[kAttnMaxGroup][2];
+
+    for (int c = s; c < nch; c += S) {
+        if (c == own_chunk) {
 #pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) acc[h][0] = acc[h][1] = 0.f;
-            const __half* vbase = a.vc + (size_t)j0 * kvd + (size_t)g * hd + 2 * t2;
-            for (int jj = phase; jj < ncache; jj += 8) {
-                const float2 v0 = __half22float2(*reinterpret_cast<const __half2*>(vbase + (size_t)jj * kvd));
-                float2 v1 = make_float2(0.f, 0.f);
-                const bool two = jj + 4 < ncache;
-                if (two) v1 = __half22float2(*reinterpret_cast<const __half2*>(vbase + (size_t)(jj + 4) * kvd));
-#pragma unroll
-                for (int h = 0; h < kAttnMaxGroup; ++h) {
-                    if (h >= group) break;
-                    const float p0 = sc[h][jj], p1 = two ? sc[h][jj + 4] : 0.f;
-                    acc[h][0] = fmaf(p1, v1.x, fmaf(p0, v0.x, acc[h][0]));
-                    acc[h][1] = fmaf(p1, v1.y, fmaf(p0, v0.y, acc[h][1]));
+            for (int i = 0; i < NP; ++i)
+                if (c * kAttnChunk + i * NPG + pg == pos) {
+                    kraw[i] = *reinterpret_cast<const uint4*>(&kvh[0][sub * 8]);
+                    vraw[i] = *reinterpret_cast<const uint4*>(&kvh[1][sub * 8]);
                 }
-            }
-            if (owns && phase == 0) {
+        }
+        // scores
 #pragma unroll
-                for (int h = 0; h < kAttnMaxGroup; ++h) {
-                    if (h >= group) break;
-                    const float p = sc[h][nj - 1];
-                    acc[h][0] = fmaf(p, kvt[1][2 * t2], acc[h][0]);
-                    acc[h][1] = fmaf(p, kvt[1][2 * t2 + 1], acc[h][1]);
-                }
-            }
+        for (int i = 0; i < NP; ++i) {
+            const int jl = i * NPG + pg, j = c * kAttnChunk + jl;
+            float kf[8];
+            half8_to_float(kraw[i], kf);
 #pragma unroll
             for (int h = 0; h < kAttnMaxGroup; ++h) {
                 if (h >= group) break;
-                vacc[phase][h][2 * t2] = acc[h][0];
-                vacc[phase][h][2 * t2 + 1] = acc[h][1];
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
+                d = lane_group_sum<LPP>(d);
+                if (sub == 0) sc[h][jl] = j < L ? d * a.scale : -INFINITY;
+            }
+        }
+        if (c + S < nch) load(kraw, a.kc, c + S);
+        __syncthreads();
+        // running softmax per q head (softmax.cpp:4-18, normalised at the end)
+        for (int h = wave; h < group; h += 4) {
+            const float sv = sc[h][lane];
+            const float mo = run_m[h], mn = fmaxf(mo, wave_max_all(sv));
+            const float p = expf(sv - mn), al = expf(mo - mn);
+            const float ps = wave_sum_all(p);
+            sc[h][lane] = p;
+            if (lane == 0) {
+                run_m[h] = mn;
+                run_l[h] = run_l[h] * al + ps;
+                alpha[h] = al;
             }
         }
         __syncthreads();
-        const int nphase = min(4, 256 / npair);
-        for (int i = tid; i < group * hd; i += 256) {
-            const int h = i / hd, t = i % hd;
-            float v = 0.f;
-            for (int ph = 0; ph < nphase; ++ph) v += vacc[ph][h][t];
-            if (S == 1) {
-                a.att[(size_t)(g * group + h) * hd + t] = v / ml[h][1];
-            } else {
-                float* p = a.part + ((size_t)(g * group + h) * S + s) * (hd + 2);
-                p[2 + t] = v;
-                if (t == 0) {
-                    p[0] = ml[h][0];
-                    p[1] = ml[h][1];
-                }
+        // exp-weighted V
+#pragma unroll
+        for (int h = 0; h < kAttnMaxGroup; ++h) {
+            if (h >= group) break;
+            const float al = alpha[h];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] *= al;
+        }
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            float vf[8];
+            half8_to_float(vraw[i], vf);
+#pragma unroll
+            for (int h = 0; h < kAttnMaxGroup; ++h) {
+                if (h >= group) break;
+                const float p = sc[h][i * NPG + pg];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
             }
         }
-    } else {
-        for (int i = tid; i < group * (hd + 2); i += 256) {
-            const int h = i / (hd + 2), t = i % (hd + 2);
-            a.part[((size_t)(g * group + h) * S + s) * (hd + 2) + t] = t == 0 ? -INFINITY : 0.f;
+        if (c + S < nch) load(vraw, a.vc, c + S);
+        __syncthreads();  // sc and alpha are rewritten by the next chunk
+    }
+
+    // sum the V partials of the position groups: lanes of a wave with the
+    // same `sub`, then the four waves through LDS
+#pragma unroll
+    for (int h = 0; h < kAttnMaxGroup; ++h) {
+        if (h >= group) break;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = acc[h][e];
+#pragma unroll
+            for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+            acc[h][e] = v;
+        }
+        if (lane < LPP) {
+            float4* dst = reinterpret_cast<float4*>(&red[wave][h][sub * 8]);
+            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
         }
     }
-    if (S == 1) return;
-    // the last split of kv head g to finish merges the partials
+    __syncthreads();
+    float* part_v = a.part;                                 // [nh][S][hd]
+    float* part_ml = a.part + (size_t)a.nh * S * HD;        // [nh][S][2]
+    for (int i = tid; i < group * HD; i += 256) {
+        const int h = i / HD, t = i % HD;
+        const float v = red[0][h][t] + red[1][h][t] + red[2][h][t] + red[3][h][t];
+        const size_t qh = (size_t)g * group + h;
+        if (sact == 1) {
+            a.att[qh * HD + t] = v / run_l[h];
+        } else {
+            part_v[(qh * S + s) * HD + t] = v;
+            if (t == 0) {
+                part_ml[(qh * S + s) * 2] = run_m[h];
+                part_ml[(qh * S + s) * 2 + 1] = run_l[h];
+            }
+        }
+    }
+    if (sact == 1) return;
+
+    // the last workgroup of kv head g to finish merges the partials
     __threadfence();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(a.counter + g, 1) == S - 1;
+    if (tid == 0) last = atomicAdd(a.counter + g, 1) == sact - 1;
     __syncthreads();
     if (!last) return;
     __threadfence();
-    // lane i holds split i's (max, sum); weights e^(m_i - M) go through LDS
     for (int h = wave; h < group; h += 4) {
-        const float* p = a.part + (size_t)(g * group + h) * S * (hd + 2);
-        const float mi = lane < S ? __builtin_nontemporal_load(p + (size_t)lane * (hd + 2)) : -INFINITY;
-        const float li = lane < S ? __builtin_nontemporal_load(p + (size_t)lane * (hd + 2) + 1) : 0.f;
+        const float* ml = part_ml + ((size_t)g * group + h) * S * 2;
+        const float mi = lane < sact ? ml[2 * lane] : -INFINITY;
+        const float li = lane < sact ? ml[2 * lane + 1] : 0.f;
         const float M = wave_max_all(mi);
-        const float wi = lane < S ? expf(mi - M) : 0.f;
+        const float wi = lane < sact ? expf(mi - M) : 0.f;
         const float den = wave_sum_all(wi * li);
-        sc[h][lane] = wi;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        for (int t = lane; t < hd; t += 64) {
-            float num = 0.f;
+        wgt[h][lane] = wi / den;
+    }
+    __syncthreads();
+    // (q head, 4 dims) items; the splits of an item are shared by `per` threads
+    const int items = group * HD / 4, per = 256 / items;
+    const int item = tid % items, part = tid / items;
+    float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (part < per) {
+        const int h = item / (HD / 4), d4 = item % (HD / 4);
+        const float4* src = reinterpret_cast<const float4*>(part_v + ((size_t)g * group + h) * S * HD) + d4;
 #pragma unroll 8
-            for (int i = 0; i < S; ++i)
-                num = fmaf(sc[h][i], __builtin_nontemporal_load(p + (size_t)i * (hd + 2) + 2 + t), num);
-            a.att[(size_t)(g * group + h) * hd + t] = num / den;
+        for (int i = part; i < sact; i += per) {
+            const float4 v = src[(size_t)i * (HD / 4)];
+            const float w = wgt[h][i];
+            s4.x = fmaf(w, v.x, s4.x);
+            s4.y = fmaf(w, v.y, s4.y);
+            s4.z = fmaf(w, v.z, s4.z);
+            s4.w = fmaf(w, v.w, s4.w);
         }
+    }
+    float4* r4 = reinterpret_cast<float4*>(&red[0][0][0]);  // 256 float4 fit: 4 * 8 * HD floats >= 1024
+    __syncthreads();
+    r4[tid] = s4;
+    __syncthreads();
+    if (tid < items) {
+        float4 t4 = r4[tid];
+        for (int p = 1; p < per; ++p) {
+            const float4 u = r4[p * items + tid];
+            t4.x += u.x;
+            t4.y += u.y;
+            t4.z += u.z;
+            t4.w += u.w;
+        }
+        const int h = tid / (HD / 4), d4 = tid % (HD / 4);
+        reinterpret_cast<float4*>(a.att + ((size_t)g * group + h) * HD)[d4] = t4;
     }
     if (tid == 0) a.counter[g] = 0;
 }
@@ -400,27 +450,31 @@ int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, h
     return MXH_OK;
 }
 
-// Splits per kv head: one (no merge pass) up to 256 positions, then about
-// 256 positions per split up to kAttnMaxSplits splits, and beyond that as
-// many as the LDS score buffer (kAttnMaxPos per split) needs.
+// Workgroups per kv head: one per 64-position chunk of the context, at most
+// kAttnMaxSplits (longer contexts give each several chunks).
 int attention_splits(int n_ctx) {
-    int S = (n_ctx + 255) / 256;
-    S = S < 1 ? 1 : (S > kAttnMaxSplits ? kAttnMaxSplits : S);
-    while ((n_ctx + S - 1) / S > kAttnMaxPos) ++S;
-    return S;
+    const int S = (n_ctx + kAttnChunk - 1) / kAttnChunk;
+    return S < 1 ? 1 : (S > kAttnMaxSplits ? kAttnMaxSplits : S);
+}
+
+// head_dim 32, 64 or 128 (8 dims per lane, a power-of-two lane count per
+// position); at most kAttnMaxGroup q heads per kv head
+bool attention_supported(int nh, int nkv, int hd) {
+    return nkv > 0 && nh % nkv == 0 && nh / nkv <= kAttnMaxGroup && (hd == 32 || hd == 64 || hd == 128);
 }
 
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
-    // head_dim: a multiple of 8 with hd/8 a power of two (lanes per position)
-    const int lpp = a.hd / 8;
-    if (a.nh % a.nkv || a.nh / a.nkv > kAttnMaxGroup || a.hd > 128 || a.hd % 8 || a.hd < 16 || (lpp & (lpp - 1)))
-        return MXH_ERR_UNSUPPORTED;
-    const int S = attention_splits(n_ctx);
-    if (S > kAttnMaxSplits) return MXH_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL(attention_kernel, dim3(a.nkv, S), dim3(256), 0, st, a);
+    if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
+    const dim3 grid(a.nkv, attention_splits(n_ctx));
+    switch (a.hd) {
+    case 32: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(256), 0, st, a); break;
+    }
     return MXH_OK;
 }
 
+// V partials [nh][S][hd] followed by (max, sum) pairs [nh][S][2]
 size_t attention_scratch_floats(int nh, int hd, int n_ctx) {
     return (size_t)nh * attention_splits(n_ctx) * (hd + 2);
 }

@@ -234,9 +234,8 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     };
     if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_head <= 0 || c.n_head_kv <= 0 || c.n_ff <= 0 || c.head_dim <= 0)
         return fail(MXH_ERR_ARG, "missing architecture metadata");
-    if (c.n_head % c.n_head_kv || c.n_head / c.n_head_kv > 8 || c.head_dim > 128 || c.head_dim % 8 || c.head_dim < 16)
-        return fail(MXH_ERR_UNSUPPORTED, "unsupported head layout");
-    if (attention_splits(n_ctx) > 64) return fail(MXH_ERR_UNSUPPORTED, "context longer than 32768 positions");
+    if (!attention_supported(c.n_head, c.n_head_kv, c.head_dim))
+        return fail(MXH_ERR_UNSUPPORTED, "unsupported head layout (head_dim 32/64/128, at most 8 q heads per kv head)");
     const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
 
     // --- place every tensor in one HBM blob ---

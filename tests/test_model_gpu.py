@@ -68,10 +68,11 @@ def test_per_layer_activations_and_logits(mxh, tmp_path, name, flags):
 
 
 @pytest.mark.parametrize("name,n_ctx,warm", [("q4k-qknorm", 600, 300), ("q5_0-gqa8", 1100, 40),
-                                             ("f32-hd128", 4000, 520)])
+                                             ("f32-hd128", 4000, 520), ("q4k-qknorm", 8200, 4150)])
 def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
-    """Contexts long enough for several attention splits per kv head (merged
-    by the last split), including positions where some splits are empty."""
+    """Contexts long enough for several attention workgroups per kv head
+    (merged by the last to finish), from one active workgroup up to 64, and
+    (8200) workgroups that take two 64-position chunks each."""
     p = build(tmp_path, name)
     gm = mxhip.Model(p, n_ctx)
     om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
