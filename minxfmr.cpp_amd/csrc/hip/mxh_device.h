@@ -153,4 +153,25 @@ __device__ __forceinline__ double wave_sum_d_all(double v) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
+// Stores and loads that are coherent across the per-XCD L2 caches by
+// themselves (agent-scope relaxed atomics, issued with sc1): data one
+// workgroup hands to another within a launch goes through these, so no
+// device-wide fence (an L2 writeback and invalidate) is needed.  Ordering
+// comes from waiting for the stores (s_waitcnt) before the atomic counter
+// that publishes them.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int add_agent(int* p, int v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait until every memory operation this thread issued has completed
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
 }  // namespace mxh

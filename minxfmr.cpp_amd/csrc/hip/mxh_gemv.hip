@@ -4,9 +4,10 @@
 // (reference op: backend_matmul_rhs_transposed with m == 1,
 // src/backend/backend_runtime.cpp:266-376).
 //
-// Work decomposition.  A row of W is cut into "chunks" of 32 elements (Q4_K:
-// 16 qs bytes covering half of two sub-blocks; Q5_K: the same plus their 16
-// qh bytes; Q8_0/Q5_0: one block; F32: 128 bytes).  Lane l of a wave64 owns
+// Work decomposition.  A row of W is cut into "chunks" (Q4_K: a 64-element
+// group of a super-block, its 32 qs bytes covering two whole sub-blocks;
+// Q5_K: 32 elements, 16 qs bytes covering half of two sub-blocks plus their
+// 16 qh bytes; Q8_0/Q5_0: one block; F32: 128 bytes).  Lane l of a wave64 owns
 // chunks l, l+64, ... of every row, so one x slice serves all R rows the
 // wave handles at a time.  x is staged in LDS once per workgroup;
 // workgroups are persistent over row groups so that staging, and the
@@ -97,8 +98,10 @@ __device__ __forceinline__ void load_block_2aligned(const uint8_t* base, size_t 
 }
 
 // ---- staged x in LDS ------------------------------------------------------
-// Quantized formats: lo/hi limb bytes (K each), per-32 scales (K/32) and
-// per-16 scaled sums s_j * sum X_i (K/16).
+// Quantized formats: lo/hi limb bytes (K each, 4 per dword, with 4 dwords of
+// padding after every 16 so that lanes reading consecutive 64-element runs
+// hit distinct banks), per-32 scales (K/32) and per-16 scaled sums
+// s_j * sum X_i (K/16).
 struct XQ {
     const uint32_t* lo;
     const uint32_t* hi;
@@ -106,13 +109,28 @@ struct XQ {
     const float* sum16;
 };
 
+// dword index of limb dword d (elements 4d..4d+3) in the padded arrays
+__device__ __forceinline__ int limb(int d) { return d + ((d >> 4) << 2); }
+__host__ __device__ constexpr int limb_dwords(int k) { return k / 4 + k / 16; }
+
 __device__ __forceinline__ XQ xq_view(const float* smem, int k) {
     const uint32_t* lo = reinterpret_cast<const uint32_t*>(smem);
-    return XQ{lo, lo + k / 4, reinterpret_cast<const float*>(lo + k / 2),
-              reinterpret_cast<const float*>(lo + k / 2) + k / 32};
+    const int n = limb_dwords(k);
+    return XQ{lo, lo + n, reinterpret_cast<const float*>(lo + 2 * n), reinterpret_cast<const float*>(lo + 2 * n) + k / 32};
 }
 
 __device__ __forceinline__ uint4 lds16(const uint32_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// s_waitcnt vmcnt(N): wait until at most N vector memory operations of this
+// wave are outstanding (they complete in issue order for loads); expcnt and
+// lgkmcnt are left alone.  Explicit waits with exact counts keep the weight
+// loads of later steps in flight where the compiler's own analysis would wait
+// for them too.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
@@ -163,38 +181,71 @@ __device__ __forceinline__ float h2f(uint32_t v) {
 // load(): raw bytes of chunk c of R rows into a register buffer.
 // compute(): add the chunk's contribution to acc[r].
 
+// Q4_K, 64-element chunks: chunk c is 64-group g = c & 3 of super-block
+// c >> 2 (32 qs bytes: low nibbles = sub-block 2g, high nibbles = 2g+1).
+// Lane l always sees the same g (= l & 3), so the 6-bit scale/min unpack
+// reduces to lane-constant masks.
 template <int R>
 struct Q4K {
     static constexpr int kType = MXH_Q4_K;
     static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 6;
+    static constexpr int kLoads = 3;  // vector loads per row per chunk
     struct Buf {
-        uint4 hd[R], qs[R];
+        uint4 hd[R], qa[R], qb[R];
     };
     static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
-        const int blk = c >> 3, p = c & 7;
+        const int blk = c >> 2, g = c & 3;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint8_t* bp = w + (size_t)rows[r] * rb + (size_t)blk * 144;
             b.hd[r] = ldg16(bp);
-            b.qs[r] = ldg16(bp + 16 + 16 * p);
+            b.qa[r] = ldg16(bp + 16 + 32 * g);
+            b.qb[r] = ldg16(bp + 32 + 32 * g);
         }
     }
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int form, float (&acc)[R]) {
-        const int blk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
-        const int e0 = 256 * blk + 64 * g + 16 * h;  // low-nibble elements e0..e0+15 (sub-block 2g)
-        const uint4 xla = lds16(x.lo + e0 / 4), xha = lds16(x.hi + e0 / 4);
-        const uint4 xlb = lds16(x.lo + e0 / 4 + 8), xhb = lds16(x.hi + e0 / 4 + 8);
-        const float sa = x.scale[e0 >> 5], sb = x.scale[(e0 >> 5) + 1];
-        const float ta = x.sum16[e0 >> 4], tb = x.sum16[(e0 >> 4) + 2];
+        const int blk = c >> 2, g = c & 3;
+        const int d0 = 64 * blk + 16 * g;  // limb dword of element e0 = 256 blk + 64 g
+        const uint4 xl0 = lds16(x.lo + limb(d0)), xl1 = lds16(x.lo + limb(d0 + 4));
+        const uint4 xl2 = lds16(x.lo + limb(d0 + 8)), xl3 = lds16(x.lo + limb(d0 + 12));
+        const uint4 xh0 = lds16(x.hi + limb(d0)), xh1 = lds16(x.hi + limb(d0 + 4));
+        const uint4 xh2 = lds16(x.hi + limb(d0 + 8)), xh3 = lds16(x.hi + limb(d0 + 12));
+        const int j0 = d0 >> 3;  // sub-block 2g of the row
+        const float sa = x.scale[j0], sb = x.scale[j0 + 1];
+        const float ta = x.sum16[2 * j0] + x.sum16[2 * j0 + 1], tb = x.sum16[2 * j0 + 2] + x.sum16[2 * j0 + 3];
+        // scale/min bytes of sub-blocks (2g, 2g+1) (tensor.cpp:395-403; ggml
+        // form for form != 0): g < 2 reads bytes 2g.. of the first two dwords,
+        // g >= 2 combines low nibbles of the third dword with top bits
+        const int sh = (g & 1) * 16;
+        const bool up = g >= 2;
+        const uint32_t mA = up ? 0u : 0x3f3fu, mC = up ? 0x0f0fu : 0u, mT = up ? 0x3030u : 0u;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float2 dd = h2f2(b.hd[r].x);  // d, dmin
-            uint32_t scp, mnp;
-            k4_pair(b.hd[r].y, b.hd[r].z, b.hd[r].w, g, form, scp, mnp);
-            const uint32_t q0 = b.qs[r].x, q1 = b.qs[r].y, q2 = b.qs[r].z, q3 = b.qs[r].w;
-            const float da = dot16(xla, xha, q0 & 0x0f0f0f0fu, q1 & 0x0f0f0f0fu, q2 & 0x0f0f0f0fu, q3 & 0x0f0f0f0fu);
-            const float db = dot16(xlb, xhb, (q0 >> 4) & 0x0f0f0f0fu, (q1 >> 4) & 0x0f0f0f0fu,
-                                   (q2 >> 4) & 0x0f0f0f0fu, (q3 >> 4) & 0x0f0f0f0fu);
+            const uint32_t A = b.hd[r].y >> sh, B = b.hd[r].z >> sh, C = b.hd[r].w >> sh;
+            const uint32_t scp = (A & mA) | (C & mC) | (((form ? A : B) >> 2) & mT);
+            const uint32_t mnp = (B & mA) | ((C >> 4) & mC) | ((B >> 2) & mT);
+            const uint4 qa = b.qa[r], qb = b.qb[r];
+            // low nibbles: elements e0..e0+31; high nibbles: e0+32..e0+63
+            int la = sdot4(xl0.x, qa.x & 0x0f0f0f0fu, 0), ha = sdot4(xh0.x, qa.x & 0x0f0f0f0fu, 0);
+            la = sdot4(xl0.y, qa.y & 0x0f0f0f0fu, la); ha = sdot4(xh0.y, qa.y & 0x0f0f0f0fu, ha);
+            la = sdot4(xl0.z, qa.z & 0x0f0f0f0fu, la); ha = sdot4(xh0.z, qa.z & 0x0f0f0f0fu, ha);
+            la = sdot4(xl0.w, qa.w & 0x0f0f0f0fu, la); ha = sdot4(xh0.w, qa.w & 0x0f0f0f0fu, ha);
+            la = sdot4(xl1.x, qb.x & 0x0f0f0f0fu, la); ha = sdot4(xh1.x, qb.x & 0x0f0f0f0fu, ha);
+            la = sdot4(xl1.y, qb.y & 0x0f0f0f0fu, la); ha = sdot4(xh1.y, qb.y & 0x0f0f0f0fu, ha);
+            la = sdot4(xl1.z, qb.z & 0x0f0f0f0fu, la); ha = sdot4(xh1.z, qb.z & 0x0f0f0f0fu, ha);
+            la = sdot4(xl1.w, qb.w & 0x0f0f0f0fu, la); ha = sdot4(xh1.w, qb.w & 0x0f0f0f0fu, ha);
+            int lb = sdot4(xl2.x, (qa.x >> 4) & 0x0f0f0f0fu, 0), hb = sdot4(xh2.x, (qa.x >> 4) & 0x0f0f0f0fu, 0);
+            lb = sdot4(xl2.y, (qa.y >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh2.y, (qa.y >> 4) & 0x0f0f0f0fu, hb);
+            lb = sdot4(xl2.z, (qa.z >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh2.z, (qa.z >> 4) & 0x0f0f0f0fu, hb);
+            lb = sdot4(xl2.w, (qa.w >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh2.w, (qa.w >> 4) & 0x0f0f0f0fu, hb);
+            lb = sdot4(xl3.x, (qb.x >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.x, (qb.x >> 4) & 0x0f0f0f0fu, hb);
+            lb = sdot4(xl3.y, (qb.y >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.y, (qb.y >> 4) & 0x0f0f0f0fu, hb);
+            lb = sdot4(xl3.z, (qb.z >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.z, (qb.z >> 4) & 0x0f0f0f0fu, hb);
+            lb = sdot4(xl3.w, (qb.w >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.w, (qb.w >> 4) & 0x0f0f0f0fu, hb);
+            // |256 h + l| <= 32 * 32512 * 15 < 2^24: exact as float
+            const float da = (float)(ha * 256 + la), db = (float)(hb * 256 + lb);
             float a = acc[r];
             a = fmaf(dd.x * (float)(scp & 0xffu) * sa, da, a);
             a = fmaf(-(dd.y * (float)(mnp & 0xffu)), ta, a);
@@ -209,6 +260,8 @@ template <int R>
 struct Q5K {
     static constexpr int kType = MXH_Q5_K;
     static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 5;
+    static constexpr int kLoads = 3;
     struct Buf {
         uint4 hd[R], qh[R], qs[R];
     };
@@ -225,8 +278,8 @@ struct Q5K {
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int form, float (&acc)[R]) {
         const int blk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
         const int e0 = 256 * blk + 64 * g + 16 * h;
-        const uint4 xla = lds16(x.lo + e0 / 4), xha = lds16(x.hi + e0 / 4);
-        const uint4 xlb = lds16(x.lo + e0 / 4 + 8), xhb = lds16(x.hi + e0 / 4 + 8);
+        const uint4 xla = lds16(x.lo + limb(e0 / 4)), xha = lds16(x.hi + limb(e0 / 4));
+        const uint4 xlb = lds16(x.lo + limb(e0 / 4 + 8)), xhb = lds16(x.hi + limb(e0 / 4 + 8));
         const float sa = x.scale[e0 >> 5], sb = x.scale[(e0 >> 5) + 1];
         const float ta = x.sum16[e0 >> 4], tb = x.sum16[(e0 >> 4) + 2];
 #pragma unroll
@@ -258,6 +311,8 @@ template <int R>
 struct Q80 {
     static constexpr int kType = MXH_Q8_0;
     static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 5;
+    static constexpr int kLoads = 10;
     struct Buf {
         uint32_t bd[R][9];
     };
@@ -267,8 +322,8 @@ struct Q80 {
     }
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        const uint4 xl0 = lds16(x.lo + e0 / 4), xh0 = lds16(x.hi + e0 / 4);
-        const uint4 xl1 = lds16(x.lo + e0 / 4 + 4), xh1 = lds16(x.hi + e0 / 4 + 4);
+        const uint4 xl0 = lds16(x.lo + limb(e0 / 4)), xh0 = lds16(x.hi + limb(e0 / 4));
+        const uint4 xl1 = lds16(x.lo + limb(e0 / 4 + 4)), xh1 = lds16(x.hi + limb(e0 / 4 + 4));
         const float s = x.scale[c];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -287,6 +342,8 @@ template <int R>
 struct Q50 {
     static constexpr int kType = MXH_Q5_0;
     static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 5;
+    static constexpr int kLoads = 7;
     struct Buf {
         uint32_t bd[R][6];
     };
@@ -296,8 +353,8 @@ struct Q50 {
     }
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        const uint4 xl0 = lds16(x.lo + e0 / 4), xh0 = lds16(x.hi + e0 / 4);
-        const uint4 xl1 = lds16(x.lo + e0 / 4 + 4), xh1 = lds16(x.hi + e0 / 4 + 4);
+        const uint4 xl0 = lds16(x.lo + limb(e0 / 4)), xh0 = lds16(x.hi + limb(e0 / 4));
+        const uint4 xl1 = lds16(x.lo + limb(e0 / 4 + 4)), xh1 = lds16(x.hi + limb(e0 / 4 + 4));
         const float s = x.scale[c];
         const float t = x.sum16[2 * c] + x.sum16[2 * c + 1];
 #pragma unroll
@@ -326,6 +383,8 @@ template <int R>
 struct F32W {
     static constexpr int kType = MXH_F32;
     static constexpr bool kIntX = false;
+    static constexpr int kChunkShift = 5;
+    static constexpr int kLoads = 8;
     struct Buf {
         f32x4 v[R][8];
     };
@@ -390,93 +449,156 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
     __syncthreads();
 }
 
-// Stage x as 16-bit block fixed point (see the file comment).  Each thread
-// handles 4 consecutive elements; the 8 threads of a 32-element sub-block
-// share its maximum through shuffles.  With a norm weight x is first
-// replaced by the reference rmsnorm, as in stage_x.
-// Stage x as 16-bit block fixed point (see the file comment).  Each thread
-// handles groups of 4 consecutive elements; the 8 threads of a 32-element
-// sub-block share its maximum through DPP.  With a norm weight x is first
-// replaced by the reference rmsnorm, as in stage_x.
-__device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
-                                         int k, float eps, double* red) {
+// Quantize 4 consecutive staged values of thread `threadIdx.x` (elements e..e+3,
+// part of a 32-element sub-block shared by 8 consecutive threads) into the
+// limb layout.  Runs with the whole wave active (DPP); `store` guards the
+// LDS writes.
+//
+// X = rint(x / s) with s = max|x| / 32512 fits 16 bits; with Y = X + 128 the
+// signed limbs of X = 256 hi + lo are hi = byte 1 of Y and lo = byte 0 of Y
+// xor 0x80, so four values pack with byte permutes.
+__device__ __forceinline__ void quantize4(float4 w4, int e, bool store, uint32_t* lo, uint32_t* hi, float* scale,
+                                          float* sum16) {
+    const float m = max8_dpp(fmaxf(fmaxf(fabsf(w4.x), fabsf(w4.y)), fmaxf(fabsf(w4.z), fabsf(w4.w))));
+    // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite);
+    // |x * is| <= 32512 (1 + 2^-22) still rounds into range
+    const bool live = m > 1e-30f;
+    const float sc = live ? m * (1.0f / 32512.0f) : 0.f;
+    const float is = live ? __builtin_amdgcn_rcpf(m) * 32512.0f : 0.f;
+    const float r0 = rintf(w4.x * is), r1 = rintf(w4.y * is), r2 = rintf(w4.z * is), r3 = rintf(w4.w * is);
+    const uint32_t y0 = (uint32_t)(int)(r0 + 128.0f), y1 = (uint32_t)(int)(r1 + 128.0f);
+    const uint32_t y2 = (uint32_t)(int)(r2 + 128.0f), y3 = (uint32_t)(int)(r3 + 128.0f);
+    const uint32_t p01 = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // y0.b0 y0.b1 y1.b0 y1.b1
+    const uint32_t p23 = __builtin_amdgcn_perm(y3, y2, 0x05040100u);
+    const uint32_t plo = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+    const uint32_t phi = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+    // sum of the 16 X of this thread's quad (exact in float)
+    float t = (r0 + r1) + (r2 + r3);
+    t += dpp_f<0xb1>(t);  // quad_perm [1,0,3,2]
+    t += dpp_f<0x4e>(t);  // quad_perm [2,3,0,1]
+    if (store) {
+        lo[limb(e >> 2)] = plo;
+        hi[limb(e >> 2)] = phi;
+        if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * t;
+        if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
+    }
+}
+
+// Stage x as 16-bit block fixed point (see the file comment).  Thread t
+// handles elements 4t + 1024u (u < NB, NB * 1024 >= k); all of its x (and
+// norm weight) loads are issued before any arithmetic, so staging costs one
+// memory latency.  With a norm weight x is first replaced by the reference
+// rmsnorm x / sqrt(mean(x^2) + eps) * w (rmsnorm.cpp:5-26,
+// transformer.cpp:189-214; float products where the reference rounds a
+// double product to float, within 1 ulp); the sum of squares is reduced in
+// double in a fixed order, so every workgroup stages identical values.
+template <int NB, bool NORM, class F>
+__device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
+                                            int k, float eps, double* red, F&& after_loads) {
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
-    uint32_t* hi = lo + k / 4;
-    float* scale = reinterpret_cast<float*>(lo + k / 2);
+    uint32_t* hi = lo + limb_dwords(k);
+    float* scale = reinterpret_cast<float*>(lo + 2 * limb_dwords(k));
     float* sum16 = scale + k / 32;
-    // x loads are issued in batches of kB per thread so their latencies
-    // overlap (the DPP steps below are convergent, which blocks automatic
-    // unrolling of a loop with a runtime trip count)
-    constexpr int kB = 4;
+    constexpr int kStep = kThreads * 4;
+    const int base = threadIdx.x * 4;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v[NB], g[NORM ? NB : 1];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int e = base + u * kStep;
+        // unconditional (clamped) loads keep the count of outstanding loads
+        // static for the explicit wait in after_loads; out-of-range values
+        // are replaced by zero only after that wait
+        const int ec = e < k ? e : k - 4;
+        v[u] = *reinterpret_cast<const float4*>(x + ec);
+        if (NORM) g[u] = *reinterpret_cast<const float4*>(nw + ec);
+    }
+    // issues the first weight steps (younger than x) and waits for x only
+    after_loads();
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+        if (base + u * kStep >= k) v[u] = z;
+    if (NORM) {
+        // per-thread float partials (at most 64 squares), summed in double
+        float sf = 0.f;
+#pragma unroll
+        for (int u = 0; u < NB; ++u)
+            sf = fmaf(v[u].x, v[u].x, fmaf(v[u].y, v[u].y, fmaf(v[u].z, v[u].z, fmaf(v[u].w, v[u].w, sf))));
+        const double ss = wave_sum_d_lane63((double)sf);
+        if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float inv = (float)(1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps));
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            v[u].x = v[u].x * inv * g[u].x;
+            v[u].y = v[u].y * inv * g[u].y;
+            v[u].z = v[u].z * inv * g[u].z;
+            v[u].w = v[u].w * inv * g[u].w;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+        if (u * kStep < k) quantize4(v[u], base + u * kStep, base + u * kStep < k, lo, hi, scale, sum16);
+    __syncthreads();
+}
+
+// Staging for K above what one thread keeps in registers (k > 12288, or
+// k > 4096 with a norm): the same values, x read again per pass.
+__device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
+                                            int k, float eps, double* red) {
+    // (the first weight steps are issued by the caller before this call)
+    uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
+    uint32_t* hi = lo + limb_dwords(k);
+    float* scale = reinterpret_cast<float*>(lo + 2 * limb_dwords(k));
+    float* sum16 = scale + k / 32;
     constexpr int kStep = kThreads * 4;
     double inv = 1.0;
     if (nw) {
         double ss = 0.0;
-        for (int base = threadIdx.x * 4; base < k; base += kB * kStep) {
-            float4 v[kB];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                const int e = base + u * kStep;
-                v[u] = e < k ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int u = 0; u < kB; ++u)
-                ss += (double)v[u].x * v[u].x + (double)v[u].y * v[u].y + (double)v[u].z * v[u].z +
-                      (double)v[u].w * v[u].w;
+        for (int e = threadIdx.x * 4; e < k; e += kStep) {
+            const float4 v = *reinterpret_cast<const float4*>(x + e);
+            ss += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
         }
         ss = wave_sum_d_lane63(ss);
         if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
         inv = 1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps);
     }
-    for (int base = threadIdx.x * 4; base < k; base += kB * kStep) {
-        float4 v[kB], g[kB];
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-            const int e = base + u * kStep;
-            const bool in = e < k;
-            v[u] = in ? *reinterpret_cast<const float4*>(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (nw) g[u] = in ? *reinterpret_cast<const float4*>(nw + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    // the trip count is uniform across the workgroup (k is a multiple of 32
+    // and every pass covers kStep elements), so the DPP runs convergent
+    for (int b = 0; b < k; b += kStep) {
+        const int e = b + threadIdx.x * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f), g = v;
+        if (e < k) v = *reinterpret_cast<const float4*>(x + e);
+        if (nw) {
+            if (e < k) g = *reinterpret_cast<const float4*>(nw + e);
+            v.x = (float)((double)v.x * inv) * g.x;
+            v.y = (float)((double)v.y * inv) * g.y;
+            v.z = (float)((double)v.z * inv) * g.z;
+            v.w = (float)((double)v.w * inv) * g.w;
         }
-#pragma unroll
-        for (int u = 0; u < kB; ++u) {
-            const int e = base + u * kStep;
-            float4 w4 = v[u];
-            if (nw) {
-                w4.x = (float)((double)w4.x * inv) * g[u].x;
-                w4.y = (float)((double)w4.y * inv) * g[u].y;
-                w4.z = (float)((double)w4.z * inv) * g[u].z;
-                w4.w = (float)((double)w4.w * inv) * g[u].w;
-            }
-            // groups of 8 threads (one sub-block) are all in or all out of range
-            const float m = max8_dpp(fmaxf(fmaxf(fabsf(w4.x), fabsf(w4.y)), fmaxf(fabsf(w4.z), fabsf(w4.w))));
-            // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite)
-            const bool live = m > 1e-30f;
-            const float sc = live ? m / 32512.0f : 0.f;
-            const float is = live ? 32512.0f / m : 0.f;
-            const float vv[4] = {w4.x, w4.y, w4.z, w4.w};
-            uint32_t plo = 0, phi = 0;
-            int sum = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int X = (int)rintf(vv[i] * is);
-                X = X > 32512 ? 32512 : (X < -32512 ? -32512 : X);
-                const int l = ((X + 128) & 255) - 128;
-                const int h = (X - l) >> 8;
-                plo |= (uint32_t)(l & 255) << (8 * i);
-                phi |= (uint32_t)(h & 255) << (8 * i);
-                sum += X;
-            }
-            sum = sum4_dpp(sum);
-            if (e < k) {
-                lo[e >> 2] = plo;
-                hi[e >> 2] = phi;
-                if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * (float)sum;
-                if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
-            }
-        }
+        quantize4(v, e, e < k, lo, hi, scale, sum16);
     }
     __syncthreads();
+}
+
+// Stage x (limb layout) and issue the first weight loads through
+// `issue_first` right after the x loads.
+template <class F>
+__device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
+                                         int k, float eps, double* red, F&& issue_first) {
+    const int nb = (k + kThreads * 4 - 1) / (kThreads * 4);
+    // register budget: the two weight buffers issued during staging stay
+    // live, so at most 48 staged registers (x, and the norm weight)
+    if (nw) {
+        if (nb <= 4) return stage_xq_nb<4, true>(smem, x, nw, k, eps, red, issue_first);
+    } else {
+        if (nb <= 4) return stage_xq_nb<4, false>(smem, x, nw, k, eps, red, issue_first);
+        if (nb <= 8) return stage_xq_nb<8, false>(smem, x, nw, k, eps, red, issue_first);
+        if (nb <= 12) return stage_xq_nb<12, false>(smem, x, nw, k, eps, red, issue_first);
+    }
+    issue_first();
+    stage_xq_2pass(smem, x, nw, k, eps, red);
 }
 
 // Output modes (epilogues) of one GEMV launch.
@@ -494,13 +616,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __shared__ float wmax[kWaves];
     __shared__ int widx[kWaves];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave index in an SGPR: every per-wave quantity below is provably
+    // uniform, so the pipeline's branches are scalar and its waits exact
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // rows a wave accumulates at once; in SILU mode rows [j] and [R/2 + j]
     // are the gate and up rows of output i0 + j
     constexpr int kOut = MODE == GEMV_SILU ? R / 2 : R;
     const int n_out = MODE == GEMV_SILU ? a.n / 2 : a.n;
     const int n_groups = (n_out + kOut - 1) / kOut;
-    const int nchunks = a.k >> 5;                // every chunk covers 32 elements
+    const int nchunks = a.k >> Ty::kChunkShift;  // chunks of 32 (64 for Q4_K) elements
     const int cpl = (nchunks + 63) >> 6;         // chunk steps per lane per row group
     const size_t rbytes = row_bytes(Ty::kType, a.k);
     const int wave_id = blockIdx.x * kWaves + wave, n_waves = gridDim.x * kWaves;
@@ -522,25 +646,41 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    auto issue = [&](Cursor& cu, Buf& b) {
-        const int grp = wave_id + cu.g * n_waves;
+    // PLAIN mode also prefetches the residual of the row group with each step
+    constexpr bool kRes = MODE == GEMV_PLAIN;
+    constexpr int kL = Ty::kLoads * R + (kRes ? kOut : 0);  // vector loads per step
+    constexpr int kL1 = kL < 63 ? kL : 63, kL2 = 2 * kL < 63 ? 2 * kL : 63;
+    const float* res_src = a.res ? a.res : a.y;  // (not used without a residual)
+    struct Step {
+        Buf b;
+        float rs[kRes ? kOut : 1];
+    };
+    // every step issues exactly kL loads (chunk and row indices clamped in
+    // bounds), so the explicit waits below can count them
+    // A step past the wave's last one repeats the last step's addresses (its
+    // loads hit lines already in flight and its data is never consumed).
+    auto issue = [&](Cursor& cu, Step& st) {
+        const bool past = cu.g >= my_groups;
+        const int gi = past ? my_groups - 1 : cu.g, ji = past ? cpl - 1 : cu.j;
+        const int grp = wave_id + gi * n_waves;
         int rows[R];
 #pragma unroll
         for (int r = 0; r < kOut; ++r) {
-            const int o = min(grp * kOut + r, n_out - 1);  // clamp loads in bounds
+            const int o = min(max(grp * kOut + r, 0), n_out - 1);
             rows[r] = o;
             if (MODE == GEMV_SILU) rows[kOut + r] = o + n_out;
+            if constexpr (kRes) st.rs[r] = res_src[o];
         }
-        const int c = lane + 64 * cu.j;
-        if (c < nchunks) Ty::load(a.w, rbytes, rows, c, b);
+        const int c = min(lane + 64 * ji, nchunks - 1);
+        Ty::load(a.w, rbytes, rows, c, st.b);
         if (++cu.j == cpl) {
             cu.j = 0;
             ++cu.g;
         }
     };
-    auto consume = [&](Cursor& cu, const Buf& b) {
+    auto consume = [&](Cursor& cu, const Step& st) {
         const int c = lane + 64 * cu.j;
-        if (c < nchunks) Ty::compute(b, c, xview, a.form, acc);
+        if (c < nchunks) Ty::compute(st.b, c, xview, a.form, acc);
         if (cu.j == cpl - 1) {
             // row group complete: reduce across lanes (total lands in lane 63) and write
             const int grp = wave_id + cu.g * n_waves;
@@ -552,11 +692,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                     const int o = grp * kOut + r;
                     if (o < n_out) {
                         float v;
-                        if (MODE == GEMV_SILU) {
+                        if constexpr (MODE == GEMV_SILU) {
                             const float gt = acc[r];
                             v = gt / (1.0f + expf(-gt)) * acc[kOut + r];
+                        } else if constexpr (kRes) {
+                            v = a.res ? acc[r] + st.rs[r] : acc[r];
                         } else {
-                            v = a.res ? acc[r] + a.res[o] : acc[r];
+                            v = acc[r];
                         }
                         a.y[o] = v;
                         if (MODE == GEMV_ARGMAX && (v > best || (v == best && o < best_i))) {
@@ -575,22 +717,51 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         }
     };
     Cursor ci{0, 0}, cc{0, 0};
-    Buf b0, b1, b2;
-    // the first two steps' weight loads do not depend on x: issue them before
-    // staging x so both latencies overlap
-    if (total > 0) issue(ci, b0);
-    if (total > 1) issue(ci, b1);
-    if constexpr (Ty::kIntX) stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red);
-    else stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
+    Step s0, s1, s2;
+    // the first two steps' weight loads do not depend on x: they are issued
+    // right after the x loads, so both latencies overlap, and the staging
+    // arithmetic waits for x only
+    auto issue_first = [&] {
+        issue(ci, s0);
+        issue(ci, s1);
+        wait_vmcnt<kL2>();
+    };
+    if constexpr (Ty::kIntX) {
+        stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
+    } else {
+        issue_first();
+        stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
+    }
+    // before consuming a step, wait until only the loads issued after it
+    // (0, 1 or 2 steps) may be outstanding
     for (int it = 0; it < total; it += 3) {
-        if (it + 2 < total) issue(ci, b2);
-        consume(cc, b0);
+        if (it + 2 < total) {
+            issue(ci, s2);
+            wait_vmcnt<kL2>();
+        } else {
+            wait_vmcnt<kL1>();  // step it + 1 (or a repeat of step it) is younger
+        }
+        consume(cc, s0);
         if (it + 1 >= total) break;
-        if (it + 3 < total) issue(ci, b0);
-        consume(cc, b1);
+        if (it + 3 < total) {
+            issue(ci, s0);
+            wait_vmcnt<kL2>();
+        } else if (it + 2 < total) {
+            wait_vmcnt<kL1>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        consume(cc, s1);
         if (it + 2 >= total) break;
-        if (it + 4 < total) issue(ci, b1);
-        consume(cc, b2);
+        if (it + 4 < total) {
+            issue(ci, s1);
+            wait_vmcnt<kL2>();
+        } else if (it + 3 < total) {
+            wait_vmcnt<kL1>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        consume(cc, s2);
     }
     if constexpr (MODE == GEMV_ARGMAX) {
         if (lane == 63) {
@@ -682,7 +853,7 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
                        : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU>
                                            : (const void*)gemv_kernel<T, R, GEMV_ARGMAX>;
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
-    const size_t lds = T<R>::kIntX ? (size_t)a.k * 2 + (size_t)(a.k / 32 + a.k / 16) * 4
+    const size_t lds = T<R>::kIntX ? (size_t)(2 * limb_dwords(a.k) + a.k / 32 + a.k / 16) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
     const int cap = grid_cap > 0 ? grid_cap : resident_grid(kern, lds);
     const unsigned grid = (unsigned)(need < cap ? need : cap);

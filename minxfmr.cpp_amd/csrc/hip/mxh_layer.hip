@@ -59,21 +59,27 @@ constexpr int kAttnMaxSplits = 64;  // workgroups per kv head (one lane each in 
 __device__ void head_prep(const float* __restrict__ src, const float* __restrict__ bias,
                           const float* __restrict__ nw, const double* __restrict__ cs, float* dst, int hd, float eps,
                           int neox) {
-    const int lane = threadIdx.x & 63;
-    float v[2] = {0.f, 0.f};  // hd <= 128: elements lane and lane + 64
+    const int lane = threadIdx.x & 63, half = hd / 2;
+    // every global input is requested before any arithmetic
+    float v[2] = {0.f, 0.f}, g[2] = {1.f, 1.f};  // hd <= 128: elements lane and lane + 64
+    double c = 1.0, s = 0.0;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int t = lane + 64 * r;
-        if (t < hd) v[r] = src[t] + (bias ? bias[t] : 0.f);
+        if (t < hd) {
+            v[r] = src[t] + (bias ? bias[t] : 0.f);
+            if (nw) g[r] = nw[t];
+        }
+    }
+    if (lane < half) {
+        c = cs[2 * lane];
+        s = cs[2 * lane + 1];
     }
     if (nw) {
         const double ss = wave_sum_d_all((double)v[0] * v[0] + (double)v[1] * v[1]);
         const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int t = lane + 64 * r;
-            if (t < hd) v[r] = (float)((double)v[r] * inv) * nw[t];
-        }
+        for (int r = 0; r < 2; ++r) v[r] = (float)((double)v[r] * inv) * g[r];
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -83,11 +89,9 @@ __device__ void head_prep(const float* __restrict__ src, const float* __restrict
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     // RoPE (rope.cpp:6-57): pair i = (2i, 2i+1), or (i, i + hd/2) for NeoX;
-    // each lane reads and rewrites only its own pair
-    const int half = hd / 2, i = lane;
-    if (i < half) {
-        const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
-        const double c = cs[2 * i], s = cs[2 * i + 1];
+    // lane i reads and rewrites only pair i
+    if (lane < half) {
+        const int ia = neox ? lane : 2 * lane, ib = neox ? lane + half : 2 * lane + 1;
         const double x0 = dst[ia], x1 = dst[ib];
         dst[ia] = (float)(x0 * c - x1 * s);
         dst[ib] = (float)(x0 * s + x1 * c);
@@ -303,26 +307,26 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         if (sact == 1) {
             a.att[qh * HD + t] = v / run_l[h];
         } else {
-            part_v[(qh * S + s) * HD + t] = v;
+            st_agent(part_v + (qh * S + s) * HD + t, v);
             if (t == 0) {
-                part_ml[(qh * S + s) * 2] = run_m[h];
-                part_ml[(qh * S + s) * 2 + 1] = run_l[h];
+                st_agent(part_ml + (qh * S + s) * 2, run_m[h]);
+                st_agent(part_ml + (qh * S + s) * 2 + 1, run_l[h]);
             }
         }
     }
     if (sact == 1) return;
 
-    // the last workgroup of kv head g to finish merges the partials
-    __threadfence();
+    // the last workgroup of kv head g to finish merges the partials; they
+    // were stored device-coherently and are complete before the count
+    wait_mem();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(a.counter + g, 1) == sact - 1;
+    if (tid == 0) last = add_agent(a.counter + g, 1) == sact - 1;
     __syncthreads();
     if (!last) return;
-    __threadfence();
     for (int h = wave; h < group; h += 4) {
         const float* ml = part_ml + ((size_t)g * group + h) * S * 2;
-        const float mi = lane < sact ? ml[2 * lane] : -INFINITY;
-        const float li = lane < sact ? ml[2 * lane + 1] : 0.f;
+        const float mi = lane < sact ? ld_agent(ml + 2 * lane) : -INFINITY;
+        const float li = lane < sact ? ld_agent(ml + 2 * lane + 1) : 0.f;
         const float M = wave_max_all(mi);
         const float wi = lane < sact ? expf(mi - M) : 0.f;
         const float den = wave_sum_all(wi * li);
@@ -335,15 +339,15 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (part < per) {
         const int h = item / (HD / 4), d4 = item % (HD / 4);
-        const float4* src = reinterpret_cast<const float4*>(part_v + ((size_t)g * group + h) * S * HD) + d4;
-#pragma unroll 8
+        const float* src = part_v + ((size_t)g * group + h) * S * HD + 4 * d4;
+#pragma unroll 4
         for (int i = part; i < sact; i += per) {
-            const float4 v = src[(size_t)i * (HD / 4)];
+            const float* q = src + (size_t)i * HD;
             const float w = wgt[h][i];
-            s4.x = fmaf(w, v.x, s4.x);
-            s4.y = fmaf(w, v.y, s4.y);
-            s4.z = fmaf(w, v.z, s4.z);
-            s4.w = fmaf(w, v.w, s4.w);
+            s4.x = fmaf(w, ld_agent(q), s4.x);
+            s4.y = fmaf(w, ld_agent(q + 1), s4.y);
+            s4.z = fmaf(w, ld_agent(q + 2), s4.z);
+            s4.w = fmaf(w, ld_agent(q + 3), s4.w);
         }
     }
     float4* r4 = reinterpret_cast<float4*>(&red[0][0][0]);  // 256 float4 fit: 4 * 8 * HD floats >= 1024
@@ -362,7 +366,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         const int h = tid / (HD / 4), d4 = tid % (HD / 4);
         reinterpret_cast<float4*>(a.att + ((size_t)g * group + h) * HD)[d4] = t4;
     }
-    if (tid == 0) a.counter[g] = 0;
+    if (tid == 0) st_agent(a.counter + g, 0);
 }
 
 // h[i] = silu(g[i]) * u[i], gu = [g | u]
