@@ -11,8 +11,10 @@ through the whole device-resident stack plus the lm-head and argmax.
 
 One JSON line is printed.  `value` is decode tokens/s; `roofline` is for the
 dominant kernel, the Q4_K dequant-GEMV, timed with HIP events over every
-Q4_K GEMV of the model on its own HBM-resident weights; `cpu_baseline` is the
-CPU oracle decoding a bounded sample of the same model on the host cores.
+Q4_K GEMV of the model on its own HBM-resident weights (`traffic` is the
+HBM bytes per launch that rocprofv3 counters measured for the same shapes,
+profiles/gemv_q4k_traffic.json); `cpu_baseline` is the CPU oracle decoding a
+bounded sample of the same model on the host cores.
 """
 from __future__ import annotations
 
@@ -77,6 +79,20 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
     return {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} greedy decode steps (positions 0..{n - 1}, lm-head included) of the same model "
                       f"by the C oracle with {threads} OpenMP threads, {el:.1f}s"}
+
+
+def measured_traffic(per_launch_bytes: int):
+    """HBM bytes per Q4_K GEMV launch from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE measurement of the same shapes (None if absent or
+    for other shapes)."""
+    p = ROOT / "profiles" / "gemv_q4k_traffic.json"
+    try:
+        d = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    if int(d.get("per_launch_algorithmic_bytes", -1)) != int(per_launch_bytes):
+        return None
+    return int(d["traffic_per_launch_bytes"])
 
 
 def main() -> int:
@@ -155,7 +171,7 @@ def main() -> int:
         "decode_hbm_frac": round(step_bytes / (wall_s / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
         "prefill_tok_s": round(args.prompt / (prefill_ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(g_bytes_launch),
                      "kernel": "Q4_K dequant-GEMV (gemv_kernel<Q4K>)",
                      "per_launch_bytes": int(g_bytes_launch), "avg_launch_us": round(g_avg_us, 3)},
     }

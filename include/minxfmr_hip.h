@@ -78,6 +78,7 @@ int mxh_free(void *dptr);
 int mxh_upload(void *dst, const void *src, size_t bytes);   /* synchronous */
 int mxh_download(void *dst, const void *src, size_t bytes); /* synchronous */
 int mxh_memset(void *dptr, int value, size_t bytes);        /* async */
+int mxh_copy(void *dst, const void *src, size_t bytes);      /* device to device, async */
 
 /* Elapsed time of the work enqueued between begin and end, measured with
  * events on the library stream.  mxh_timer_end synchronizes. */

@@ -179,6 +179,12 @@ int mxh_memset(void* dptr, int value, size_t bytes) {
     return check_hip(hipMemsetAsync(dptr, value, bytes, g_ctx.stream), "memset");
 }
 
+int mxh_copy(void* dst, const void* src, size_t bytes) {
+    if (int rc = ensure_ready()) return rc;
+    if (!dst || !src) return set_error(MXH_ERR_ARG, "copy: null pointer");
+    return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx.stream), "copy");
+}
+
 int mxh_timer_begin(void) {
     if (int rc = ensure_ready()) return rc;
     return check_hip(hipEventRecord(g_ctx.ev0, g_ctx.stream), "hipEventRecord");

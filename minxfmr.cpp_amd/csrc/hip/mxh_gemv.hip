@@ -39,6 +39,14 @@ namespace {
 constexpr int kWaves = 4;  // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 
+// sum of the per-wave partials in a fixed order
+__device__ __forceinline__ double block_sum(const double* red) {
+    double s = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; w += 2) s += red[w] + red[w + 1];
+    return s;
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -435,7 +443,7 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    const double inv = 1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps);
+    const double inv = 1.0 / sqrt(block_sum(red) / (double)k + (double)eps);
     // each thread rescales the elements it staged
     for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
         float4 v = *reinterpret_cast<const float4*>(xs + xpad(e));
@@ -527,7 +535,7 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict
         const double ss = wave_sum_d_lane63((double)sf);
         if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
-        const float inv = (float)(1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps));
+        const float inv = (float)(1.0 / sqrt(block_sum(red) / (double)k + (double)eps));
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             v[u].x = v[u].x * inv * g[u].x;
@@ -562,7 +570,7 @@ __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict
         ss = wave_sum_d_lane63(ss);
         if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
-        inv = 1.0 / sqrt((((red[0] + red[1]) + (red[2] + red[3]))) / (double)k + (double)eps);
+        inv = 1.0 / sqrt(block_sum(red) / (double)k + (double)eps);
     }
     // the trip count is uniform across the workgroup (k is a multiple of 32
     // and every pass covers kStep elements), so the DPP runs convergent

@@ -423,7 +423,9 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     if (!rc) rc = dalloc(&m->trace, (size_t)(c.n_layer + 1) * c.n_embd);
     if (!rc) rc = dalloc(&m->tokens, (size_t)n_ctx + 1);
     if (!rc) rc = dalloc(&m->pos, 1);
-    m->red_cap = c.n_vocab / 4 + 2;  // >= workgroups of the head GEMV (>= 4 rows each)
+    // >= workgroups of the head GEMV: at most one per row group (>= 2 rows)
+    // and never more than the resident grid
+    m->red_cap = c.n_vocab / 2 + 2 < 8192 ? c.n_vocab / 2 + 2 : 8192;
     if (!rc) rc = dalloc(&m->red_val, (size_t)m->red_cap);
     if (!rc) rc = dalloc(&m->red_idx, (size_t)m->red_cap);
     if (!rc) rc = dalloc(&m->counters, (size_t)c.n_head_kv + 1);

@@ -69,6 +69,7 @@ def _load() -> C.CDLL:
         "mxh_upload": (ip, [vp, vp, sz]),
         "mxh_download": (ip, [vp, vp, sz]),
         "mxh_memset": (ip, [vp, ip, sz]),
+        "mxh_copy": (ip, [vp, vp, sz]),
         "mxh_timer_begin": (ip, []),
         "mxh_timer_end": (ip, [fp]),
         "mxh_gemv": (ip, [ip, vp, vp, vp, i64, i64, ip]),
@@ -103,7 +104,7 @@ def _load() -> C.CDLL:
 lib = _load()
 EXPORTED = (
     "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
-    "mxh_download mxh_memset mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
+    "mxh_download mxh_memset mxh_copy mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_generate mxh_model_close "
@@ -181,6 +182,16 @@ def gemv(type_: int, w: DeviceBuffer | int, x: DeviceBuffer | int, y: DeviceBuff
          form: int = FORM_REF) -> None:
     addr = lambda b: b.ptr if isinstance(b, DeviceBuffer) else int(b)
     check(lib.mxh_gemv(type_, addr(w), addr(x), addr(y), n, k, form), "mxh_gemv")
+
+
+def memset(buf: DeviceBuffer, value: int) -> None:
+    check(lib.mxh_memset(buf.ptr, value, buf.nbytes), "mxh_memset")
+
+
+def copy(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+    """Device-to-device copy on the library stream (asynchronous)."""
+    assert nbytes <= dst.nbytes and nbytes <= src.nbytes
+    check(lib.mxh_copy(dst.ptr, src.ptr, nbytes), "mxh_copy")
 
 
 def dequant(type_: int, w: DeviceBuffer, rows: int, cols: int, form: int = FORM_REF) -> np.ndarray:

@@ -1,0 +1,175 @@
+"""Workloads to run under rocprofv3 and summaries of what it writes.
+
+    # HBM traffic of the Q4_K dequant-GEMV at the Qwen3-8B decode shapes,
+    # calibrated against a plain device-to-device copy of known size
+    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- \
+        python3 -m mxhip.profiling workload
+    rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- \
+        python3 -m mxhip.profiling workload
+    python3 -m mxhip.profiling traffic OUT/fetch OUT/write > summary.md
+
+    # per-kernel time table from a --kernel-trace --stats run
+    python3 -m mxhip.profiling stats OUT/trace/run_kernel_stats.csv
+
+The workload launches each shape `reps` times over rotating weight copies
+(more than the 256 MB Infinity Cache in total) and copies 256 MiB once per
+rep.  FETCH_SIZE and WRITE_SIZE are reported by rocprofv3 in KiB per
+dispatch; the calibration factor is the copy's known byte count divided by
+what the counter reads for it.
+"""
+from __future__ import annotations
+
+import csv
+import glob
+import os
+import re
+import sys
+from pathlib import Path
+
+# Q4_K GEMV shapes of one Qwen3-8B layer (out x in): fused q|k|v, o,
+# fused gate|up, down
+SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288)]
+COPY_BYTES = 256 << 20
+
+
+def algorithmic_bytes(n: int, k: int) -> int:
+    """Q4_K GEMV: N*K/256*144 weight bytes + 4K (x) + 4N (y)."""
+    return n * k // 256 * 144 + 4 * k + 4 * n
+
+
+def workload(reps: int = 20) -> None:
+    import numpy as np
+
+    import mxhip
+
+    mxhip.init(0)
+    rng = np.random.default_rng(1)
+    src = mxhip.DeviceBuffer(COPY_BYTES)
+    dst = mxhip.DeviceBuffer(COPY_BYTES)
+    mxhip.memset(src, 1)
+    for name, n, k in SHAPES:
+        wbytes = mxhip.row_bytes(mxhip.Q4_K, k) * n
+        copies = max(2, (768 << 20) // wbytes)
+        raw = rng.integers(0, 256, wbytes, dtype=np.uint8)
+        raw.reshape(-1, 144)[:, 0:4] = np.frombuffer(np.array([0.01, 0.01], np.float16).tobytes(), np.uint8)
+        bufs = []
+        for _ in range(copies):
+            b = mxhip.DeviceBuffer(wbytes)
+            b.upload(raw)
+            bufs.append(b)
+        x = mxhip.DeviceBuffer.from_array(rng.standard_normal(k, dtype=np.float32))
+        y = mxhip.DeviceBuffer(4 * n)
+        for i in range(reps):
+            mxhip.gemv(mxhip.Q4_K, bufs[i % copies], x, y, n, k)
+        mxhip.synchronize()
+        for b in bufs:
+            b.close()
+        print(f"[workload] {name} {n}x{k}: {reps} launches", file=sys.stderr, flush=True)
+    for _ in range(reps):
+        mxhip.copy(dst, src, COPY_BYTES)
+    mxhip.synchronize()
+    print(f"[workload] copy {COPY_BYTES} B x {reps}", file=sys.stderr, flush=True)
+
+
+def _counter_rows(d: str):
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _per_dispatch(rows, counter: str):
+    """{kernel name: [value per dispatch]} for one counter (summed over
+    the per-instance rows rocprofv3 may write for a dispatch)."""
+    acc: dict[tuple[str, str], float] = {}
+    for r in rows:
+        if r.get("Counter_Name") != counter:
+            continue
+        key = (r["Dispatch_Id"], r["Kernel_Name"])
+        acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+    out: dict[str, list[float]] = {}
+    for (did, name), v in sorted(acc.items(), key=lambda kv: int(kv[0][0])):
+        out.setdefault(name, []).append(v)
+    return out
+
+
+def traffic(fetch_dir: str, write_dir: str) -> None:
+    fetch = _per_dispatch(_counter_rows(fetch_dir), "FETCH_SIZE")
+    write = _per_dispatch(_counter_rows(write_dir), "WRITE_SIZE")
+    copy_name = next((n for n in fetch if "copy" in n.lower()), None)
+    if copy_name is None:
+        raise SystemExit("no copy dispatch found")
+    kib = COPY_BYTES / 1024
+    f_cal = kib / (sum(fetch[copy_name]) / len(fetch[copy_name]))
+    w_cal = kib / (sum(write[copy_name]) / len(write[copy_name]))
+    gemv = [n for n in fetch if "gemv_kernel" in n and "Q4K" in n]
+    if len(gemv) != 1:
+        raise SystemExit(f"expected one Q4_K GEMV kernel, found {gemv}")
+    fv, wv = fetch[gemv[0]], write[gemv[0]]
+    reps = len(fv) // len(SHAPES)
+    print("| shape (N x K) | algorithmic B | FETCH (scaled) B | WRITE (scaled) B | traffic / algorithmic |")
+    print("|---|---:|---:|---:|---:|")
+    tot_alg = tot_traffic = 0.0
+    for i, (name, n, k) in enumerate(SHAPES):
+        # skip each shape's first launch (cold instruction and TLB state)
+        fs = fv[i * reps + 1:(i + 1) * reps]
+        ws = wv[i * reps + 1:(i + 1) * reps]
+        fb = sum(fs) / len(fs) * 1024 * f_cal
+        wb = sum(ws) / len(ws) * 1024 * w_cal
+        alg = algorithmic_bytes(n, k)
+        tot_alg += alg
+        tot_traffic += fb + wb
+        print(f"| {name} {n} x {k} | {alg:,} | {fb:,.0f} | {wb:,.0f} | {(fb + wb) / alg:.3f} |")
+    print(f"| mean per launch | {tot_alg / len(SHAPES):,.0f} | | | {tot_traffic / tot_alg:.3f} |")
+    print()
+    print(f"Calibration: a {COPY_BYTES:,} B device-to-device copy reads FETCH_SIZE "
+          f"{sum(fetch[copy_name]) / len(fetch[copy_name]):,.0f} KiB and WRITE_SIZE "
+          f"{sum(write[copy_name]) / len(write[copy_name]):,.0f} KiB per dispatch; factors "
+          f"{f_cal:.4f} (fetch) and {w_cal:.4f} (write) are applied above.")
+    print(f"TRAFFIC_PER_LAUNCH_BYTES={tot_traffic / len(SHAPES):.0f}")
+
+
+def stats(path: str, top: int = 15) -> None:
+    with open(path, newline="") as fh:
+        rows = list(csv.DictReader(fh))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    print("| kernel | calls | avg us | total ms | share |")
+    print("|---|---:|---:|---:|---:|")
+    for r in rows[:top]:
+        name = r["Name"].replace("mxh::(anonymous namespace)::", "").replace("mxh::", "").replace("void ", "")
+        name = re.sub(r"\([^()]*\)$", "", name)  # argument list
+        print(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+              f"{float(r['TotalDurationNs']) / 1e6:.2f} | {100 * float(r['TotalDurationNs']) / tot:.1f}% |")
+    q = [r for r in rows if "gemv_kernel" in r["Name"] and "Q4K" in r["Name"]]
+    if q:
+        calls = sum(int(r["Calls"]) for r in q)
+        print()
+        print(f"All Q4_K GEMV dispatches (every epilogue): {calls} calls, average "
+              f"{sum(float(r['TotalDurationNs']) for r in q) / calls / 1e3:.2f} us")
+
+
+def main(argv: list[str]) -> int:
+    if not argv:
+        print(__doc__)
+        return 2
+    cmd = argv[0]
+    if cmd == "workload":
+        workload(int(argv[1]) if len(argv) > 1 else 20)
+    elif cmd == "traffic":
+        traffic(argv[1], argv[2])
+    elif cmd == "stats":
+        stats(argv[1])
+    else:
+        print(__doc__)
+        return 2
+    return 0
+
+
+if __name__ == "__main__":
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent))
+    sys.exit(main(sys.argv[1:]))
