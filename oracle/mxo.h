@@ -11,6 +11,18 @@
  * Every function cites the reference file:line it restates.  Where the
  * reference has no counterpart (Q5_K, Qwen3 QK-norm, seeded sampling) the
  * comment says so and names the published algorithm followed instead.
+ *
+ * Pins (tests/test_oracle_pins.py, tests/test_oracle_layer.py): fp16 decode,
+ * Q4_K/Q8_0/Q5_0 dequant, matmul_rhs_t, rmsnorm, rope, softmax and the layer
+ * stack are checked against the reference's own KATs, vectors from the
+ * reference source compiled under oracle/_ref, closed forms and brute force.
+ * Not pinned against the reference:
+ *   - mxo_dequant_q5k_block: parity unpinned (no reference Q5_K); checked by
+ *     its exact reduction to Q4_K with a zero high-bit plane and round trips;
+ *   - QK-norm placement in the model step: parity unpinned (Qwen3 order:
+ *     after the q/k projections, before RoPE; the norm itself is pinned);
+ *   - mxo_sample's random draw: parity unpinned (the reference draws from an
+ *     unseeded mt19937); the greedy limit and determinism are checked.
  */
 #ifndef MXO_H
 #define MXO_H
