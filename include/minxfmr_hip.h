@@ -104,6 +104,14 @@ int mxh_matmul_rhs_t(int type, const float *a, int64_t m, const void *w, int64_t
  * (src/backend/cuda/cuda_backend.cu:583-674, cuda_backend_compare_dequant). */
 int mxh_dequant(int type, const void *w, float *out, int64_t rows, int64_t cols, int form);
 
+/* out[m x n] = bf16(a[m x k]) . bf16(dequant(w[n x k]))^T with fp32
+ * accumulation on the matrix cores (v_mfma_f32_32x32x16_bf16); device
+ * pointers, k a multiple of 64.  The prefill contraction: the reference runs
+ * it as backend_matmul_rhs_transposed with m > 1
+ * (src/backend/backend_runtime.cpp:302-319); this entry trades its fp32
+ * inputs for bf16 ones. */
+int mxh_gemm_q_bf16(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out, int form);
+
 /* ---- per-op backend interface (host pointers) ------------------------- */
 /* These keep the reference op semantics for drop-in use: host pointers in
  * and out, one synchronous device round trip per call.  Quantized weights
@@ -161,7 +169,9 @@ enum {
     MXH_MODEL_ROPE_NEOX = 1,    /* (i, i + rot/2) pairs; default (2i, 2i+1) as rope.cpp:39-45 */
     MXH_MODEL_GGML_FORM = 4,    /* ggml Q4_K/Q5_K scale unpacking instead of the reference CPU form */
     MXH_MODEL_NO_QK_NORM = 8,   /* ignore attn_{q,k}_norm (reference layer semantics) */
-    MXH_MODEL_NO_GRAPH = 16     /* enqueue kernels directly instead of replaying HIP graphs */
+    MXH_MODEL_NO_GRAPH = 16,    /* enqueue kernels directly instead of replaying HIP graphs */
+    MXH_MODEL_TOKEN_PREFILL = 32 /* prompt token by token through the decode step (fp32 GEMVs) instead of
+                                    batched on the matrix cores (bf16 GEMM inputs) */
 };
 
 /* Load a GGUF file into HBM with room for n_ctx positions.
@@ -174,6 +184,12 @@ int mxh_model_position(const mxh_model *m);
 /* Run `token` at the current position and advance.  logits (n_vocab floats)
  * and trace ((n_layer + 1) * n_embd floats: hidden after each layer, then the
  * final-normed hidden) are host buffers and may be NULL.  Synchronous. */
+/* Feed n prompt tokens at the current position without producing logits:
+ * batched on the matrix cores in chunks of up to 512 tokens (dequant-to-bf16
+ * MFMA GEMMs, row-batched QK-norm/RoPE/KV append and causal attention),
+ * unless the model was opened with MXH_MODEL_TOKEN_PREFILL.  Replaces the
+ * reference's token-by-token prompt loop (src/api/minxfmr.cpp:1503-1548). */
+int mxh_model_prefill(mxh_model *m, const int *tokens, int n);
 int mxh_model_step(mxh_model *m, int token, float *logits, float *trace);
 /* Greedy generation from position 0: prefill n_prompt ids, then n_gen
  * decode steps; out receives n_gen ids.  prefill_ms / decode_ms (nullable)

@@ -224,6 +224,24 @@ int mxh_dequant(int type, const void* w, float* out, int64_t rows, int64_t cols,
     return check_hip(hipGetLastError(), "dequant launch");
 }
 
+int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k, float* out, int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (!a || !w || !out) return set_error(MXH_ERR_ARG, "gemm: null pointer");
+    if (m <= 0 || n <= 0 || k <= 0 || k % 64 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX ||
+        row_bytes(type, k) == 0)
+        return set_error(MXH_ERR_ARG, "gemm: bad shape %lldx%lldx%lld for type %d", (long long)m, (long long)n,
+                         (long long)k, type);
+    void* abf = nullptr;
+    if (int rc = stage(3, (size_t)m * (size_t)k * 2, &abf)) return rc;
+    if (int rc = rows_to_bf16_launch(a, (int)k, nullptr, 0.f, (int)k, (uint16_t*)abf, nullptr, (int)k, (int)m,
+                                     g_ctx.stream))
+        return set_error(rc, "gemm: conversion launch");
+    if (int rc = gemm_bf16_run(type, (const uint16_t*)abf, nullptr, (int)k, w, out, (int)n, nullptr, (int)m, (int)n,
+                               (int)k, form, g_ctx.stream))
+        return set_error(rc, "gemm: unsupported type %d", type);
+    return check_hip(hipGetLastError(), "gemm launch");
+}
+
 int mxh_preload(const void* host, size_t bytes) {
     if (int rc = ensure_ready()) return rc;
     if (!host || !bytes) return set_error(MXH_ERR_ARG, "preload: empty tensor");

@@ -77,4 +77,20 @@ int embed_launch(int type, const void* w, const int* tokens, const int* pos, flo
 int argmax_launch(const float* logits, int n, int* tokens, const int* pos, hipStream_t st);
 int add_int_launch(int* p, int v, hipStream_t st);
 
+// Batched prefill (mxh_prefill.hip): dequant-to-bf16 MFMA GEMM
+// out[m x n] (row stride ldo) = a[m x k] (bf16, row stride lda) . W[n x k]^T (+ res);
+// with a_lo (the bf16 residual of a) the split three-product form
+int gemm_bf16_run(int type, const uint16_t* a, const uint16_t* a_lo, int lda, const void* w, float* out, int ldo,
+                  const float* res, int m, int n, int k, int form, hipStream_t st);
+int rows_to_bf16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a, uint16_t* a_lo,
+                        int lda, int m, hipStream_t st);
+int silu_mul_bf16_launch(const float* gu, int f, uint16_t* h, uint16_t* h_lo, int m, hipStream_t st);
+int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,
+                         const double* rope_cs, int p0, int m, float* q_out, __half* kc, __half* vc, int nh, int nkv,
+                         int hd, int neox, float eps, hipStream_t st);
+int attention_rows_launch(const float* q, const __half* kc, const __half* vc, float* att, int p0, int m, int nh,
+                          int nkv, int hd, float scale, hipStream_t st);
+int embed_rows_launch(int type, const void* w, const int* tokens, int p0, int m, float* x, int cols, int form,
+                      hipStream_t st);
+
 }  // namespace mxh

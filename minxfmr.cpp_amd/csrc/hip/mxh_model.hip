@@ -64,7 +64,12 @@ struct mxh_model {
     int* pos = nullptr;     // current position
     int host_pos = 0;
     bool trace_on = false;
+    bool token_prefill = false;  // prompt token by token instead of batched
     hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
+    // batched prefill (allocated on first use): rows of up to pf_rows tokens
+    int pf_rows = 0;
+    float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_gu = nullptr;
+    uint16_t *pf_a = nullptr, *pf_a_lo = nullptr;  // GEMM input as split bf16 (hi, lo)
 };
 
 namespace {
@@ -182,7 +187,8 @@ int free_model(mxh_model* m) {
     if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
-                    m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters};
+                    m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
+                    m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -437,6 +443,7 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
         free_model(m);
         return rc;
     }
+    m->token_prefill = (flags & MXH_MODEL_TOKEN_PREFILL) != 0;
     if (!(flags & MXH_MODEL_NO_GRAPH)) {
         if ((rc = capture(m, false, &m->g_prefill)) || (rc = capture(m, true, &m->g_decode))) {
             free_model(m);
@@ -494,6 +501,111 @@ int mxh_model_step(mxh_model* m, int token, float* logits, float* trace) {
     return check_hip(hipStreamSynchronize(st), "step");
 }
 
+namespace {
+
+constexpr int kPrefillRows = 512;  // tokens per batched prefill chunk
+
+int ensure_prefill_buffers(mxh_model* m) {
+    if (m->pf_rows) return MXH_OK;
+    const mxh_model_config& c = m->cfg;
+    const int rows = std::min(kPrefillRows, c.n_ctx);
+    const size_t qd = (size_t)c.n_head * c.head_dim, kvd = (size_t)c.n_head_kv * c.head_dim;
+    const size_t widest = std::max(std::max((size_t)c.n_embd, qd), (size_t)c.n_ff);
+    int rc = dalloc(&m->pf_x, (size_t)rows * c.n_embd);
+    if (!rc) rc = dalloc(&m->pf_qkv, (size_t)rows * (qd + 2 * kvd));
+    if (!rc) rc = dalloc(&m->pf_q, (size_t)rows * qd);
+    if (!rc) rc = dalloc(&m->pf_att, (size_t)rows * qd);
+    if (!rc) rc = dalloc(&m->pf_gu, (size_t)rows * 2 * c.n_ff);
+    if (!rc) rc = dalloc(&m->pf_a, (size_t)rows * widest);
+    if (!rc) rc = dalloc(&m->pf_a_lo, (size_t)rows * widest);
+    if (!rc) m->pf_rows = rows;
+    return rc;
+}
+
+// split-bf16 GEMM over the prefill input buffers (pf_a, pf_a_lo)
+int gemm(mxh_model* m, const DevW& w, int lda, float* out, int ldo, const float* res, int rows, hipStream_t st) {
+    return gemm_bf16_run(w.type, m->pf_a, m->pf_a_lo, lda, w.p, out, ldo, res, rows, (int)w.rows, (int)w.cols,
+                         m->form, st);
+}
+
+// Prompt tokens tokens[p0 .. p0+rows) through every layer at once, the
+// projections on the matrix cores (split-bf16 inputs, fp32 accumulation); the K/V
+// rows land in the cache and the position advances by `rows`.  No head: the
+// last prompt token runs through the decode step for its logits.
+int enqueue_prefill_chunk(mxh_model* m, int p0, int rows, hipStream_t st) {
+    const mxh_model_config& c = m->cfg;
+    const int d = c.n_embd, hd = c.head_dim, nh = c.n_head, nkv = c.n_head_kv, f = c.n_ff;
+    const int qd = nh * hd, kvd = nkv * hd, ldq = qd + 2 * kvd;
+    int rc = embed_rows_launch(m->embd.type, m->embd.p, m->tokens, p0, rows, m->pf_x, d, m->form, st);
+    for (int l = 0; l < c.n_layer && !rc; ++l) {
+        const Layer& L = m->layers[(size_t)l];
+        rc |= rows_to_bf16_launch(m->pf_x, d, L.attn_norm, c.eps, d, m->pf_a, m->pf_a_lo, d, rows, st);
+        if (L.qkv_fused) {
+            rc |= gemm(m, L.qkv, d, m->pf_qkv, ldq, nullptr, rows, st);
+        } else {
+            rc |= gemm(m, L.q, d, m->pf_qkv, ldq, nullptr, rows, st);
+            rc |= gemm(m, L.k, d, m->pf_qkv + qd, ldq, nullptr, rows, st);
+            rc |= gemm(m, L.v, d, m->pf_qkv + qd + kvd, ldq, nullptr, rows, st);
+        }
+        rc |= qkv_prep_rows_launch(m->pf_qkv, ldq, L.bias, L.q_norm, L.k_norm, m->rope_cs, p0, rows, m->pf_q, L.kc,
+                                   L.vc, nh, nkv, hd, m->neox, c.eps, st);
+        rc |= attention_rows_launch(m->pf_q, L.kc, L.vc, m->pf_att, p0, rows, nh, nkv, hd, 1.0f / sqrtf((float)hd), st);
+        rc |= rows_to_bf16_launch(m->pf_att, qd, nullptr, 0.f, qd, m->pf_a, m->pf_a_lo, qd, rows, st);
+        rc |= gemm(m, L.o, qd, m->pf_x, d, m->pf_x, rows, st);
+        rc |= rows_to_bf16_launch(m->pf_x, d, L.ffn_norm, c.eps, d, m->pf_a, m->pf_a_lo, d, rows, st);
+        if (L.gu_fused) {
+            rc |= gemm(m, L.gu, d, m->pf_gu, 2 * f, nullptr, rows, st);
+        } else {
+            rc |= gemm(m, L.g, d, m->pf_gu, 2 * f, nullptr, rows, st);
+            rc |= gemm(m, L.u, d, m->pf_gu + f, 2 * f, nullptr, rows, st);
+        }
+        rc |= silu_mul_bf16_launch(m->pf_gu, f, m->pf_a, m->pf_a_lo, rows, st);
+        rc |= gemm(m, L.down, f, m->pf_x, d, m->pf_x, rows, st);
+    }
+    if (!rc) rc = add_int_launch(m->pos, rows, st);
+    return rc ? set_error(MXH_ERR_HIP, "prefill enqueue failed") : MXH_OK;
+}
+
+// tokens[host_pos .. host_pos + n) (already on the device) in chunks
+int run_prefill(mxh_model* m, int n) {
+    if (n <= 0) return MXH_OK;
+    if (int rc = ensure_prefill_buffers(m)) return rc;
+    hipStream_t st = lib_stream();
+    for (int done = 0; done < n;) {
+        const int rows = std::min(m->pf_rows, n - done);
+        if (int rc = enqueue_prefill_chunk(m, m->host_pos + done, rows, st)) return rc;
+        done += rows;
+    }
+    return MXH_OK;
+}
+
+bool batched_prefill_supported(const mxh_model* m) {
+    const mxh_model_config& c = m->cfg;
+    return !m->token_prefill && c.n_embd % 64 == 0 && c.n_ff % 64 == 0 && (c.n_head * c.head_dim) % 64 == 0;
+}
+
+}  // namespace
+
+int mxh_model_prefill(mxh_model* m, const int* tokens, int n) {
+    if (!m || (!tokens && n > 0) || n < 0) return set_error(MXH_ERR_ARG, "prefill: bad arguments");
+    if (m->host_pos + n > m->cfg.n_ctx)
+        return set_error(MXH_ERR_ARG, "prefill: position %d + %d exceeds the context of %d", m->host_pos, n, m->cfg.n_ctx);
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m->embd.rows) return set_error(MXH_ERR_ARG, "prefill: id %d out of range", tokens[i]);
+    if (n == 0) return MXH_OK;
+    hipStream_t st = lib_stream();
+    int rc = check_hip(hipMemcpyAsync(m->tokens + m->host_pos, tokens, sizeof(int) * n, hipMemcpyHostToDevice, st),
+                       "prefill ids");
+    if (!rc) {
+        if (batched_prefill_supported(m)) rc = run_prefill(m, n);
+        else
+            for (int i = 0; i < n && !rc; ++i) rc = run_step(m, false);
+    }
+    if (!rc) rc = check_hip(hipStreamSynchronize(st), "prefill");
+    if (!rc) m->host_pos += n;
+    return rc;
+}
+
 int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen, int* out, float* prefill_ms,
                        float* decode_ms) {
     if (!m || !prompt || n_prompt <= 0 || n_gen <= 0 || !out) return set_error(MXH_ERR_ARG, "generate: bad arguments");
@@ -509,9 +621,12 @@ int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen,
     (void)hipEventCreate(&e2);
     int rc = check_hip(hipMemcpyAsync(m->tokens, prompt, sizeof(int) * n_prompt, hipMemcpyHostToDevice, st), "prompt");
     if (!rc) rc = check_hip(hipEventRecord(e0, st), "event");
-    // prompt positions 0 .. n_prompt-2 need no logits; the last prompt token
-    // runs with the head and yields the first generated id (minxfmr.cpp:1860)
-    for (int i = 0; i < n_prompt - 1 && !rc; ++i) rc = run_step(m, false);
+    // prompt positions 0 .. n_prompt-2 need no logits (batched on the
+    // matrix cores, or token by token); the last prompt token runs with the
+    // head and yields the first generated id (minxfmr.cpp:1860)
+    if (!rc && batched_prefill_supported(m)) rc = run_prefill(m, n_prompt - 1);
+    else
+        for (int i = 0; i < n_prompt - 1 && !rc; ++i) rc = run_step(m, false);
     if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
     for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true);
     if (!rc) rc = check_hip(hipEventRecord(e2, st), "event");

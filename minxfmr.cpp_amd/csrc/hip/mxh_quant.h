@@ -1,0 +1,82 @@
+// mxh_quant.h — device decode of one 32-element run of a GGUF row.
+//
+// Bit-exact with the reference CPU decoders (src/tensor/tensor.cpp:405-457):
+// every product is exact in fp32 (fp16 d x 6-bit scale x 4/5-bit code needs at
+// most 22 significant bits), so only the final subtraction rounds and fused
+// or separate multiply-add give the same bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mxh_device.h"
+
+namespace mxh {
+
+__device__ __forceinline__ uint32_t rd_u8(const uint8_t* p) { return *p; }
+__device__ __forceinline__ uint32_t rd_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+// y[0..31] = elements 32*run .. 32*run+31 of the row starting at rp
+template <int TYPE>
+__device__ __forceinline__ void dequant_run32(const uint8_t* __restrict__ rp, int64_t run, int form, float* y) {
+    if constexpr (TYPE == MXH_Q4_K || TYPE == MXH_Q5_K) {
+        constexpr int BB = TYPE == MXH_Q4_K ? 144 : 176;
+        const int64_t b = run >> 3;
+        const int j = (int)(run & 7);  // sub-block: elements 32j..32j+31
+        const uint8_t* blk = rp + (size_t)b * BB;
+        const float d = half_bits_to_float(rd_u16(blk));
+        const float dm = half_bits_to_float(rd_u16(blk + 2));
+        const uint32_t s0 = rd_u16(blk + 4) | (rd_u16(blk + 6) << 16);
+        const uint32_t s1 = rd_u16(blk + 8) | (rd_u16(blk + 10) << 16);
+        const uint32_t s2 = rd_u16(blk + 12) | (rd_u16(blk + 14) << 16);
+        uint32_t sc, mn;
+        k4_scale_min(s0, s1, s2, j, form, sc, mn);
+        const float ds = d * (float)sc, ms = dm * (float)mn;
+        const int g = j >> 1, hi = j & 1;
+        const uint8_t* qs = blk + (TYPE == MXH_Q4_K ? 16 : 48) + 32 * g;
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) {
+            uint32_t q = rd_u8(qs + i);
+            q = hi ? (q >> 4) : (q & 15u);
+            if constexpr (TYPE == MXH_Q5_K) q |= ((rd_u8(blk + 16 + i) >> j) & 1u) << 4;
+            y[i] = ds * (float)q - ms;
+        }
+    } else if constexpr (TYPE == MXH_Q8_0) {
+        const uint8_t* blk = rp + (size_t)run * 34;
+        const float d = half_bits_to_float(rd_u16(blk));
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) y[i] = d * (float)(int)(int8_t)blk[2 + i];
+    } else if constexpr (TYPE == MXH_Q5_0) {
+        const uint8_t* blk = rp + (size_t)run * 22;
+        const float d = half_bits_to_float(rd_u16(blk));
+        const uint32_t qh = rd_u16(blk + 2) | (rd_u16(blk + 4) << 16);
+#pragma unroll 8
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t ql = blk[6 + i];
+            const int a = (int)((ql & 15u) | (((qh >> i) & 1u) << 4));
+            const int c = (int)((ql >> 4) | (((qh >> (i + 16)) & 1u) << 4));
+            y[i] = d * (float)(a - 16);
+            y[i + 16] = d * (float)(c - 16);
+        }
+    } else if constexpr (TYPE == MXH_F16) {
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) y[i] = half_bits_to_float(rd_u16(rp + 2 * (run * 32 + i)));
+    } else {
+        const float* src = reinterpret_cast<const float*>(rp) + run * 32;
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) y[i] = src[i];
+    }
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+}  // namespace mxh

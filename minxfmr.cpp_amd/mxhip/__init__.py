@@ -50,7 +50,7 @@ class SynthArch(C.Structure):
                                        "ffn_down_type")]
 
 
-MODEL_ROPE_NEOX, MODEL_GGML_FORM, MODEL_NO_QK_NORM, MODEL_NO_GRAPH = 1, 4, 8, 16
+MODEL_ROPE_NEOX, MODEL_GGML_FORM, MODEL_NO_QK_NORM, MODEL_NO_GRAPH, MODEL_TOKEN_PREFILL = 1, 4, 8, 16, 32
 
 
 def _load() -> C.CDLL:
@@ -70,6 +70,7 @@ def _load() -> C.CDLL:
         "mxh_download": (ip, [vp, vp, sz]),
         "mxh_memset": (ip, [vp, ip, sz]),
         "mxh_copy": (ip, [vp, vp, sz]),
+        "mxh_gemm_q_bf16": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
         "mxh_timer_begin": (ip, []),
         "mxh_timer_end": (ip, [fp]),
         "mxh_gemv": (ip, [ip, vp, vp, vp, i64, i64, ip]),
@@ -88,6 +89,7 @@ def _load() -> C.CDLL:
         "mxh_model_reset": (ip, [vp]),
         "mxh_model_position": (ip, [vp]),
         "mxh_model_step": (ip, [vp, ip, vp, vp]),
+        "mxh_model_prefill": (ip, [vp, vp, ip]),
         "mxh_model_generate": (ip, [vp, vp, ip, ip, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mxh_model_close": (None, [vp]),
         "mxh_model_decode": (ip, [vp, ip, vp, C.POINTER(C.c_float)]),
@@ -104,10 +106,10 @@ def _load() -> C.CDLL:
 lib = _load()
 EXPORTED = (
     "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
-    "mxh_download mxh_memset mxh_copy mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
+    "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
-    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_generate mxh_model_close "
+    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_generate mxh_model_close "
     "mxh_write_synthetic_gguf mxh_model_decode mxh_model_bench_gemv"
 ).split()
 
@@ -184,6 +186,12 @@ def gemv(type_: int, w: DeviceBuffer | int, x: DeviceBuffer | int, y: DeviceBuff
     check(lib.mxh_gemv(type_, addr(w), addr(x), addr(y), n, k, form), "mxh_gemv")
 
 
+def gemm_bf16(type_: int, a: DeviceBuffer, m: int, w: DeviceBuffer, n: int, k: int, out: DeviceBuffer,
+              form: int = FORM_REF) -> None:
+    """out[m x n] = bf16(a) . bf16(dequant(w))^T on the matrix cores."""
+    check(lib.mxh_gemm_q_bf16(type_, a.ptr, m, w.ptr, n, k, out.ptr, form), "mxh_gemm_q_bf16")
+
+
 def memset(buf: DeviceBuffer, value: int) -> None:
     check(lib.mxh_memset(buf.ptr, value, buf.nbytes), "mxh_memset")
 
@@ -250,6 +258,11 @@ class Model:
     @property
     def position(self) -> int:
         return lib.mxh_model_position(self.h)
+
+    def prefill(self, tokens) -> None:
+        """Feed prompt ids at the current position (no logits)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        check(lib.mxh_model_prefill(self.h, ptr(t) if t.size else None, t.size), "prefill")
 
     def step(self, token: int, logits: bool = True, trace: bool = False):
         c = self.cfg
