@@ -237,7 +237,7 @@ int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t 
                                      g_ctx.stream))
         return set_error(rc, "gemm: conversion launch");
     if (int rc = gemm_bf16_run(type, (const uint16_t*)abf, nullptr, (int)k, w, out, (int)n, nullptr, (int)m, (int)n,
-                               (int)k, form, g_ctx.stream))
+                               (int)k, form, nullptr, 0, g_ctx.stream))
         return set_error(rc, "gemm: unsupported type %d", type);
     return check_hip(hipGetLastError(), "gemm launch");
 }

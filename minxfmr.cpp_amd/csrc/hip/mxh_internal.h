@@ -79,9 +79,10 @@ int add_int_launch(int* p, int v, hipStream_t st);
 
 // Batched prefill (mxh_prefill.hip): dequant-to-bf16 MFMA GEMM
 // out[m x n] (row stride ldo) = a[m x k] (bf16, row stride lda) . W[n x k]^T (+ res);
-// with a_lo (the bf16 residual of a) the split three-product form
+// with a_lo (the bf16 residual of a) the split three-product form; `part`
+// (part_floats floats, may be null) lets narrow shapes split K
 int gemm_bf16_run(int type, const uint16_t* a, const uint16_t* a_lo, int lda, const void* w, float* out, int ldo,
-                  const float* res, int m, int n, int k, int form, hipStream_t st);
+                  const float* res, int m, int n, int k, int form, float* part, size_t part_floats, hipStream_t st);
 int rows_to_bf16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a, uint16_t* a_lo,
                         int lda, int m, hipStream_t st);
 int silu_mul_bf16_launch(const float* gu, int f, uint16_t* h, uint16_t* h_lo, int m, hipStream_t st);

@@ -70,6 +70,8 @@ struct mxh_model {
     int pf_rows = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_gu = nullptr;
     uint16_t *pf_a = nullptr, *pf_a_lo = nullptr;  // GEMM input as split bf16 (hi, lo)
+    float* pf_part = nullptr;                        // split-K partial tiles
+    size_t pf_part_floats = 0;
 };
 
 namespace {
@@ -188,7 +190,7 @@ int free_model(mxh_model* m) {
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
                     m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
-                    m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo};
+                    m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -518,6 +520,9 @@ int ensure_prefill_buffers(mxh_model* m) {
     if (!rc) rc = dalloc(&m->pf_gu, (size_t)rows * 2 * c.n_ff);
     if (!rc) rc = dalloc(&m->pf_a, (size_t)rows * widest);
     if (!rc) rc = dalloc(&m->pf_a_lo, (size_t)rows * widest);
+    // split-K partials: up to 4 splits of the narrower outputs (x, q|k|v)
+    m->pf_part_floats = 4 * (size_t)rows * std::max((size_t)c.n_embd, qd + 2 * kvd);
+    if (!rc) rc = dalloc(&m->pf_part, m->pf_part_floats);
     if (!rc) m->pf_rows = rows;
     return rc;
 }
@@ -525,7 +530,7 @@ int ensure_prefill_buffers(mxh_model* m) {
 // split-bf16 GEMM over the prefill input buffers (pf_a, pf_a_lo)
 int gemm(mxh_model* m, const DevW& w, int lda, float* out, int ldo, const float* res, int rows, hipStream_t st) {
     return gemm_bf16_run(w.type, m->pf_a, m->pf_a_lo, lda, w.p, out, ldo, res, rows, (int)w.rows, (int)w.cols,
-                         m->form, st);
+                         m->form, m->pf_part, m->pf_part_floats, st);
 }
 
 // Prompt tokens tokens[p0 .. p0+rows) through every layer at once, the

@@ -54,21 +54,38 @@ __device__ __forceinline__ uint4 pack8_lo(const float* y) {
     return pack8(r);
 }
 
-// Decode W rows [n0, n0 + 128) x columns [k0, k0 + 64) into Ws: thread t
-// takes run (k0 / 32 + t % 2) of row n0 + t / 2 (rows past n repeat the last).
+// Weight tile staging, split in two so the next K step's global loads are
+// in flight while the current step runs on the matrix cores: fetch() reads
+// thread t's part of W rows [n0, n0 + 128) x columns [k0, k0 + 64) (run
+// k0 / 32 + t % 2 of row n0 + t / 2; rows past n repeat the last) into
+// registers, store() decodes it (bit-exact fp32, then bf16 hi / lo) into
+// the LDS tiles.
 template <int TYPE>
-__device__ __forceinline__ void load_w_tile(const uint8_t* __restrict__ w, size_t rb, int n, int n0, int k0, int form,
-                                            uint16_t* Ws, uint16_t* Ws_lo) {
-    const int t = threadIdx.x, r = t >> 1, h = t & 1;
-    const int row = min(n0 + r, n - 1);
-    float y[32];
-    if constexpr (TYPE == MXH_Q4_K) {
-        // 16-byte loads: header and the 32 qs bytes of 64-group g
+struct WStage {
+    float y[32];  // generic types decode at fetch time
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int h, int form) {
+        dequant_run32<TYPE>(w + (size_t)row * rb, (k0 >> 5) + h, form, y);
+    }
+    __device__ __forceinline__ void decode(int, int, float* out) const {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) out[i] = y[i];
+    }
+};
+
+template <>
+struct WStage<MXH_Q4_K> {
+    uint4 hd, qa, qb;  // header and the 32 qs bytes of 64-group g
+    int form;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int, int f) {
         const uint8_t* blk = w + (size_t)row * rb + (size_t)(k0 >> 8) * 144;
-        const int g = (k0 & 255) >> 6, j = 2 * g + h;
-        const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-        const uint4 qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
-        const uint4 qb = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
+        const int g = (k0 & 255) >> 6;
+        hd = *reinterpret_cast<const uint4*>(blk);
+        qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
+        qb = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
+        form = f;
+    }
+    __device__ __forceinline__ void decode(int k0, int h, float* y) const {
+        const int j = 2 * ((k0 & 255) >> 6) + h;
         uint32_t sc, mn;
         k4_scale_min(hd.y, hd.z, hd.w, j, form, sc, mn);
         const float ds = half_bits_to_float(hd.x & 0xffffu) * (float)sc;
@@ -79,9 +96,14 @@ __device__ __forceinline__ void load_w_tile(const uint8_t* __restrict__ w, size_
         for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int b = 0; b < 4; ++b) y[4 * i + b] = ds * (float)((q[i] >> (8 * b + sh)) & 15u) - ms;
-    } else {
-        dequant_run32<TYPE>(w + (size_t)row * rb, (k0 >> 5) + h, form, y);
     }
+};
+
+template <int TYPE>
+__device__ __forceinline__ void store_w_tile(const WStage<TYPE>& ws, int k0, uint16_t* Ws, uint16_t* Ws_lo) {
+    const int t = threadIdx.x, r = t >> 1, h = t & 1;
+    float y[32];
+    ws.decode(k0, h, y);
     uint4* dst = reinterpret_cast<uint4*>(Ws + r * kLdk + h * 32);
 #pragma unroll
     for (int q = 0; q < 4; ++q) dst[q] = pack8(y + 8 * q);
@@ -92,28 +114,37 @@ __device__ __forceinline__ void load_w_tile(const uint8_t* __restrict__ w, size_
     }
 }
 
-// A rows [m0, m0 + 128) x columns [k0, k0 + 64) (bf16) into As; rows past m
-// are zero.
-__device__ __forceinline__ void load_a_tile(const uint16_t* __restrict__ a, int lda, int m, int m0, int k0,
-                                            uint16_t* As) {
+// A rows [m0, m0 + 128) x columns [k0, k0 + 64): 32 bf16 of row m0 + t / 2
+// per thread (zeros past m)
+__device__ __forceinline__ void fetch_a(const uint16_t* __restrict__ a, int lda, int m, int m0, int k0, uint4 (&v)[4]) {
     const int t = threadIdx.x, r = t >> 1, h = t & 1;
-    uint4* dst = reinterpret_cast<uint4*>(As + r * kLdk + h * 32);
     if (m0 + r < m) {
         const uint4* src = reinterpret_cast<const uint4*>(a + (size_t)(m0 + r) * lda + k0 + h * 32);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dst[q] = src[q];
+        for (int q = 0; q < 4; ++q) v[q] = src[q];
     } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dst[q] = make_uint4(0, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) v[q] = make_uint4(0, 0, 0, 0);
     }
+}
+
+__device__ __forceinline__ void store_a(const uint4 (&v)[4], uint16_t* As) {
+    const int t = threadIdx.x, r = t >> 1, h = t & 1;
+    uint4* dst = reinterpret_cast<uint4*>(As + r * kLdk + h * 32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = v[q];
 }
 
 constexpr size_t kTileBytes = (size_t)kBM * kLdk * sizeof(uint16_t);  // one [128][72] bf16 tile
 
+// Split K: workgroup z of gridDim.z takes K steps [z * ksteps, (z+1) * ksteps)
+// and, with more than one split, writes its fp32 partial tile to
+// part[z][m][n] for gemm_reduce_kernel.
 template <int TYPE, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ a_lo,
                                                         int lda, const uint8_t* __restrict__ w, float* out, int ldo,
-                                                        const float* res, int m, int n, int k, int form) {
+                                                        const float* res, int m, int n, int k, int form, int ksteps,
+                                                        float* __restrict__ part) {
     // tiles: A, W, and (split) A lo, W lo
     extern __shared__ __align__(16) uint16_t smem[];
     uint16_t* As = smem;
@@ -123,7 +154,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wr = wave >> 1, wc = wave & 1;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const int kb = blockIdx.z * ksteps * kBK, ke = min(k, kb + ksteps * kBK);
     const size_t rb = row_bytes(TYPE, k);
+    const int wrow = min(n0 + (int)(threadIdx.x >> 1), n - 1), wh = threadIdx.x & 1;
     f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -132,11 +165,22 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
     const int lr = lane & 31, lk = 8 * (lane >> 5);
-    for (int k0 = 0; k0 < k; k0 += kBK) {
-        load_a_tile(a, lda, m, m0, k0, As);
-        if (SPLIT) load_a_tile(a_lo, lda, m, m0, k0, As_lo);
-        load_w_tile<TYPE>(w, rb, n, n0, k0, form, Ws, Ws_lo);
+    uint4 av_g[4], al_g[4];
+    WStage<TYPE> ws;
+    fetch_a(a, lda, m, m0, kb, av_g);
+    if (SPLIT) fetch_a(a_lo, lda, m, m0, kb, al_g);
+    ws.fetch(w, rb, wrow, kb, wh, form);
+    for (int k0 = kb; k0 < ke; k0 += kBK) {
+        store_a(av_g, As);
+        if (SPLIT) store_a(al_g, As_lo);
+        store_w_tile<TYPE>(ws, k0, Ws, Ws_lo);
         __syncthreads();
+        // next step's loads fly while this one runs on the matrix cores
+        if (k0 + kBK < ke) {
+            fetch_a(a, lda, m, m0, k0 + kBK, av_g);
+            if (SPLIT) fetch_a(a_lo, lda, m, m0, k0 + kBK, al_g);
+            ws.fetch(w, rb, wrow, k0 + kBK, wh, form);
+        }
 #pragma unroll
         for (int ks = 0; ks < kBK; ks += 16) {
             bf16x8 av[2], bv[2], al[2], bl[2];
@@ -164,6 +208,9 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
         }
         __syncthreads();
     }
+    const bool partial = gridDim.z > 1;
+    float* dst = partial ? part + (size_t)blockIdx.z * m * n : out;
+    const int ld = partial ? n : ldo;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -174,11 +221,24 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
                 if (row < m) {
-                    const size_t o = (size_t)row * ldo + col;
-                    out[o] = res ? acc[i][j][e] + res[o] : acc[i][j][e];
+                    const size_t o = (size_t)row * ld + col;
+                    if (partial) dst[o] = acc[i][j][e];
+                    else dst[o] = res ? acc[i][j][e] + res[o] : acc[i][j][e];
                 }
             }
         }
+}
+
+// out = sum over splits of part (in split order) (+ res)
+__global__ void gemm_reduce_kernel(const float* __restrict__ part, int splits, float* out, int ldo, const float* res,
+                                   int m, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * n) return;
+    const int r = i / n, c = i % n;
+    float v = 0.f;
+    for (int s = 0; s < splits; ++s) v += part[(size_t)s * m * n + i];
+    const size_t o = (size_t)r * ldo + c;
+    out[o] = res ? v + res[o] : v;
 }
 
 // bf16 copy of rows of x, optionally replaced by the reference rmsnorm
@@ -244,7 +304,7 @@ namespace {
 
 template <int TYPE, bool SPLIT>
 int gemm_launch(const uint16_t* a, const uint16_t* a_lo, int lda, const uint8_t* w, float* out, int ldo,
-                const float* res, int m, int n, int k, int form, hipStream_t st) {
+                const float* res, int m, int n, int k, int form, float* part, size_t part_floats, hipStream_t st) {
     const size_t lds = (SPLIT ? 4 : 2) * kTileBytes;
     static bool attr_set = false;  // above 64 KiB of LDS needs the opt-in, once per kernel
     if (!attr_set) {
@@ -253,22 +313,32 @@ int gemm_launch(const uint16_t* a, const uint16_t* a_lo, int lda, const uint8_t*
             return MXH_ERR_HIP;
         attr_set = true;
     }
-    const dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
+    const int tn = (n + kBN - 1) / kBN, tm = (m + kBM - 1) / kBM, steps = k / kBK;
+    // split K while the tile grid leaves CUs idle (at most 4 ways, partials
+    // in `part`, reduced in split order)
+    int splits = 1;
+    while (splits < 4 && tn * tm * splits * 2 <= 512 && steps % (splits * 2) == 0 &&
+           (size_t)(splits * 2) * m * n <= part_floats)
+        splits *= 2;
+    const dim3 grid(tn, tm, splits);
     hipLaunchKernelGGL((gemm_bf16_kernel<TYPE, SPLIT>), grid, dim3(256), lds, st, a, a_lo, lda, w, out, ldo, res, m, n,
-                       k, form);
+                       k, form, steps / splits, part);
+    if (splits > 1)
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
+                           res, m, n);
     return MXH_OK;
 }
 
 template <bool SPLIT>
 int gemm_dispatch(int type, const uint16_t* a, const uint16_t* a_lo, int lda, const uint8_t* w, float* out, int ldo,
-                  const float* res, int m, int n, int k, int form, hipStream_t st) {
+                  const float* res, int m, int n, int k, int form, float* part, size_t pf, hipStream_t st) {
     switch (type) {
-    case MXH_Q4_K: return gemm_launch<MXH_Q4_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, st);
-    case MXH_Q5_K: return gemm_launch<MXH_Q5_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, st);
-    case MXH_Q8_0: return gemm_launch<MXH_Q8_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, st);
-    case MXH_Q5_0: return gemm_launch<MXH_Q5_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, st);
-    case MXH_F16: return gemm_launch<MXH_F16, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, st);
-    case MXH_F32: return gemm_launch<MXH_F32, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, st);
+    case MXH_Q4_K: return gemm_launch<MXH_Q4_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q5_K: return gemm_launch<MXH_Q5_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q8_0: return gemm_launch<MXH_Q8_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q5_0: return gemm_launch<MXH_Q5_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_F16: return gemm_launch<MXH_F16, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_F32: return gemm_launch<MXH_F32, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     }
     return MXH_ERR_UNSUPPORTED;
 }
@@ -276,11 +346,12 @@ int gemm_dispatch(int type, const uint16_t* a, const uint16_t* a_lo, int lda, co
 }  // namespace
 
 int gemm_bf16_run(int type, const uint16_t* a, const uint16_t* a_lo, int lda, const void* w, float* out, int ldo,
-                  const float* res, int m, int n, int k, int form, hipStream_t st) {
+                  const float* res, int m, int n, int k, int form, float* part, size_t part_floats, hipStream_t st) {
     if (m <= 0 || n <= 0 || k <= 0 || k % kBK || lda < k || ldo < n || row_bytes(type, k) == 0) return MXH_ERR_ARG;
     const uint8_t* wb = (const uint8_t*)w;
-    return a_lo ? gemm_dispatch<true>(type, a, a_lo, lda, wb, out, ldo, res, m, n, k, form, st)
-                : gemm_dispatch<false>(type, a, nullptr, lda, wb, out, ldo, res, m, n, k, form, st);
+    if (!part) part_floats = 0;
+    return a_lo ? gemm_dispatch<true>(type, a, a_lo, lda, wb, out, ldo, res, m, n, k, form, part, part_floats, st)
+                : gemm_dispatch<false>(type, a, nullptr, lda, wb, out, ldo, res, m, n, k, form, part, part_floats, st);
 }
 
 int rows_to_bf16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a, uint16_t* a_lo,
