@@ -11,6 +11,11 @@
     # per-kernel time table from a --kernel-trace --stats run
     python3 -m mxhip.profiling stats OUT/trace/run_kernel_stats.csv
 
+    # MFMA utilisation of the prefill GEMMs
+    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 -d OUT/mfma -o run \
+        --output-format csv -- python3 bench.py --steps 1 --warmup 0 --gemv-reps 1 --no-cpu-baseline
+    python3 -m mxhip.profiling mfma OUT/mfma
+
 The workload launches each shape `reps` times over rotating weight copies
 (more than the 256 MB Infinity Cache in total) and copies 256 MiB once per
 rep.  FETCH_SIZE and WRITE_SIZE are reported by rocprofv3 in KiB per
@@ -82,15 +87,18 @@ def _counter_rows(d: str):
     return rows
 
 
-def _per_dispatch(rows, counter: str):
-    """{kernel name: [value per dispatch]} for one counter (summed over
-    the per-instance rows rocprofv3 may write for a dispatch)."""
+def _per_dispatch(rows, counter: str, reduce=None):
+    """{kernel name: [value per dispatch]} for one counter, combining the
+    per-instance rows rocprofv3 may write for a dispatch with `reduce`
+    (sum by default; max for whole-device clocks such as GRBM_GUI_ACTIVE)."""
+    reduce = reduce or (lambda a, b: a + b)
     acc: dict[tuple[str, str], float] = {}
     for r in rows:
         if r.get("Counter_Name") != counter:
             continue
         key = (r["Dispatch_Id"], r["Kernel_Name"])
-        acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+        v = float(r["Counter_Value"])
+        acc[key] = reduce(acc[key], v) if key in acc else v
     out: dict[str, list[float]] = {}
     for (did, name), v in sorted(acc.items(), key=lambda kv: int(kv[0][0])):
         out.setdefault(name, []).append(v)
@@ -133,6 +141,37 @@ def traffic(fetch_dir: str, write_dir: str) -> None:
     print(f"TRAFFIC_PER_LAUNCH_BYTES={tot_traffic / len(SHAPES):.0f}")
 
 
+def mfma(d: str) -> None:
+    """Per-kernel MFMA utilisation from a run with
+    --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16:
+    busy cycles / (GUI-active cycles x SIMDs) (rocprofv3's MfmaUtil), and the
+    bf16 MFMA flops issued (512 per MOP)."""
+    rows = _counter_rows(d)
+    simds = None
+    agent = glob.glob(os.path.join(d, "**", "*agent_info.csv"), recursive=True)
+    if agent:
+        with open(agent[0], newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Agent_Type", "").upper() == "GPU" or r.get("Type", "").upper() == "GPU":
+                    simds = int(r.get("Simd_Count") or r.get("SIMD_Count") or 0) or None
+    busy = _per_dispatch(rows, "SQ_VALU_MFMA_BUSY_CYCLES")
+    gui = _per_dispatch(rows, "GRBM_GUI_ACTIVE", max)
+    mops = _per_dispatch(rows, "SQ_INSTS_VALU_MFMA_MOPS_BF16")
+    simds = simds or 1024
+    print(f"| kernel | dispatches | MFMA busy (% of SIMD cycles) | bf16 MFMA GFLOP per dispatch |")
+    print("|---|---:|---:|---:|")
+    for name in busy:
+        if name not in gui:
+            continue
+        b, g = busy[name], gui[name]
+        util = 100.0 * sum(b) / (sum(g) * simds) if sum(g) else 0.0
+        fl = sum(mops.get(name, [0])) * 512 / max(1, len(mops.get(name, [1]))) / 1e9
+        short = name.replace("mxh::(anonymous namespace)::", "").replace("void ", "")
+        short = re.sub(r"\([^()]*\)$", "", short)
+        print(f"| `{short}` | {len(b)} | {util:.1f} | {fl:.1f} |")
+    print(f"\nSIMDs: {simds}")
+
+
 def stats(path: str, top: int = 15) -> None:
     with open(path, newline="") as fh:
         rows = list(csv.DictReader(fh))
@@ -164,6 +203,8 @@ def main(argv: list[str]) -> int:
         traffic(argv[1], argv[2])
     elif cmd == "stats":
         stats(argv[1])
+    elif cmd == "mfma":
+        mfma(argv[1])
     else:
         print(__doc__)
         return 2
