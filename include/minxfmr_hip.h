@@ -184,6 +184,22 @@ int mxh_model_position(const mxh_model *m);
 /* Run `token` at the current position and advance.  logits (n_vocab floats)
  * and trace ((n_layer + 1) * n_embd floats: hidden after each layer, then the
  * final-normed hidden) are host buffers and may be NULL.  Synchronous. */
+/* Sampling of the next token after each step (replaces the greedy argmax):
+ * the top_k (1..64) largest logits, softmax at `temperature` in double,
+ * then the top-p and min-p cuts, then a draw from a seeded splitmix64
+ * stream (the d-th draw uses state seed + (d+1) * 0x9E3779B97F4A7C15).
+ * temperature <= 0 restores greedy decoding.  mxh_model_reset rewinds the
+ * stream to draw 0.  Replaces the sampler of src/api/minxfmr.cpp:2091-2171,
+ * whose std::mt19937 is unseeded; the arithmetic before the draw is the
+ * same. */
+int mxh_model_set_sampling(mxh_model *m, int top_k, double temperature, double top_p, double min_p, uint64_t seed);
+
+/* One sampling decision over n device-resident logits with the rules of
+ * mxh_model_set_sampling, using draw number `draw` of the stream; the token
+ * id is written to *token (host).  For tests and per-op callers. */
+int mxh_sample(const float *logits, int n, int top_k, double temperature, double top_p, double min_p, uint64_t seed,
+               uint64_t draw, int *token);
+
 /* Feed n prompt tokens at the current position without producing logits:
  * batched on the matrix cores in chunks of up to 512 tokens (dequant-to-bf16
  * MFMA GEMMs, row-batched QK-norm/RoPE/KV append and causal attention),

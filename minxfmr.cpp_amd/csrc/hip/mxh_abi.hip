@@ -242,6 +242,32 @@ int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t 
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
+int mxh_sample(const float* logits, int n, int top_k, double temperature, double top_p, double min_p, uint64_t seed,
+               uint64_t draw, int* token) {
+    if (int rc = ensure_ready()) return rc;
+    if (!logits || !token || n <= 0) return set_error(MXH_ERR_ARG, "sample: bad arguments");
+    if (top_k < 1 || top_k > 64 || top_k > n) return set_error(MXH_ERR_ARG, "sample: top_k %d outside 1..min(64, n)", top_k);
+    void *prm = nullptr, *cand = nullptr;
+    if (int rc = stage(0, sizeof(SampleParams) + sizeof(int), &prm)) return rc;
+    if (int rc = stage(1, sample_scratch_keys(n, top_k) * sizeof(uint64_t), &cand)) return rc;
+    SampleParams h{};
+    h.top_k = top_k;
+    h.temperature = temperature;
+    h.top_p = top_p;
+    h.min_p = min_p;
+    h.seed = seed;
+    h.draws = draw;
+    int* out = reinterpret_cast<int*>(static_cast<char*>(prm) + sizeof(SampleParams));
+    if (int rc = check_hip(hipMemcpyAsync(prm, &h, sizeof(h), hipMemcpyHostToDevice, g_ctx.stream), "sample params"))
+        return rc;
+    if (int rc = sample_launch(logits, n, static_cast<SampleParams*>(prm), top_k, static_cast<uint64_t*>(cand), out,
+                               nullptr, nullptr, g_ctx.stream))
+        return set_error(rc, "sample: vocabulary of %d too large for top_k %d", n, top_k);
+    if (int rc = check_hip(hipMemcpyAsync(token, out, sizeof(int), hipMemcpyDeviceToHost, g_ctx.stream), "sample id"))
+        return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "sample");
+}
+
 int mxh_preload(const void* host, size_t bytes) {
     if (int rc = ensure_ready()) return rc;
     if (!host || !bytes) return set_error(MXH_ERR_ARG, "preload: empty tensor");

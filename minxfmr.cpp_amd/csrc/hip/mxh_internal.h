@@ -86,6 +86,19 @@ int gemm_bf16_run(int type, const uint16_t* a, const uint16_t* a_lo, int lda, co
 int rows_to_bf16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a, uint16_t* a_lo,
                         int lda, int m, hipStream_t st);
 int silu_mul_bf16_launch(const float* gu, int f, uint16_t* h, uint16_t* h_lo, int m, hipStream_t st);
+// Device sampling (mxh_sample.hip).  Parameters live in device memory so a
+// captured decode graph reads the current values; `draws` counts the random
+// draws taken (the stream position of the seeded generator).
+struct SampleParams {
+    int top_k;
+    int pad;
+    double temperature, top_p, min_p;
+    uint64_t seed;
+    uint64_t draws;
+};
+size_t sample_scratch_keys(int n, int top_k);
+int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint64_t* cand, int* out, int* tokens,
+                  int* pos, hipStream_t st);
 int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,
                          const double* rope_cs, int p0, int m, float* q_out, __half* kc, __half* vc, int nh, int nkv,
                          int hd, int neox, float eps, hipStream_t st);

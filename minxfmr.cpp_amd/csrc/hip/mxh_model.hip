@@ -65,7 +65,12 @@ struct mxh_model {
     int host_pos = 0;
     bool trace_on = false;
     bool token_prefill = false;  // prompt token by token instead of batched
-    hipGraphExec_t g_prefill = nullptr, g_decode = nullptr;
+    hipGraphExec_t g_prefill = nullptr, g_decode = nullptr, g_sample = nullptr;
+    // sampling instead of greedy argmax (mxh_model_set_sampling)
+    bool sampling = false;
+    int top_k = 1;
+    SampleParams* sprm = nullptr;  // device copy, draw counter included
+    uint64_t* scand = nullptr;     // pass-1 candidates
     // batched prefill (allocated on first use): rows of up to pf_rows tokens
     int pf_rows = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_gu = nullptr;
@@ -152,7 +157,13 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
     }
     if (with_head) {
         if (m->trace_on) rc |= rmsnorm_launch(m->x, m->out_norm, m->trace + (size_t)c.n_layer * d, d, c.eps, st);
-        rc |= gemv(m->out, m->x, m->logits, nullptr, m->form, st, m->out_norm, c.eps, GEMV_ARGMAX, m);
+        if (m->sampling) {
+            // logits, then top-k / temperature sampling writes tokens[pos+1]
+            rc |= gemv(m->out, m->x, m->logits, nullptr, m->form, st, m->out_norm, c.eps);
+            rc |= sample_launch(m->logits, c.n_vocab, m->sprm, m->top_k, m->scand, nullptr, m->tokens, m->pos, st);
+        } else {
+            rc |= gemv(m->out, m->x, m->logits, nullptr, m->form, st, m->out_norm, c.eps, GEMV_ARGMAX, m);
+        }
     } else {
         rc |= add_int_launch(m->pos, 1, st);
     }
@@ -188,9 +199,11 @@ int free_model(mxh_model* m) {
     (void)hipStreamSynchronize(lib_stream());
     if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
+    if (m->g_sample) (void)hipGraphExecDestroy(m->g_sample);
     void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
                     m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
-                    m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part};
+                    m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part,
+                    m->sprm, m->scand};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -436,6 +449,9 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     m->red_cap = c.n_vocab / 2 + 2 < 8192 ? c.n_vocab / 2 + 2 : 8192;
     if (!rc) rc = dalloc(&m->red_val, (size_t)m->red_cap);
     if (!rc) rc = dalloc(&m->red_idx, (size_t)m->red_cap);
+    if (!rc) rc = dalloc(&m->sprm, 1);
+    if (!rc) rc = dalloc(&m->scand, std::max(sample_scratch_keys(c.n_vocab, 64), (size_t)4096));
+    if (!rc) rc = check_hip(hipMemset(m->sprm, 0, sizeof(SampleParams)), "sampler init");
     if (!rc) rc = dalloc(&m->counters, (size_t)c.n_head_kv + 1);
     if (!rc) rc = check_hip(hipMemset(m->counters, 0, sizeof(int) * ((size_t)c.n_head_kv + 1)), "counter init");
     if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * ((size_t)n_ctx + 1)), "token init");
@@ -466,7 +482,11 @@ int mxh_model_reset(mxh_model* m) {
     if (!m) return set_error(MXH_ERR_ARG, "reset: null model");
     m->host_pos = 0;
     const int zero = 0;
+    const uint64_t zero64 = 0;
     if (int rc = check_hip(hipMemcpyAsync(m->pos, &zero, sizeof(int), hipMemcpyHostToDevice, lib_stream()), "reset"))
+        return rc;
+    if (int rc = check_hip(hipMemcpyAsync(&m->sprm->draws, &zero64, sizeof(uint64_t), hipMemcpyHostToDevice,
+                                          lib_stream()), "reset"))
         return rc;
     return check_hip(hipStreamSynchronize(lib_stream()), "reset");
 }
@@ -477,8 +497,9 @@ namespace {
 
 int run_step(mxh_model* m, bool with_head) {
     hipStream_t st = lib_stream();
-    if (m->trace_on || !(with_head ? m->g_decode : m->g_prefill)) return enqueue_step(m, with_head, st);
-    return check_hip(hipGraphLaunch(with_head ? m->g_decode : m->g_prefill, st), "graph launch");
+    hipGraphExec_t g = with_head ? (m->sampling ? m->g_sample : m->g_decode) : m->g_prefill;
+    if (m->trace_on || !g) return enqueue_step(m, with_head, st);
+    return check_hip(hipGraphLaunch(g, st), "graph launch");
 }
 
 }  // namespace
@@ -590,6 +611,39 @@ bool batched_prefill_supported(const mxh_model* m) {
 }
 
 }  // namespace
+
+int mxh_model_set_sampling(mxh_model* m, int top_k, double temperature, double top_p, double min_p, uint64_t seed) {
+    if (!m) return set_error(MXH_ERR_ARG, "set_sampling: null model");
+    if (temperature > 0.0 && (top_k < 1 || top_k > 64))
+        return set_error(MXH_ERR_ARG, "set_sampling: top_k %d outside 1..64", top_k);
+    hipStream_t st = lib_stream();
+    if (int rc = check_hip(hipStreamSynchronize(st), "set_sampling")) return rc;
+    if (!(temperature > 0.0)) {
+        m->sampling = false;
+        return MXH_OK;
+    }
+    if (top_k > m->cfg.n_vocab) top_k = m->cfg.n_vocab;  // the reference clamps k to the vocabulary
+    SampleParams h{};
+    h.top_k = top_k;
+    h.temperature = temperature;
+    h.top_p = top_p;
+    h.min_p = min_p;
+    h.seed = seed;
+    h.draws = 0;
+    if (int rc = check_hip(hipMemcpy(m->sprm, &h, sizeof(h), hipMemcpyHostToDevice), "sampler params")) return rc;
+    const bool recapture = m->g_decode && (!m->g_sample || top_k != m->top_k);
+    m->top_k = top_k;
+    m->sampling = true;
+    if (recapture) {
+        if (m->g_sample) (void)hipGraphExecDestroy(m->g_sample);
+        m->g_sample = nullptr;
+        if (int rc = capture(m, true, &m->g_sample)) {
+            m->sampling = false;
+            return rc;
+        }
+    }
+    return MXH_OK;
+}
 
 int mxh_model_prefill(mxh_model* m, const int* tokens, int n) {
     if (!m || (!tokens && n > 0) || n < 0) return set_error(MXH_ERR_ARG, "prefill: bad arguments");

@@ -1,0 +1,197 @@
+// mxh_sample.hip — top-k / temperature / top-p / min-p sampling on the device
+// (reference: src/api/minxfmr.cpp:2091-2171, with a seeded draw).
+//
+// Pass 1: each of W workgroups sorts its slice of the logits in LDS (bitonic,
+// 64-bit keys: order-preserving bits of the logit above the complemented id,
+// so ties go to the lower id, as the reference's partial_sort with `>` and an
+// increasing initial order) and keeps its best kk = pow2(top_k) candidates.
+// Pass 2: one workgroup sorts the W * kk candidates the same way, then thread
+// 0 forms the probabilities in double exactly as the reference does (exp of
+// (l - max) / T, normalise, top-p cut and renormalise, min-p cut and
+// renormalise) and draws.  The uniform of draw d is splitmix64 at state
+// seed + (d + 1) * 0x9E3779B97F4A7C15, the d-th value of the sequence that
+// starts at `seed`.
+#include <hip/hip_runtime.h>
+
+#include "mxh_device.h"
+#include "mxh_internal.h"
+
+namespace mxh {
+
+namespace {
+
+constexpr int kSortMax = 4096;  // keys one workgroup sorts in LDS
+constexpr int kTopKMax = 64;
+
+__device__ __forceinline__ uint64_t sort_key(float v, int idx) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) u = 0u;  // NaN sorts last
+    else u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)(~(uint32_t)idx);
+}
+
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)(~(uint32_t)(k & 0xffffffffu)); }
+
+// descending bitonic sort of s[0 .. p), p a power of two
+__device__ void bitonic_desc(uint64_t* s, int p) {
+    for (int k = 2; k <= p; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < p; i += blockDim.x) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint64_t a = s[i], b = s[ixj];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? (a < b) : (a > b)) {
+                        s[i] = b;
+                        s[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+__device__ __forceinline__ int pow2_at_least(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+__global__ __launch_bounds__(1024) void topk_pass1_kernel(const float* __restrict__ logits, int n, int slice, int kk,
+                                                          uint64_t* __restrict__ cand) {
+    __shared__ uint64_t s[kSortMax];
+    const int b0 = blockIdx.x * slice, b1 = min(n, b0 + slice);
+    const int p = pow2_at_least(slice > kk ? slice : kk);  // short slices pad up to the list length
+    for (int i = threadIdx.x; i < p; i += blockDim.x) {
+        const int idx = b0 + i;
+        s[i] = idx < b1 ? sort_key(logits[idx], idx) : 0ull;
+    }
+    __syncthreads();
+    bitonic_desc(s, p);
+    for (int i = threadIdx.x; i < kk; i += blockDim.x) cand[(size_t)blockIdx.x * kk + i] = s[i];
+}
+
+__device__ __forceinline__ double draw_uniform(uint64_t seed, uint64_t d) {
+    uint64_t z = seed + (d + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// Candidates -> token.  The token goes to out[0] or, with tokens/pos, to
+// tokens[*pos + 1] with the position advanced (the decode loop on device);
+// the draw counter advances either way.
+__global__ __launch_bounds__(1024) void topk_pass2_kernel(const float* __restrict__ logits, const uint64_t* cand,
+                                                          int ncand, SampleParams* prm, int* out, int* tokens,
+                                                          int* pos) {
+    __shared__ uint64_t s[kSortMax];
+    const int p = pow2_at_least(ncand);
+    for (int i = threadIdx.x; i < p; i += blockDim.x) s[i] = i < ncand ? cand[i] : 0ull;
+    __syncthreads();
+    bitonic_desc(s, p);
+    if (threadIdx.x != 0) return;
+    const int k = prm->top_k;
+    const double temperature = prm->temperature;
+    double top_p = prm->top_p, min_p = prm->min_p;
+    int pick = key_id(s[0]);
+    if (temperature > 0.0) {
+        if (top_p <= 0.0 || top_p > 1.0) top_p = 1.0;
+        if (min_p < 0.0) min_p = 0.0;
+        if (min_p > 1.0) min_p = 1.0;
+        double pr[kTopKMax];
+        const double mx = logits[key_id(s[0])];
+        double sum = 0.0;
+        for (int i = 0; i < k; ++i) {
+            pr[i] = exp(((double)logits[key_id(s[i])] - mx) / temperature);
+            sum += pr[i];
+        }
+        if (sum > 0.0) {
+            for (int i = 0; i < k; ++i) pr[i] /= sum;
+            int m = k;
+            if (top_p < 1.0) {
+                double cum = 0.0;
+                m = 0;
+                for (int i = 0; i < k; ++i) {
+                    cum += pr[i];
+                    m = i + 1;
+                    if (cum >= top_p) break;
+                }
+                double r = 0.0;
+                for (int i = 0; i < m; ++i) r += pr[i];
+                if (r > 0.0)
+                    for (int i = 0; i < m; ++i) pr[i] /= r;
+            }
+            if (min_p > 0.0 && m > 1) {
+                const double thr = pr[0] * min_p;
+                int keep = 1;
+                for (int i = 1; i < m; ++i) {
+                    if (pr[i] >= thr) keep = i + 1;
+                    else break;
+                }
+                m = keep;
+                double r = 0.0;
+                for (int i = 0; i < m; ++i) r += pr[i];
+                if (r > 0.0)
+                    for (int i = 0; i < m; ++i) pr[i] /= r;
+            }
+            double total = 0.0;
+            for (int i = 0; i < m; ++i) total += pr[i];
+            const double u = draw_uniform(prm->seed, prm->draws) * total;
+            double cum = 0.0;
+            pick = key_id(s[m - 1]);
+            for (int i = 0; i < m; ++i) {
+                cum += pr[i];
+                if (u < cum) {
+                    pick = key_id(s[i]);
+                    break;
+                }
+            }
+        }
+        prm->draws += 1;
+    }
+    if (out) out[0] = pick;
+    if (tokens) {
+        const int q = *pos;
+        tokens[q + 1] = pick;
+        *pos = q + 1;
+    }
+}
+
+}  // namespace
+
+// Pass-1 workgroups and the per-workgroup list length for n logits and
+// top_k: the candidates of all workgroups must fit one LDS sort.
+void sample_shape(int n, int top_k, int* groups, int* slice, int* kk) {
+    int k2 = 1;
+    while (k2 < top_k) k2 <<= 1;
+    int w = kSortMax / k2;
+    if (w > 256) w = 256;
+    int sl = (n + w - 1) / w;
+    while (sl > kSortMax) {  // very large vocabularies: fewer, larger lists are not possible
+        w *= 2;
+        sl = (n + w - 1) / w;
+    }
+    *groups = (n + sl - 1) / sl;
+    *slice = sl;
+    *kk = k2;
+}
+
+size_t sample_scratch_keys(int n, int top_k) {
+    int g, sl, kk;
+    sample_shape(n, top_k, &g, &sl, &kk);
+    return (size_t)g * kk;
+}
+
+int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint64_t* cand, int* out, int* tokens,
+                  int* pos, hipStream_t st) {
+    if (n <= 0 || top_k < 1 || top_k > kTopKMax || top_k > n) return MXH_ERR_ARG;
+    int g, sl, kk;
+    sample_shape(n, top_k, &g, &sl, &kk);
+    if ((size_t)g * kk > (size_t)kSortMax) return MXH_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(topk_pass1_kernel, dim3(g), dim3(1024), 0, st, logits, n, sl, kk, cand);
+    hipLaunchKernelGGL(topk_pass2_kernel, dim3(1), dim3(1024), 0, st, logits, cand, g * kk, prm, out, tokens, pos);
+    return MXH_OK;
+}
+
+}  // namespace mxh

@@ -90,6 +90,8 @@ def _load() -> C.CDLL:
         "mxh_model_position": (ip, [vp]),
         "mxh_model_step": (ip, [vp, ip, vp, vp]),
         "mxh_model_prefill": (ip, [vp, vp, ip]),
+        "mxh_model_set_sampling": (ip, [vp, ip, C.c_double, C.c_double, C.c_double, C.c_uint64]),
+        "mxh_sample": (ip, [vp, ip, ip, C.c_double, C.c_double, C.c_double, C.c_uint64, C.c_uint64, C.POINTER(C.c_int)]),
         "mxh_model_generate": (ip, [vp, vp, ip, ip, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mxh_model_close": (None, [vp]),
         "mxh_model_decode": (ip, [vp, ip, vp, C.POINTER(C.c_float)]),
@@ -109,7 +111,7 @@ EXPORTED = (
     "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
-    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_generate mxh_model_close "
+    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_sample mxh_model_generate mxh_model_close "
     "mxh_write_synthetic_gguf mxh_model_decode mxh_model_bench_gemv"
 ).split()
 
@@ -192,6 +194,14 @@ def gemm_bf16(type_: int, a: DeviceBuffer, m: int, w: DeviceBuffer, n: int, k: i
     check(lib.mxh_gemm_q_bf16(type_, a.ptr, m, w.ptr, n, k, out.ptr, form), "mxh_gemm_q_bf16")
 
 
+def sample(logits: DeviceBuffer, n: int, top_k: int, temperature: float, top_p: float = 1.0, min_p: float = 0.0,
+           seed: int = 0, draw: int = 0) -> int:
+    """One device sampling decision over n logits (draw number `draw` of the seeded stream)."""
+    tok = C.c_int(-1)
+    check(lib.mxh_sample(logits.ptr, n, top_k, temperature, top_p, min_p, seed, draw, C.byref(tok)), "mxh_sample")
+    return tok.value
+
+
 def memset(buf: DeviceBuffer, value: int) -> None:
     check(lib.mxh_memset(buf.ptr, value, buf.nbytes), "mxh_memset")
 
@@ -258,6 +268,10 @@ class Model:
     @property
     def position(self) -> int:
         return lib.mxh_model_position(self.h)
+
+    def set_sampling(self, top_k: int, temperature: float, top_p: float = 1.0, min_p: float = 0.0, seed: int = 0):
+        """Top-k / temperature sampling on the device (temperature <= 0: greedy)."""
+        check(lib.mxh_model_set_sampling(self.h, top_k, temperature, top_p, min_p, seed), "set_sampling")
 
     def prefill(self, tokens) -> None:
         """Feed prompt ids at the current position (no logits)."""

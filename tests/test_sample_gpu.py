@@ -1,0 +1,84 @@
+"""Top-k / temperature / top-p / min-p sampling on the device vs the oracle
+(GPU).
+
+The oracle (oracle/mxo.c: mxo_sample) restates minxfmr.cpp:2091-2171 with a
+seeded splitmix64 draw; the device sampler must pick the same id for the
+same logits and the same draw number.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mxhip
+import mxo
+
+pytestmark = pytest.mark.gpu
+
+PARAMS = [
+    (1, 0.8, 1.0, 0.0), (8, 0.8, 1.0, 0.0), (8, 1.5, 0.9, 0.0), (40, 0.7, 0.95, 0.05), (64, 1.0, 1.0, 0.1),
+    (5, 0.0, 1.0, 0.0),  # temperature 0: greedy
+]
+
+
+@pytest.mark.parametrize("n", [300, 151936])
+@pytest.mark.parametrize("k,t,p,mp", PARAMS)
+def test_sample_matches_oracle_on_fixed_logits(mxh, n, k, t, p, mp):
+    rng = np.random.default_rng(n + k)
+    logits = (rng.standard_normal(n) * 2.0).astype(np.float32)
+    logits[rng.integers(0, n, 20)] = logits.max()  # ties at the top: lowest id first
+    buf = mxhip.DeviceBuffer.from_array(logits)
+    seed = 0x5EED + k
+    state = seed
+    for d in range(40):
+        want, state = mxo.sample(logits, k, t, p, mp, state)
+        got = mxhip.sample(buf, n, k, t, p, mp, seed, d)
+        assert got == want, f"draw {d}: device {got}, oracle {want}"
+    buf.close()
+
+
+def test_sample_rejects_bad_top_k(mxh):
+    buf = mxhip.DeviceBuffer.from_array(np.zeros(10, np.float32))
+    for k in (0, 65, 11):
+        with pytest.raises(mxhip.MxhError, match="top_k"):
+            mxhip.sample(buf, 10, k, 1.0)
+    buf.close()
+
+
+from test_model_gpu import TINY, build  # noqa: E402
+
+
+@pytest.mark.parametrize("name", ["q4k-qknorm", "q4k-mixed-q5k"])
+def test_model_sampling_matches_oracle(mxh, tmp_path, name):
+    """Seeded top-k=8, T=0.8 decoding (the BASELINE Llama-3 workload's
+    sampler) of a tiny model: ids equal the oracle's token by token; a reset
+    replays the same stream; graph replay equals eager launches."""
+    p = build(tmp_path, name)
+    prompt = np.random.default_rng(9).integers(0, TINY["n_vocab"], 16).astype(np.int32)
+    k, t, seed, n_gen = 8, 0.8, 4242, 48
+    gm = mxhip.Model(p, 128)
+    gm.set_sampling(k, t, seed=seed)
+    ids, _, _ = gm.generate(prompt, n_gen)
+    ids2, _, _ = gm.generate(prompt, n_gen)
+    assert np.array_equal(ids, ids2)
+    em = mxhip.Model(p, 128, mxhip.MODEL_NO_GRAPH)
+    em.set_sampling(k, t, seed=seed)
+    ids3, _, _ = em.generate(prompt, n_gen)
+    assert np.array_equal(ids, ids3)
+    om = mxo.Model(p, 128)
+    lg = None
+    for tok in prompt:
+        lg, _ = om.step(int(tok))
+    state, want = seed, []
+    for _ in range(n_gen):
+        nxt, state = mxo.sample(lg, k, t, 1.0, 0.0, state)
+        want.append(nxt)
+        lg, _ = om.step(nxt)
+    assert ids.tolist() == want
+    # back to greedy
+    gm.set_sampling(1, 0.0)
+    g1, _, _ = gm.generate(prompt, 8)
+    g2, _, _ = mxhip.Model(p, 128).generate(prompt, 8)
+    assert np.array_equal(g1, g2)
+    for m in (gm, em):
+        m.close()
