@@ -82,6 +82,79 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
                       f"by the C oracle with {threads} OpenMP threads, {el:.1f}s"}
 
 
+LLAMA3_MIXED = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336, n_vocab=128256,
+                    ctx=8192, rope_theta=5e5, eps=1e-5, qk_norm=False, tied=False)
+QWEN3_06B = dict(n_layer=28, n_embd=1024, n_head=16, n_head_kv=8, head_dim=128, n_ff=3072, n_vocab=151936,
+                 ctx=40960, rope_theta=1e6, eps=1e-6, qk_norm=True, tied=True)
+
+
+def extra_model(mxhip, name: str, seed: int) -> Path:
+    d = Path(os.environ.get("MXH_BENCH_DIR", "/tmp"))
+    p = d / f"mxh_bench_{name}_seed{seed}.gguf"
+    if p.exists():
+        return p
+    tmp = p.with_suffix(".tmp")
+    t0 = time.time()
+    if name == "llama3_8b_mixed":
+        mxhip.write_synthetic_gguf(tmp, "llama", wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K,
+                                   attn_v_type=mxhip.Q5_K, ffn_down_type=mxhip.Q5_K, seed=seed,
+                                   threads=min(16, os.cpu_count() or 8), **LLAMA3_MIXED)
+    else:
+        mxhip.write_synthetic_gguf(tmp, "qwen3", wtype=mxhip.Q8_0, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0,
+                                   seed=seed, threads=min(16, os.cpu_count() or 8), **QWEN3_06B)
+    tmp.rename(p)
+    log(f"wrote {p} ({p.stat().st_size / 1e9:.2f} GB) in {time.time() - t0:.1f}s")
+    return p
+
+
+def run_long_context(mxhip, path: Path, seed: int) -> dict:
+    """8192-token prompt prefilled in 512-token chunks on
+    the matrix cores, then 128 greedy decode tokens against the 8192+ cache."""
+    import numpy as np
+
+    n_prompt, n_dec = 8192, 128
+    m = mxhip.Model(path, n_prompt + n_dec + 8)
+    prompt = np.random.default_rng(seed + 1).integers(0, m.cfg.n_vocab, n_prompt).astype(np.int32)
+    _, pf_ms, _ = m.generate(prompt, 1)
+    mxhip.synchronize()
+    t0 = time.perf_counter()
+    m.decode(n_dec)
+    mxhip.synchronize()
+    dt = time.perf_counter() - t0
+    kv_bytes = 2 * m.cfg.n_layer * m.cfg.n_head_kv * m.cfg.head_dim * 2 * (n_prompt + n_dec // 2)
+    m.close()
+    out = {"prompt": n_prompt, "decode_tokens": n_dec, "prefill_tok_s": round(n_prompt / (pf_ms * 1e-3), 1),
+           "decode_tok_s": round(n_dec / dt, 2),
+           "decode_hbm_gbs": round((m.cfg.step_read_bytes + kv_bytes) / (dt / n_dec) / 1e9, 1)}
+    log(f"long context: {out}")
+    return out
+
+
+def run_extra_configs(mxhip, seed: int) -> dict:
+    """BASELINE configs 0 and 3: Qwen3-0.6B Q8_0 greedy (32-token prompt, 128
+    tokens) and Llama-3-8B mixed Q4_K/Q5_K with seeded top-k 8, T 0.8 sampling
+    (128-token prompt, 512 tokens)."""
+    import numpy as np
+
+    res = {}
+    for name, n_prompt, n_gen, sampling in (("qwen3_0_6b_q8", 32, 128, None),
+                                            ("llama3_8b_mixed", 128, 512, (8, 0.8, 0xC0F3))):
+        p = extra_model(mxhip, name, seed)
+        m = mxhip.Model(p, n_prompt + n_gen + 8)
+        if sampling:
+            m.set_sampling(sampling[0], sampling[1], seed=sampling[2])
+        prompt = np.random.default_rng(seed + 2).integers(0, m.cfg.n_vocab, n_prompt).astype(np.int32)
+        m.generate(prompt, 8)  # warm-up
+        ids, pf_ms, dec_ms = m.generate(prompt, n_gen)
+        res[name] = {"prompt": n_prompt, "tokens": n_gen, "sampling": "top-k 8, T 0.8, seeded" if sampling else "greedy",
+                     "prefill_tok_s": round(n_prompt / (pf_ms * 1e-3), 1),
+                     "decode_tok_s": round((n_gen - 1) / (dec_ms * 1e-3), 2),
+                     "decode_weight_gbs": round(m.cfg.step_read_bytes / (dec_ms * 1e-3 / (n_gen - 1)) / 1e9, 1)}
+        log(f"{name}: {res[name]}")
+        m.close()
+    return res
+
+
 def measured_traffic(per_launch_bytes: int):
     """HBM bytes per Q4_K GEMV launch from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE measurement of the same shapes (None if absent or
@@ -107,6 +180,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="enqueue kernels directly instead of replaying HIP graphs")
+    ap.add_argument("--no-long-context", action="store_true", help="skip the 8192-token context measurement")
+    ap.add_argument("--all-configs", action="store_true",
+                    help="also run BASELINE configs 0 (Qwen3-0.6B Q8_0) and 3 (Llama-3-8B mixed, sampled)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build targets a single MI355X); --gpus {args.gpus} is not "
@@ -186,6 +262,10 @@ def main() -> int:
                      "kernel": "Q4_K dequant-GEMV (gemv_kernel<Q4K>)",
                      "per_launch_bytes": int(g_bytes_launch), "avg_launch_us": round(g_avg_us, 3)},
     }
+    if not args.no_long_context:
+        out["long_context"] = run_long_context(mxhip, path, args.seed)
+    if args.all_configs:
+        out["configs"] = run_extra_configs(mxhip, args.seed)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(path, prompt, args.cpu_seconds, min(16, os.cpu_count() or 8))
     print(json.dumps(out), flush=True)
