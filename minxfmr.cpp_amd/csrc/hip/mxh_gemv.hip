@@ -546,7 +546,10 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict
     }
 #pragma unroll
     for (int u = 0; u < NB; ++u)
-        if (u * kStep < k) quantize4(v[u], base + u * kStep, base + u * kStep < k, lo, hi, scale, sum16);
+        // no branch per unit: the units are independent, so their DPP and
+        // conversion chains interleave; units past k hold zeros and skip
+        // their stores
+        quantize4(v[u], base + u * kStep, base + u * kStep < k, lo, hi, scale, sum16);
     __syncthreads();
 }
 
