@@ -259,7 +259,7 @@ def main() -> int:
                              "flops": pf_flops, "kernel": "dequant-to-bf16 MFMA GEMM (split hi+lo operands)"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(g_bytes_launch),
-                     "kernel": "Q4_K dequant-GEMV (gemv_kernel<Q4K>)",
+                     "kernel": "Q4_K dequant-GEMV, tiled weight layout (gemv_kernel<Q4KT>)",
                      "per_launch_bytes": int(g_bytes_launch), "avg_launch_us": round(g_avg_us, 3)},
     }
     if not args.no_long_context:

@@ -201,7 +201,7 @@ int mxh_gemv(int type, const void* w, const float* x, float* y, int64_t n, int64
     if (int rc = ensure_ready()) return rc;
     if (int rc = check_weight_ptr(type, w)) return rc;
     if (!x || !y || !aligned(x, 16)) return set_error(MXH_ERR_ARG, "x must be non-null and 16-byte aligned");
-    if (n <= 0 || k <= 0 || row_bytes(type, k) == 0)
+    if (n <= 0 || k <= 0 || type >= kTiledFlag || row_bytes(type, k) == 0)
         return set_error(MXH_ERR_ARG, "gemv: k=%lld is not a whole number of type-%d blocks", (long long)k, type);
     int rc = gemv_launch(type, w, x, y, nullptr, n, k, form, g_ctx.stream);
     if (rc == MXH_ERR_ARG) return set_error(rc, "gemv: unsupported shape n=%lld k=%lld", (long long)n, (long long)k);
@@ -228,7 +228,7 @@ int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t 
     if (int rc = ensure_ready()) return rc;
     if (!a || !w || !out) return set_error(MXH_ERR_ARG, "gemm: null pointer");
     if (m <= 0 || n <= 0 || k <= 0 || k % 64 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX ||
-        row_bytes(type, k) == 0)
+        type >= kTiledFlag || row_bytes(type, k) == 0)
         return set_error(MXH_ERR_ARG, "gemm: bad shape %lldx%lldx%lld for type %d", (long long)m, (long long)n,
                          (long long)k, type);
     void* abf = nullptr;
@@ -291,7 +291,7 @@ int mxh_host_matmul_rhs_t(int type, const float* a, int64_t m, int64_t k, const 
                           float* out, int form) {
     if (int rc = ensure_ready()) return rc;
     if (!a || !w || !out || m <= 0 || n <= 0 || k <= 0) return set_error(MXH_ERR_ARG, "matmul_rhs_t: bad arguments");
-    const size_t rb = row_bytes(type, k);
+    const size_t rb = type >= kTiledFlag ? 0 : row_bytes(type, k);
     if (!rb || w_bytes < rb * (size_t)n) return set_error(MXH_ERR_ARG, "matmul_rhs_t: weight bytes too small");
     const void* dw = nullptr;
     if (int rc = device_weight(w, rb * (size_t)n, &dw)) return rc;

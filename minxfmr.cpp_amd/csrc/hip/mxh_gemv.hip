@@ -20,7 +20,8 @@
 //
 // Integer inner products.  For the quantized formats x is staged as 16-bit
 // block fixed point: per 32-element sub-block j, X_i = rint(x_i / s_j) with
-// s_j = max|x| / 32512, split into two signed bytes X = 256*hi + lo.  The
+// s_j = max|x| / 32512 (up to one float rounding of x_i / s_j before the
+// rint), split into two signed bytes X = 256*hi + lo.  The
 // codes q are small integers, so sum_i X_i q_i is exact in int32 and costs
 // two v_dot4_i32_i8 per four elements (no per-element conversion).  With
 //   sum_i x_i (d*sc*q_i - dmin*m) = d*sc*s_j * sum_i X_i q_i - dmin*m * s_j * sum_i X_i
@@ -48,6 +49,8 @@ __device__ __forceinline__ double block_sum(const double* red) {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short short2v __attribute__((ext_vector_type(2)));
+typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // x index -> padded LDS index (4 floats of padding after every 64)
@@ -264,6 +267,24 @@ struct Q4K {
     }
 };
 
+// Q4_K in the tiled device layout: the same bytes per chunk, read from
+// line-contiguous 16-byte pieces (q4k_tile_offsets)
+template <int R>
+struct Q4KT : Q4K<R> {
+    static constexpr int kType = MXH_Q4_K_TILED;
+    using Buf = typename Q4K<R>::Buf;
+    static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
+        const Q4KTileOffs o = q4k_tile_offsets(c, (int64_t)(rb / 144));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t* rp = w + (size_t)rows[r] * rb;
+            b.hd[r] = ldg16(rp + o.hd);
+            b.qa[r] = ldg16(rp + o.qa);
+            b.qb[r] = ldg16(rp + o.qb);
+        }
+    }
+};
+
 template <int R>
 struct Q5K {
     static constexpr int kType = MXH_Q5_K;
@@ -342,6 +363,42 @@ struct Q80 {
             for (int i = 0; i < 8; ++i) q[i] = (b.bd[r][i] >> 16) | (b.bd[r][i + 1] << 16);
             const float v = dot16(xl0, xh0, q[0], q[1], q[2], q[3]) + dot16(xl1, xh1, q[4], q[5], q[6], q[7]);
             acc[r] = fmaf(d * s, v, acc[r]);
+        }
+    }
+};
+
+// Q8_0 in the tiled device layout (q80_tile_offsets): two aligned 16-byte
+// quant loads and the scale per block instead of ten 2-aligned pieces
+template <int R>
+struct Q80T {
+    static constexpr int kType = MXH_Q8_0_TILED;
+    static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 5;
+    static constexpr int kLoads = 3;
+    struct Buf {
+        uint4 lo[R], hi[R];
+        uint32_t d[R];
+    };
+    static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
+        const Q80TileOffs o = q80_tile_offsets(c, (int64_t)(rb / 34));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t* rp = w + (size_t)rows[r] * rb;
+            b.lo[r] = ldg16(rp + o.lo);
+            b.hi[r] = ldg16(rp + o.hi);
+            b.d[r] = *reinterpret_cast<const uint16_t*>(rp + o.d);
+        }
+    }
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
+        const int e0 = 32 * c;
+        const uint4 xl0 = lds16(x.lo + limb(e0 / 4)), xh0 = lds16(x.hi + limb(e0 / 4));
+        const uint4 xl1 = lds16(x.lo + limb(e0 / 4 + 4)), xh1 = lds16(x.hi + limb(e0 / 4 + 4));
+        const float s = x.scale[c];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = dot16(xl0, xh0, b.lo[r].x, b.lo[r].y, b.lo[r].z, b.lo[r].w) +
+                            dot16(xl1, xh1, b.hi[r].x, b.hi[r].y, b.hi[r].z, b.hi[r].w);
+            acc[r] = fmaf(h2f(b.d[r]) * s, v, acc[r]);
         }
     }
 };
@@ -462,32 +519,31 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // limb layout.  Runs with the whole wave active (DPP); `store` guards the
 // LDS writes.
 //
-// X = rint(x / s) with s = max|x| / 32512 fits 16 bits; with Y = X + 128 the
-// signed limbs of X = 256 hi + lo are hi = byte 1 of Y and lo = byte 0 of Y
-// xor 0x80, so four values pack with byte permutes.
+// X = rint(x / s) with s = max|x| / 32512 fits 16 bits.  v_cvt_pknorm_i16_f32
+// converts two values at once (rint(clamp(v, -1, 1) * 32767) into the two
+// halves of a dword), so x is prescaled by 32512 / (32767 max|x|).  With
+// Y = X + 128 (a packed 16-bit add) the signed limbs of X = 256 hi + lo are
+// hi = byte 1 of Y and lo = byte 0 of Y xor 0x80, gathered by byte permutes;
+// the sub-block sums of X come from v_dot2 with (1, 1), exact in int32.
 __device__ __forceinline__ void quantize4(float4 w4, int e, bool store, uint32_t* lo, uint32_t* hi, float* scale,
                                           float* sum16) {
     const float m = max8_dpp(fmaxf(fmaxf(fabsf(w4.x), fabsf(w4.y)), fmaxf(fabsf(w4.z), fabsf(w4.w))));
-    // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite);
-    // |x * is| <= 32512 (1 + 2^-22) still rounds into range
+    // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite)
     const bool live = m > 1e-30f;
     const float sc = live ? m * (1.0f / 32512.0f) : 0.f;
-    const float is = live ? __builtin_amdgcn_rcpf(m) * 32512.0f : 0.f;
-    const float r0 = rintf(w4.x * is), r1 = rintf(w4.y * is), r2 = rintf(w4.z * is), r3 = rintf(w4.w * is);
-    const uint32_t y0 = (uint32_t)(int)(r0 + 128.0f), y1 = (uint32_t)(int)(r1 + 128.0f);
-    const uint32_t y2 = (uint32_t)(int)(r2 + 128.0f), y3 = (uint32_t)(int)(r3 + 128.0f);
-    const uint32_t p01 = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // y0.b0 y0.b1 y1.b0 y1.b1
-    const uint32_t p23 = __builtin_amdgcn_perm(y3, y2, 0x05040100u);
-    const uint32_t plo = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
-    const uint32_t phi = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
-    // sum of the 16 X of this thread's quad (exact in float)
-    float t = (r0 + r1) + (r2 + r3);
-    t += dpp_f<0xb1>(t);  // quad_perm [1,0,3,2]
-    t += dpp_f<0x4e>(t);  // quad_perm [2,3,0,1]
+    const float is = live ? __builtin_amdgcn_rcpf(m) * (32512.0f / 32767.0f) : 0.f;
+    const short2v x01 = __builtin_amdgcn_cvt_pknorm_i16(w4.x * is, w4.y * is);
+    const short2v x23 = __builtin_amdgcn_cvt_pknorm_i16(w4.z * is, w4.w * is);
+    const uint32_t y01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x01) + (ushort2v){128, 128});
+    const uint32_t y23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x23) + (ushort2v){128, 128});
+    const uint32_t plo = __builtin_amdgcn_perm(y23, y01, 0x06040200u) ^ 0x80808080u;
+    const uint32_t phi = __builtin_amdgcn_perm(y23, y01, 0x07050301u);
+    // sum of the 16 X of this thread's quad
+    const int t = sum4_dpp(__builtin_amdgcn_sdot2(x23, (short2v){1, 1}, __builtin_amdgcn_sdot2(x01, (short2v){1, 1}, 0, false), false));
     if (store) {
         lo[limb(e >> 2)] = plo;
         hi[limb(e >> 2)] = phi;
-        if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * t;
+        if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * (float)t;
         if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
     }
 }
@@ -618,7 +674,7 @@ __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ 
 //               (transformer.cpp:183-185, 696-704) for i < F
 //  GEMV_ARGMAX: y = logits; each workgroup also leaves its (largest logit,
 //               lowest index) in red_val/red_idx[blockIdx] for argmax_finish
-template <template <int> class T, int R, int MODE>
+template <template <int> class T, int R, int MODE, bool SHORT>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     using Ty = T<R>;
     using Buf = typename Ty::Buf;
@@ -682,7 +738,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             if (MODE == GEMV_SILU) rows[kOut + r] = o + n_out;
             if constexpr (kRes) st.rs[r] = res_src[o];
         }
-        const int c = min(lane + 64 * ji, nchunks - 1);
+        // past the end every lane reads the same bytes: the loads only keep
+        // the count of outstanding operations uniform and cost no bandwidth
+        const int c = past ? 0 : min(lane + 64 * ji, nchunks - 1);
         Ty::load(a.w, rbytes, rows, c, st.b);
         if (++cu.j == cpl) {
             cu.j = 0;
@@ -729,50 +787,83 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     };
     Cursor ci{0, 0}, cc{0, 0};
     Step s0, s1, s2;
-    // the first two steps' weight loads do not depend on x: they are issued
-    // right after the x loads, so both latencies overlap, and the staging
-    // arithmetic waits for x only
-    auto issue_first = [&] {
-        issue(ci, s0);
-        issue(ci, s1);
-        wait_vmcnt<kL2>();
-    };
-    if constexpr (Ty::kIntX) {
-        stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
-    } else {
-        issue_first();
-        stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
-    }
-    // before consuming a step, wait until only the loads issued after it
-    // (0, 1 or 2 steps) may be outstanding
-    for (int it = 0; it < total; it += 3) {
-        if (it + 2 < total) {
-            issue(ci, s2);
-            wait_vmcnt<kL2>();
-        } else {
-            wait_vmcnt<kL1>();  // step it + 1 (or a repeat of step it) is younger
-        }
-        consume(cc, s0);
-        if (it + 1 >= total) break;
-        if (it + 3 < total) {
+    if constexpr (SHORT) {
+        // At most three steps per wave (the launcher sizes the grid for it):
+        // all of them are issued right after the x loads, so every weight
+        // byte of the wave is in flight during staging, and each step waits
+        // for a fixed count of younger loads, in straight-line code whose
+        // waits the compiler's own analysis leaves alone.
+        constexpr int kL3 = 3 * kL;
+        static_assert(kL3 <= 63, "short form needs three steps of loads in flight");
+        auto issue_all = [&] {
             issue(ci, s0);
-            wait_vmcnt<kL2>();
-        } else if (it + 2 < total) {
-            wait_vmcnt<kL1>();
+            issue(ci, s1);
+            issue(ci, s2);
+            wait_vmcnt<kL3>();
+        };
+        if constexpr (Ty::kIntX) {
+            stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
         } else {
-            wait_vmcnt<0>();
+            issue_all();
+            stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
-        consume(cc, s1);
-        if (it + 2 >= total) break;
-        if (it + 4 < total) {
+        wait_vmcnt<2 * kL>();
+        consume(cc, s0);
+        if (total > 1) {
+            wait_vmcnt<kL>();
+            consume(cc, s1);
+        }
+        if (total > 2) {
+            wait_vmcnt<0>();
+            consume(cc, s2);
+        }
+        wait_vmcnt<0>();  // loads of steps past the end
+    } else {
+        // the first two steps' weight loads do not depend on x: they are
+        // issued right after the x loads, so both latencies overlap, and the
+        // staging arithmetic waits for x only
+        auto issue_first = [&] {
+            issue(ci, s0);
             issue(ci, s1);
             wait_vmcnt<kL2>();
-        } else if (it + 3 < total) {
-            wait_vmcnt<kL1>();
+        };
+        if constexpr (Ty::kIntX) {
+            stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
         } else {
-            wait_vmcnt<0>();
+            issue_first();
+            stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
-        consume(cc, s2);
+        // before consuming a step, wait until only the loads issued after it
+        // (0, 1 or 2 steps) may be outstanding
+        for (int it = 0; it < total; it += 3) {
+            if (it + 2 < total) {
+                issue(ci, s2);
+                wait_vmcnt<kL2>();
+            } else {
+                wait_vmcnt<kL1>();  // step it + 1 (or a repeat of step it) is younger
+            }
+            consume(cc, s0);
+            if (it + 1 >= total) break;
+            if (it + 3 < total) {
+                issue(ci, s0);
+                wait_vmcnt<kL2>();
+            } else if (it + 2 < total) {
+                wait_vmcnt<kL1>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            consume(cc, s1);
+            if (it + 2 >= total) break;
+            if (it + 4 < total) {
+                issue(ci, s1);
+                wait_vmcnt<kL2>();
+            } else if (it + 3 < total) {
+                wait_vmcnt<kL1>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            consume(cc, s2);
+        }
     }
     if constexpr (MODE == GEMV_ARGMAX) {
         if (lane == 63) {
@@ -830,6 +921,16 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(const float* __rest
 // Resident workgroups of a kernel on the whole device (occupancy x CUs),
 // cached per kernel and LDS size: a persistent grid of exactly this size runs
 // in one round, so each resident slot stages x once.
+int device_cus() {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n_cu = 256;
+    }
+    return n_cu;
+}
+
 int resident_grid(const void* kernel, size_t lds) {
     struct Entry {
         const void* k;
@@ -838,14 +939,9 @@ int resident_grid(const void* kernel, size_t lds) {
     };
     static Entry cache[64];
     static int n_cache = 0;
-    static int n_cu = 0;
     for (int i = 0; i < n_cache; ++i)
         if (cache[i].k == kernel && cache[i].lds == lds) return cache[i].grid;
-    if (!n_cu) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            n_cu = 256;
-    }
+    const int n_cu = device_cus();
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
@@ -860,19 +956,52 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const int64_t n_out = mode == GEMV_SILU ? a.n / 2 : a.n;
     const int64_t n_groups = (n_out + kout - 1) / kout;
     const int64_t need = (n_groups + kWaves - 1) / kWaves;
-    const void* kern = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN>
-                       : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU>
-                                           : (const void*)gemv_kernel<T, R, GEMV_ARGMAX>;
+    const int64_t cpl = ((a.k >> T<R>::kChunkShift) + 63) >> 6;  // chunk steps per row group
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
     const size_t lds = T<R>::kIntX ? (size_t)(2 * limb_dwords(a.k) + a.k / 32 + a.k / 16) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
-    const int cap = grid_cap > 0 ? grid_cap : resident_grid(kern, lds);
+    const int n_cu = device_cus();
+    // Short form: when every wave can finish in at most three steps with a
+    // resident grid, one workgroup per CU where that suffices (x is staged
+    // and quantized once per CU), more where three steps per wave need it.
+    constexpr bool kShortOk = 3 * (T<R>::kLoads * R + R) <= 63;
+    if constexpr (kShortOk) {
+        if (mode != GEMV_ARGMAX && grid_cap <= 0 && cpl <= 3) {
+            const int64_t per_wg = (int64_t)kWaves * (3 / cpl);
+            const int64_t min_grid = (n_groups + per_wg - 1) / per_wg;
+            int64_t grid = need < n_cu ? need : n_cu;
+            if (grid < min_grid) grid = min_grid;
+            const void* ks = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, true>
+                                                : (const void*)gemv_kernel<T, R, GEMV_SILU, true>;
+            if (grid <= resident_grid(ks, lds)) {
+                if (mode == GEMV_PLAIN)
+                    hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, true>), dim3((unsigned)grid), dim3(kThreads), lds,
+                                       st, a);
+                else
+                    hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, true>), dim3((unsigned)grid), dim3(kThreads), lds,
+                                       st, a);
+                return MXH_OK;
+            }
+        }
+    }
+    const void* kern = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, false>
+                       : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU, false>
+                                           : (const void*)gemv_kernel<T, R, GEMV_ARGMAX, false>;
+    int cap = grid_cap > 0 ? grid_cap : resident_grid(kern, lds);
+    // Short runs (a few row groups per wave with one workgroup per CU): one
+    // workgroup per CU, so x is staged and quantized once per CU and no CU
+    // carries two workgroups' staging while others carry one.  Long runs keep
+    // the resident occupancy, whose extra waves hide latency.
+    if (grid_cap <= 0 && need > n_cu && (n_groups + (int64_t)n_cu * kWaves - 1) / ((int64_t)n_cu * kWaves) <= 8)
+        cap = n_cu;
     const unsigned grid = (unsigned)(need < cap ? need : cap);
-    if (mode == GEMV_PLAIN) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN>), dim3(grid), dim3(kThreads), lds, st, a);
-    else if (mode == GEMV_SILU) hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU>), dim3(grid), dim3(kThreads), lds, st, a);
+    if (mode == GEMV_PLAIN)
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, false>), dim3(grid), dim3(kThreads), lds, st, a);
+    else if (mode == GEMV_SILU)
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, false>), dim3(grid), dim3(kThreads), lds, st, a);
     else {
         if ((int)grid > a.red_cap) return MXH_ERR_ARG;
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, false>), dim3(grid), dim3(kThreads), lds, st, a);
         hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, st, a.red_val, a.red_idx, (int)grid, a.tokens,
                            a.pos);
     }
@@ -889,6 +1018,8 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.tokens || !a.pos)) return MXH_ERR_ARG;
     switch (type) {
     case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);
+    case MXH_Q4_K_TILED: return launch_gemv<Q4KT, 4>(a, mode, st);
+    case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
     case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
     case MXH_Q5_0: return launch_gemv<Q50, 4>(a, mode, st);

@@ -39,6 +39,12 @@ struct GemvArgs {
     int* pos;
 };
 int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st);
+
+// Tiled device layout for a weight of this type and row length (the type
+// itself when there is none), and the in-place regrouping of `rows` rows at w
+// (16-byte aligned) into it.
+int tiled_type(int type, int64_t cols);
+int tile_rows_launch(int type, void* w, int64_t rows, int64_t cols, hipStream_t st);
 int dequant_launch(int type, const void* w, float* out, int64_t rows, int64_t cols, int form, hipStream_t st);
 
 // small F32 vector ops (attention over host caches, F32 weights)

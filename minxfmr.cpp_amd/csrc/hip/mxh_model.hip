@@ -410,6 +410,28 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     c.type_wffn_down = lo[0].td->type;
     c.type_output = m->out.type;
     c.type_embd = m->embd.type;
+    if (!(flags & MXH_MODEL_GGUF_LAYOUT)) {
+        // regroup the projection weights into the tiled device layout; the
+        // embedding table, read one row per token, keeps the GGUF order, and
+        // so does an output projection tied to it
+        std::vector<DevW*> ws;
+        for (Layer& D : m->layers)
+            for (DevW* w : {&D.qkv, &D.q, &D.k, &D.v, &D.o, &D.gu, &D.g, &D.u, &D.down}) ws.push_back(w);
+        if (to) ws.push_back(&m->out);
+        for (DevW* w : ws) {
+            const int tt = tiled_type(w->type, w->cols);
+            if (!w->p || tt == w->type) continue;
+            if (int rc = tile_rows_launch(w->type, const_cast<void*>(w->p), w->rows, w->cols, lib_stream())) {
+                free_model(m);
+                return set_error(rc, "weight tiling failed");
+            }
+            w->type = tt;
+        }
+        if (int rc = check_hip(hipStreamSynchronize(lib_stream()), "weight tiling")) {
+            free_model(m);
+            return rc;
+        }
+    }
 
     // --- caches, RoPE table, activations ---
     const size_t kv_per_layer = (size_t)n_ctx * kvd;
@@ -732,11 +754,11 @@ int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* l
     std::vector<const DevW*> ws;
     for (const Layer& L : m->layers)
         for (const DevW* w : {&L.qkv, &L.q, &L.k, &L.v, &L.o, &L.gu, &L.g, &L.u, &L.down})
-            if (w->p && w->type == type) ws.push_back(w);
-    if (m->out.type == type) ws.push_back(&m->out);
+            if (w->p && storage_type(w->type) == type) ws.push_back(w);
+    if (storage_type(m->out.type) == type) ws.push_back(&m->out);
     if (ws.empty()) return set_error(MXH_ERR_ARG, "bench_gemv: model has no matrices of type %d", type);
     int64_t b = 0;
-    for (const DevW* w : ws) b += (int64_t)tensor_bytes(w->type, w->rows, w->cols) + 4 * (w->rows + w->cols);
+    for (const DevW* w : ws) b += (int64_t)row_bytes(w->type, w->cols) * w->rows + 4 * (w->rows + w->cols);
     hipEvent_t e0, e1;
     if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
     (void)hipEventCreate(&e1);

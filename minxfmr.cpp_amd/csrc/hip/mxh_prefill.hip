@@ -64,7 +64,7 @@ template <int TYPE>
 struct WStage {
     float y[32];  // generic types decode at fetch time
     __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int h, int form) {
-        dequant_run32<TYPE>(w + (size_t)row * rb, (k0 >> 5) + h, form, y);
+        dequant_run32<TYPE>(w + (size_t)row * rb, (k0 >> 5) + h, form, y, (int64_t)(rb / block_geom(TYPE).bytes));
     }
     __device__ __forceinline__ void decode(int, int, float* out) const {
 #pragma unroll
@@ -96,6 +96,19 @@ struct WStage<MXH_Q4_K> {
         for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int b = 0; b < 4; ++b) y[4 * i + b] = ds * (float)((q[i] >> (8 * b + sh)) & 15u) - ms;
+    }
+};
+
+// tiled device layout: the same three 16-byte pieces (q4k_tile_offsets)
+template <>
+struct WStage<MXH_Q4_K_TILED> : WStage<MXH_Q4_K> {
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int, int f) {
+        const Q4KTileOffs o = q4k_tile_offsets(k0 >> 6, (int64_t)(rb / 144));
+        const uint8_t* rp = w + (size_t)row * rb;
+        hd = *reinterpret_cast<const uint4*>(rp + o.hd);
+        qa = *reinterpret_cast<const uint4*>(rp + o.qa);
+        qb = *reinterpret_cast<const uint4*>(rp + o.qb);
+        form = f;
     }
 };
 
@@ -334,6 +347,10 @@ int gemm_dispatch(int type, const uint16_t* a, const uint16_t* a_lo, int lda, co
                   const float* res, int m, int n, int k, int form, float* part, size_t pf, hipStream_t st) {
     switch (type) {
     case MXH_Q4_K: return gemm_launch<MXH_Q4_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q4_K_TILED:
+        return gemm_launch<MXH_Q4_K_TILED, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q8_0_TILED:
+        return gemm_launch<MXH_Q8_0_TILED, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q5_K: return gemm_launch<MXH_Q5_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q8_0: return gemm_launch<MXH_Q8_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q5_0: return gemm_launch<MXH_Q5_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);

@@ -10,16 +10,39 @@
 #include <stdint.h>
 
 #include "mxh_device.h"
+#include "mxh_types.h"
 
 namespace mxh {
 
 __device__ __forceinline__ uint32_t rd_u8(const uint8_t* p) { return *p; }
 __device__ __forceinline__ uint32_t rd_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
 
-// y[0..31] = elements 32*run .. 32*run+31 of the row starting at rp
+// y[0..31] = elements 32*run .. 32*run+31 of the row starting at rp; the
+// tiled layouts also need the row's block count
 template <int TYPE>
-__device__ __forceinline__ void dequant_run32(const uint8_t* __restrict__ rp, int64_t run, int form, float* y) {
-    if constexpr (TYPE == MXH_Q4_K || TYPE == MXH_Q5_K) {
+__device__ __forceinline__ void dequant_run32(const uint8_t* __restrict__ rp, int64_t run, int form, float* y,
+                                              int64_t row_blocks = 0) {
+    if constexpr (TYPE == MXH_Q4_K_TILED) {
+        const int j = (int)(run & 7);
+        const Q4KTileOffs o = q4k_tile_offsets((run >> 3) * 4 + (j >> 1), row_blocks);
+        const uint8_t* hd = rp + o.hd;
+        uint32_t sc, mn;
+        k4_scale_min(rd_u16(hd + 4) | (rd_u16(hd + 6) << 16), rd_u16(hd + 8) | (rd_u16(hd + 10) << 16),
+                     rd_u16(hd + 12) | (rd_u16(hd + 14) << 16), j, form, sc, mn);
+        const float ds = half_bits_to_float(rd_u16(hd)) * (float)sc, ms = half_bits_to_float(rd_u16(hd + 2)) * (float)mn;
+        const int hi = j & 1;
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) {
+            uint32_t q = rd_u8(rp + (i < 16 ? o.qa + i : o.qb + i - 16));
+            q = hi ? (q >> 4) : (q & 15u);
+            y[i] = ds * (float)q - ms;
+        }
+    } else if constexpr (TYPE == MXH_Q8_0_TILED) {
+        const Q80TileOffs o = q80_tile_offsets(run, row_blocks);
+        const float d = half_bits_to_float(rd_u16(rp + o.d));
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) y[i] = d * (float)(int)(int8_t)rp[i < 16 ? o.lo + i : o.hi + i - 16];
+    } else if constexpr (TYPE == MXH_Q4_K || TYPE == MXH_Q5_K) {
         constexpr int BB = TYPE == MXH_Q4_K ? 144 : 176;
         const int64_t b = run >> 3;
         const int j = (int)(run & 7);  // sub-block: elements 32j..32j+31

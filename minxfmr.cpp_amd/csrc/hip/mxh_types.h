@@ -15,7 +15,18 @@ struct BlockGeom {
     int bytes;
 };
 
-__host__ __device__ constexpr BlockGeom block_geom(int type) {
+// Device-resident layouts that no GGUF file holds: the blocks of each row
+// regrouped in tiles so that the 16-byte loads of one wave instruction read
+// whole cache lines (see q4k_tile_offsets / q80_tile_offsets).  A row keeps
+// the byte count of its GGUF type; the C ABI never accepts these ids.
+constexpr int kTiledFlag = 0x100;
+constexpr int MXH_Q4_K_TILED = kTiledFlag | MXH_Q4_K;
+constexpr int MXH_Q8_0_TILED = kTiledFlag | MXH_Q8_0;
+
+__host__ __device__ constexpr int storage_type(int type) { return type & (kTiledFlag - 1); }
+
+__host__ __device__ constexpr BlockGeom block_geom(int t) {
+    const int type = t == MXH_Q4_K_TILED || t == MXH_Q8_0_TILED ? storage_type(t) : t;
     return type == MXH_Q4_K   ? BlockGeom{256, 144}
            : type == MXH_Q5_K ? BlockGeom{256, 176}
            : type == MXH_Q8_0 ? BlockGeom{32, 34}
@@ -29,6 +40,35 @@ __host__ __device__ constexpr size_t row_bytes(int type, int64_t cols) {
     return block_geom(type).elems == 0 || cols % block_geom(type).elems
                ? 0
                : (size_t)(cols / block_geom(type).elems) * (size_t)block_geom(type).bytes;
+}
+
+// Q4_K tiles of 16 blocks (4096 elements, 2304 bytes; the last tile of a row
+// may hold fewer, nb): the nb 16-byte block headers (d, dmin, scales), then
+// for each 64-element chunk l = 4 b + g of the tile (block b, group g) the
+// first 16 qs bytes of the group, then for each chunk the last 16.  Lane l
+// of a wave reading chunk l thus reads line-contiguous 16-byte pieces.
+struct Q4KTileOffs {
+    uint32_t hd, qa, qb;
+};
+__host__ __device__ constexpr Q4KTileOffs q4k_tile_offsets(int64_t chunk, int64_t nblocks) {
+    const int64_t j = chunk >> 6, l = chunk & 63;
+    const int64_t nb = nblocks - 16 * j < 16 ? nblocks - 16 * j : 16;
+    const uint32_t base = (uint32_t)(j * 2304);
+    return Q4KTileOffs{base + 16u * (uint32_t)(l >> 2), base + 16u * (uint32_t)(nb + l),
+                       base + 16u * (uint32_t)(5 * nb + l)};
+}
+
+// Q8_0 tiles of 64 blocks (2176 bytes; the last may hold fewer, nb): the
+// first 16 quant bytes of each block, then the last 16, then the nb fp16
+// scales.
+struct Q80TileOffs {
+    uint32_t lo, hi, d;
+};
+__host__ __device__ constexpr Q80TileOffs q80_tile_offsets(int64_t block, int64_t nblocks) {
+    const int64_t j = block >> 6, l = block & 63;
+    const int64_t nb = nblocks - 64 * j < 64 ? nblocks - 64 * j : 64;
+    const uint32_t base = (uint32_t)(j * 2176);
+    return Q80TileOffs{base + 16u * (uint32_t)l, base + 16u * (uint32_t)(nb + l), base + (uint32_t)(32 * nb + 2 * l)};
 }
 
 }  // namespace mxh

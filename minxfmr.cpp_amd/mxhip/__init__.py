@@ -50,7 +50,7 @@ class SynthArch(C.Structure):
                                        "ffn_down_type")]
 
 
-MODEL_ROPE_NEOX, MODEL_GGML_FORM, MODEL_NO_QK_NORM, MODEL_NO_GRAPH, MODEL_TOKEN_PREFILL = 1, 4, 8, 16, 32
+MODEL_ROPE_NEOX, MODEL_GGML_FORM, MODEL_NO_QK_NORM, MODEL_NO_GRAPH, MODEL_TOKEN_PREFILL, MODEL_GGUF_LAYOUT = 1, 4, 8, 16, 32, 64
 
 
 def _load() -> C.CDLL:

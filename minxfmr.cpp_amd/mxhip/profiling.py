@@ -1,11 +1,13 @@
 """Workloads to run under rocprofv3 and summaries of what it writes.
 
-    # HBM traffic of the Q4_K dequant-GEMV at the Qwen3-8B decode shapes,
-    # calibrated against a plain device-to-device copy of known size
+    # HBM traffic of the model's Q4_K dequant-GEMVs (tiled weight layout) at
+    # the Qwen3-8B decode shapes, calibrated against a plain device-to-device
+    # copy of known size; MODEL is the bench's synthetic GGUF (bench.py writes
+    # it to $MXH_BENCH_DIR, /tmp by default)
     rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o run --output-format csv -- \
-        python3 -m mxhip.profiling workload
+        python3 -m mxhip.profiling workload MODEL
     rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- \
-        python3 -m mxhip.profiling workload
+        python3 -m mxhip.profiling workload MODEL
     python3 -m mxhip.profiling traffic OUT/fetch OUT/write > summary.md
 
     # per-kernel time table from a --kernel-trace --stats run
@@ -16,11 +18,11 @@
         --output-format csv -- python3 bench.py --steps 1 --warmup 0 --gemv-reps 1 --no-cpu-baseline
     python3 -m mxhip.profiling mfma OUT/mfma
 
-The workload launches each shape `reps` times over rotating weight copies
-(more than the 256 MB Infinity Cache in total) and copies 256 MiB once per
-rep.  FETCH_SIZE and WRITE_SIZE are reported by rocprofv3 in KiB per
-dispatch; the calibration factor is the copy's known byte count divided by
-what the counter reads for it.
+The workload runs every Q4_K GEMV of the model (per layer: fused q|k|v, o,
+fused gate|up, down) `reps` times, as the bench's roofline pass does, and
+copies 256 MiB once per rep.  FETCH_SIZE and WRITE_SIZE are reported by
+rocprofv3 in KiB per dispatch; the calibration factor is the copy's known
+byte count divided by what the counter reads for it.
 """
 from __future__ import annotations
 
@@ -34,6 +36,7 @@ from pathlib import Path
 # Q4_K GEMV shapes of one Qwen3-8B layer (out x in): fused q|k|v, o,
 # fused gate|up, down
 SHAPES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288)]
+N_LAYER = 36
 COPY_BYTES = 256 << 20
 
 
@@ -42,38 +45,21 @@ def algorithmic_bytes(n: int, k: int) -> int:
     return n * k // 256 * 144 + 4 * k + 4 * n
 
 
-def workload(reps: int = 20) -> None:
-    import numpy as np
-
+def workload(path: str, reps: int = 4) -> None:
     import mxhip
 
     mxhip.init(0)
-    rng = np.random.default_rng(1)
+    m = mxhip.Model(path, 64)
     src = mxhip.DeviceBuffer(COPY_BYTES)
     dst = mxhip.DeviceBuffer(COPY_BYTES)
     mxhip.memset(src, 1)
-    for name, n, k in SHAPES:
-        wbytes = mxhip.row_bytes(mxhip.Q4_K, k) * n
-        copies = max(2, (768 << 20) // wbytes)
-        raw = rng.integers(0, 256, wbytes, dtype=np.uint8)
-        raw.reshape(-1, 144)[:, 0:4] = np.frombuffer(np.array([0.01, 0.01], np.float16).tobytes(), np.uint8)
-        bufs = []
-        for _ in range(copies):
-            b = mxhip.DeviceBuffer(wbytes)
-            b.upload(raw)
-            bufs.append(b)
-        x = mxhip.DeviceBuffer.from_array(rng.standard_normal(k, dtype=np.float32))
-        y = mxhip.DeviceBuffer(4 * n)
-        for i in range(reps):
-            mxhip.gemv(mxhip.Q4_K, bufs[i % copies], x, y, n, k)
-        mxhip.synchronize()
-        for b in bufs:
-            b.close()
-        print(f"[workload] {name} {n}x{k}: {reps} launches", file=sys.stderr, flush=True)
     for _ in range(reps):
+        m.bench_gemv(mxhip.Q4_K, 1)
         mxhip.copy(dst, src, COPY_BYTES)
     mxhip.synchronize()
-    print(f"[workload] copy {COPY_BYTES} B x {reps}", file=sys.stderr, flush=True)
+    m.close()
+    print(f"[workload] {reps} passes over the model's Q4_K GEMVs, copy {COPY_BYTES} B each", file=sys.stderr,
+          flush=True)
 
 
 def _counter_rows(d: str):
@@ -114,18 +100,28 @@ def traffic(fetch_dir: str, write_dir: str) -> None:
     kib = COPY_BYTES / 1024
     f_cal = kib / (sum(fetch[copy_name]) / len(fetch[copy_name]))
     w_cal = kib / (sum(write[copy_name]) / len(write[copy_name]))
-    gemv = [n for n in fetch if "gemv_kernel" in n and "Q4K" in n]
-    if len(gemv) != 1:
-        raise SystemExit(f"expected one Q4_K GEMV kernel, found {gemv}")
-    fv, wv = fetch[gemv[0]], write[gemv[0]]
-    reps = len(fv) // len(SHAPES)
+    # Q4_K GEMV dispatches in issue order (both epilogues): per layer q|k|v,
+    # o, gate|up, down; the first pass is skipped (cold instruction and TLB state)
+    rows_f = _counter_rows(fetch_dir)
+    rows_w = _counter_rows(write_dir)
+
+    def ordered(rows, counter):
+        acc: dict[int, float] = {}
+        for r in rows:
+            if r.get("Counter_Name") == counter and "gemv_kernel" in r["Kernel_Name"] and "Q4KT" in r["Kernel_Name"]:
+                acc[int(r["Dispatch_Id"])] = acc.get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
+        return [acc[k] for k in sorted(acc)]
+
+    fv, wv = ordered(rows_f, "FETCH_SIZE"), ordered(rows_w, "WRITE_SIZE")
+    per_pass = 4 * N_LAYER
+    if len(fv) < 2 * per_pass or len(fv) % per_pass or len(wv) != len(fv):
+        raise SystemExit(f"unexpected Q4_K GEMV dispatch count {len(fv)} / {len(wv)}")
     print("| shape (N x K) | algorithmic B | FETCH (scaled) B | WRITE (scaled) B | traffic / algorithmic |")
     print("|---|---:|---:|---:|---:|")
     tot_alg = tot_traffic = 0.0
     for i, (name, n, k) in enumerate(SHAPES):
-        # skip each shape's first launch (cold instruction and TLB state)
-        fs = fv[i * reps + 1:(i + 1) * reps]
-        ws = wv[i * reps + 1:(i + 1) * reps]
+        fs = [fv[j] for j in range(per_pass, len(fv)) if j % 4 == i]
+        ws = [wv[j] for j in range(per_pass, len(wv)) if j % 4 == i]
         fb = sum(fs) / len(fs) * 1024 * f_cal
         wb = sum(ws) / len(ws) * 1024 * w_cal
         alg = algorithmic_bytes(n, k)
@@ -198,7 +194,7 @@ def main(argv: list[str]) -> int:
         return 2
     cmd = argv[0]
     if cmd == "workload":
-        workload(int(argv[1]) if len(argv) > 1 else 20)
+        workload(argv[1], int(argv[2]) if len(argv) > 2 else 4)
     elif cmd == "traffic":
         traffic(argv[1], argv[2])
     elif cmd == "stats":
