@@ -30,6 +30,8 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "mxh_device.h"
 #include "mxh_internal.h"
 
@@ -38,6 +40,7 @@ namespace mxh {
 namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kShortSteps = 3;  // steps per wave of the short form
 constexpr int kThreads = 64 * kWaves;
 
 // sum of the per-wave partials in a fixed order
@@ -674,7 +677,22 @@ __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ 
 //               (transformer.cpp:183-185, 696-704) for i < F
 //  GEMV_ARGMAX: y = logits; each workgroup also leaves its (largest logit,
 //               lowest index) in red_val/red_idx[blockIdx] for argmax_finish
-template <template <int> class T, int R, int MODE, bool SHORT>
+// Consume steps K .. NS-1 of the short form: step K waits until only the
+// (NS - 1 - K) later steps' loads may be outstanding.
+template <int K, int NS, int KL, class F>
+__device__ __forceinline__ void consume_steps(F&& consume_k, int total) {
+    if constexpr (K < NS) {
+        if (K < total) {
+            wait_vmcnt<(NS - 1 - K) * KL>();
+            consume_k(std::integral_constant<int, K>{});
+            consume_steps<K + 1, NS, KL>(consume_k, total);
+        }
+    }
+}
+
+// NS = 0: persistent loop, two steps of loads ahead.  NS > 0: short form,
+// at most NS steps per wave (the launcher sizes the grid for it).
+template <template <int> class T, int R, int MODE, int NS>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     using Ty = T<R>;
     using Buf = typename Ty::Buf;
@@ -786,20 +804,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         }
     };
     Cursor ci{0, 0}, cc{0, 0};
-    Step s0, s1, s2;
-    if constexpr (SHORT) {
-        // At most three steps per wave (the launcher sizes the grid for it):
-        // all of them are issued right after the x loads, so every weight
-        // byte of the wave is in flight during staging, and each step waits
-        // for a fixed count of younger loads, in straight-line code whose
-        // waits the compiler's own analysis leaves alone.
-        constexpr int kL3 = 3 * kL;
-        static_assert(kL3 <= 63, "short form needs three steps of loads in flight");
+    if constexpr (NS > 0) {
+        // All of a wave's steps are issued right after the x loads, so every
+        // weight byte of the wave is in flight during staging, and each step
+        // waits for a fixed count of younger loads, in straight-line code
+        // whose waits the compiler's own analysis leaves alone.
+        static_assert(NS * kL <= 63, "short form: every step's loads in flight at once");
+        Step sb[NS];
         auto issue_all = [&] {
-            issue(ci, s0);
-            issue(ci, s1);
-            issue(ci, s2);
-            wait_vmcnt<kL3>();
+#pragma unroll
+            for (int k = 0; k < NS; ++k) issue(ci, sb[k]);
+            wait_vmcnt<NS * kL>();
         };
         if constexpr (Ty::kIntX) {
             stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
@@ -807,18 +822,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             issue_all();
             stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
-        wait_vmcnt<2 * kL>();
-        consume(cc, s0);
-        if (total > 1) {
-            wait_vmcnt<kL>();
-            consume(cc, s1);
-        }
-        if (total > 2) {
-            wait_vmcnt<0>();
-            consume(cc, s2);
-        }
+        consume_steps<0, NS, kL>([&](auto kc) { consume(cc, sb[decltype(kc)::value]); }, total);
         wait_vmcnt<0>();  // loads of steps past the end
     } else {
+        Step s0, s1, s2;
         // the first two steps' weight loads do not depend on x: they are
         // issued right after the x loads, so both latencies overlap, and the
         // staging arithmetic waits for x only
@@ -961,32 +968,40 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const size_t lds = T<R>::kIntX ? (size_t)(2 * limb_dwords(a.k) + a.k / 32 + a.k / 16) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
     const int n_cu = device_cus();
-    // Short form: when every wave can finish in at most three steps with a
+    // Short form: when every wave can finish in at most NS steps with a
     // resident grid, one workgroup per CU where that suffices (x is staged
-    // and quantized once per CU), more where three steps per wave need it.
-    constexpr bool kShortOk = 3 * (T<R>::kLoads * R + R) <= 63;
-    if constexpr (kShortOk) {
+    // and quantized once per CU), more where NS steps per wave need it.
+    constexpr int kLmax = T<R>::kLoads * R + R;  // loads per step, residual included
+    if constexpr (3 * kLmax <= 63) {
         if (mode != GEMV_ARGMAX && grid_cap <= 0 && cpl <= 3) {
-            const int64_t per_wg = (int64_t)kWaves * (3 / cpl);
-            const int64_t min_grid = (n_groups + per_wg - 1) / per_wg;
-            int64_t grid = need < n_cu ? need : n_cu;
-            if (grid < min_grid) grid = min_grid;
-            const void* ks = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, true>
-                                                : (const void*)gemv_kernel<T, R, GEMV_SILU, true>;
-            if (grid <= resident_grid(ks, lds)) {
-                if (mode == GEMV_PLAIN)
-                    hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, true>), dim3((unsigned)grid), dim3(kThreads), lds,
-                                       st, a);
-                else
-                    hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, true>), dim3((unsigned)grid), dim3(kThreads), lds,
-                                       st, a);
-                return MXH_OK;
-            }
+            auto try_short = [&](auto nsc) -> bool {
+                constexpr int NSv = decltype(nsc)::value;
+                if constexpr (NSv * kLmax > 63) {
+                    return false;
+                } else {
+                    if (NSv < cpl) return false;  // a row group's chunk steps exceed the form
+                    const int64_t per_wg = (int64_t)kWaves * (NSv / cpl);
+                    const int64_t min_grid = (n_groups + per_wg - 1) / per_wg;
+                    int64_t grid = need < n_cu ? need : n_cu;
+                    if (grid < min_grid) grid = min_grid;
+                    const void* ks = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, NSv>
+                                                        : (const void*)gemv_kernel<T, R, GEMV_SILU, NSv>;
+                    if (grid > resident_grid(ks, lds)) return false;
+                    if (mode == GEMV_PLAIN)
+                        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, NSv>), dim3((unsigned)grid), dim3(kThreads),
+                                           lds, st, a);
+                    else
+                        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, NSv>), dim3((unsigned)grid), dim3(kThreads),
+                                           lds, st, a);
+                    return true;
+                }
+            };
+            if (try_short(std::integral_constant<int, kShortSteps>{})) return MXH_OK;
         }
     }
-    const void* kern = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, false>
-                       : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU, false>
-                                           : (const void*)gemv_kernel<T, R, GEMV_ARGMAX, false>;
+    const void* kern = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, 0>
+                       : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU, 0>
+                                           : (const void*)gemv_kernel<T, R, GEMV_ARGMAX, 0>;
     int cap = grid_cap > 0 ? grid_cap : resident_grid(kern, lds);
     // Short runs (a few row groups per wave with one workgroup per CU): one
     // workgroup per CU, so x is staged and quantized once per CU and no CU
@@ -996,12 +1011,12 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
         cap = n_cu;
     const unsigned grid = (unsigned)(need < cap ? need : cap);
     if (mode == GEMV_PLAIN)
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, false>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, 0>), dim3(grid), dim3(kThreads), lds, st, a);
     else if (mode == GEMV_SILU)
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, false>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, 0>), dim3(grid), dim3(kThreads), lds, st, a);
     else {
         if ((int)grid > a.red_cap) return MXH_ERR_ARG;
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, false>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, 0>), dim3(grid), dim3(kThreads), lds, st, a);
         hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, st, a.red_val, a.red_idx, (int)grid, a.tokens,
                            a.pos);
     }
@@ -1018,7 +1033,7 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.tokens || !a.pos)) return MXH_ERR_ARG;
     switch (type) {
     case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);
-    case MXH_Q4_K_TILED: return launch_gemv<Q4KT, 4>(a, mode, st);
+    case MXH_Q4_K_TILED: return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
     case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
