@@ -129,6 +129,25 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // wave-wide sum / max broadcast to every lane
+// v of lane (lane ^ OFF) within the wave, OFF in {4, 8, 16, 32}: VALU lane
+// swaps for 16 and 32 (v_permlane16/32_swap: the first result holds, for the
+// odd rows / upper half, the swapped-in values, the second for the others),
+// a row rotation for 8
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v) {
+    if constexpr (OFF == 32) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((threadIdx.x & 32) ? p[0] : p[1]);
+    } else if constexpr (OFF == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((threadIdx.x & 16) ? p[0] : p[1]);
+    } else if constexpr (OFF == 8) {
+        return dpp_f<0x128>(v);  // row_ror:8 (i + 8 mod 16 == i ^ 8)
+    } else {
+        return __shfl_xor(v, OFF, 64);
+    }
+}
+
 __device__ __forceinline__ float wave_sum_all(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_lane63(v)), 63));
 }

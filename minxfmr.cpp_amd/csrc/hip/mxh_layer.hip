@@ -119,6 +119,16 @@ __device__ __forceinline__ void half8_to_float(const uint4& raw, float* f) {
     }
 }
 
+// sum over the lanes of a wave with the same lane % LPP (the position
+// groups), with VALU lane swaps where the offsets allow
+template <int LPP>
+__device__ __forceinline__ float fold_position_groups(float v) {
+    if constexpr (LPP <= 4) v += lane_xor<4>(v);
+    if constexpr (LPP <= 8) v += lane_xor<8>(v);
+    if constexpr (LPP <= 16) v += lane_xor<16>(v);
+    return v + lane_xor<32>(v);
+}
+
 // Decode attention for kv head g over the L = pos+1 positions
 // (transformer.cpp:529-629), head_dim = 8 * LPP.
 //
@@ -285,12 +295,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     for (int h = 0; h < kAttnMaxGroup; ++h) {
         if (h >= group) break;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = acc[h][e];
-#pragma unroll
-            for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-            acc[h][e] = v;
-        }
+        for (int e = 0; e < 8; ++e) acc[h][e] = fold_position_groups<LPP>(acc[h][e]);
         if (lane < LPP) {
             float4* dst = reinterpret_cast<float4*>(&red[wave][h][sub * 8]);
             dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
@@ -323,6 +328,22 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     if (tid == 0) last = add_agent(a.counter + g, 1) == sact - 1;
     __syncthreads();
     if (!last) return;
+    // (q head, 4 dims) items; the splits of an item are shared by `per`
+    // threads.  The first kPre splits of each thread are requested together
+    // with the (max, sum) pairs, so most merges cost one memory round trip.
+    constexpr int kPre = 8;
+    const int items = group * HD / 4, per = 256 / items;
+    const int item = tid % items, part = tid / items;
+    const int hi = item / (HD / 4), d4 = item % (HD / 4);
+    const float* src = part_v + ((size_t)g * group + hi) * S * HD + 4 * d4;
+    float4 pre[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        const int i = part + per * k;
+        const float* q = src + (size_t)i * HD;
+        pre[k] = part < per && i < sact ? make_float4(ld_agent(q), ld_agent(q + 1), ld_agent(q + 2), ld_agent(q + 3))
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     for (int h = wave; h < group; h += 4) {
         const float* ml = part_ml + ((size_t)g * group + h) * S * 2;
         const float mi = lane < sact ? ld_agent(ml + 2 * lane) : -INFINITY;
@@ -333,17 +354,23 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         wgt[h][lane] = wi / den;
     }
     __syncthreads();
-    // (q head, 4 dims) items; the splits of an item are shared by `per` threads
-    const int items = group * HD / 4, per = 256 / items;
-    const int item = tid % items, part = tid / items;
     float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
     if (part < per) {
-        const int h = item / (HD / 4), d4 = item % (HD / 4);
-        const float* src = part_v + ((size_t)g * group + h) * S * HD + 4 * d4;
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int i = part + per * k;
+            if (i < sact) {
+                const float w = wgt[hi][i];
+                s4.x = fmaf(w, pre[k].x, s4.x);
+                s4.y = fmaf(w, pre[k].y, s4.y);
+                s4.z = fmaf(w, pre[k].z, s4.z);
+                s4.w = fmaf(w, pre[k].w, s4.w);
+            }
+        }
 #pragma unroll 4
-        for (int i = part; i < sact; i += per) {
+        for (int i = part + per * kPre; i < sact; i += per) {
             const float* q = src + (size_t)i * HD;
-            const float w = wgt[h][i];
+            const float w = wgt[hi][i];
             s4.x = fmaf(w, ld_agent(q), s4.x);
             s4.y = fmaf(w, ld_agent(q + 1), s4.y);
             s4.z = fmaf(w, ld_agent(q + 2), s4.z);
