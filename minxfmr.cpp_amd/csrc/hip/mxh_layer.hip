@@ -224,6 +224,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             acc[h][e] = 0.f;
         }
 
+    // scores in base-2 units (exp(x - m) == exp2(x log2 e - m log2 e)): the
+    // running max and the split maxima below are in the same units
+    const float scale2 = a.scale * 1.4426950408889634f;
     for (int c = s; c < nch; c += S) {
         if (c == own_chunk) {
 #pragma unroll
@@ -246,7 +249,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
                 d = lane_group_sum<LPP>(d);
-                if (sub == 0) sc[h][jl] = j < L ? d * a.scale : -INFINITY;
+                if (sub == 0) sc[h][jl] = j < L ? d * scale2 : -INFINITY;
             }
         }
         if (c + S < nch) load(kraw, a.kc, c + S);
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int h = wave; h < group; h += 4) {
             const float sv = sc[h][lane];
             const float mo = run_m[h], mn = fmaxf(mo, wave_max_all(sv));
-            const float p = expf(sv - mn), al = expf(mo - mn);
+            const float p = __builtin_amdgcn_exp2f(sv - mn), al = __builtin_amdgcn_exp2f(mo - mn);
             const float ps = wave_sum_all(p);
             sc[h][lane] = p;
             if (lane == 0) {
@@ -349,7 +352,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         const float mi = lane < sact ? ld_agent(ml + 2 * lane) : -INFINITY;
         const float li = lane < sact ? ld_agent(ml + 2 * lane + 1) : 0.f;
         const float M = wave_max_all(mi);
-        const float wi = lane < sact ? expf(mi - M) : 0.f;
+        const float wi = lane < sact ? __builtin_amdgcn_exp2f(mi - M) : 0.f;
         const float den = wave_sum_all(wi * li);
         wgt[h][lane] = wi / den;
     }
