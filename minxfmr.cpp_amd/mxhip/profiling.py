@@ -92,27 +92,37 @@ def _per_dispatch(rows, counter: str, reduce=None):
 
 
 def traffic(fetch_dir: str, write_dir: str) -> None:
-    fetch = _per_dispatch(_counter_rows(fetch_dir), "FETCH_SIZE")
-    write = _per_dispatch(_counter_rows(write_dir), "WRITE_SIZE")
-    copy_name = next((n for n in fetch if "copy" in n.lower()), None)
-    if copy_name is None:
-        raise SystemExit("no copy dispatch found")
-    kib = COPY_BYTES / 1024
-    f_cal = kib / (sum(fetch[copy_name]) / len(fetch[copy_name]))
-    w_cal = kib / (sum(write[copy_name]) / len(write[copy_name]))
-    # Q4_K GEMV dispatches in issue order (both epilogues): per layer q|k|v,
-    # o, gate|up, down; the first pass is skipped (cold instruction and TLB state)
     rows_f = _counter_rows(fetch_dir)
     rows_w = _counter_rows(write_dir)
 
-    def ordered(rows, counter):
+    def ordered(rows, counter, pick):
         acc: dict[int, float] = {}
         for r in rows:
-            if r.get("Counter_Name") == counter and "gemv_kernel" in r["Kernel_Name"] and "Q4KT" in r["Kernel_Name"]:
+            if r.get("Counter_Name") == counter and pick(r["Kernel_Name"]):
                 acc[int(r["Dispatch_Id"])] = acc.get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
-        return [acc[k] for k in sorted(acc)]
+        return sorted(acc.items())
 
-    fv, wv = ordered(rows_f, "FETCH_SIZE"), ordered(rows_w, "WRITE_SIZE")
+    def is_gemv(n):
+        return "gemv_kernel" in n and "Q4KT" in n
+
+    def is_copy(n):
+        return "copy" in n.lower()
+
+    # Q4_K GEMV dispatches in issue order (both epilogues): per layer q|k|v,
+    # o, gate|up, down; the first pass is skipped (cold instruction and TLB
+    # state).  The calibration copies are the copy dispatches after the first
+    # GEMV (model loading also issues small copies).
+    gf, gw = ordered(rows_f, "FETCH_SIZE", is_gemv), ordered(rows_w, "WRITE_SIZE", is_gemv)
+    if not gf or not gw:
+        raise SystemExit("no Q4_K GEMV dispatch found")
+    cf = [v for k, v in ordered(rows_f, "FETCH_SIZE", is_copy) if k > gf[0][0]]
+    cw = [v for k, v in ordered(rows_w, "WRITE_SIZE", is_copy) if k > gw[0][0]]
+    if not cf or not cw:
+        raise SystemExit("no calibration copy found")
+    kib = COPY_BYTES / 1024
+    copy_f, copy_w = sum(cf) / len(cf), sum(cw) / len(cw)
+    f_cal, w_cal = kib / copy_f, kib / copy_w
+    fv, wv = [v for _, v in gf], [v for _, v in gw]
     per_pass = 4 * N_LAYER
     if len(fv) < 2 * per_pass or len(fv) % per_pass or len(wv) != len(fv):
         raise SystemExit(f"unexpected Q4_K GEMV dispatch count {len(fv)} / {len(wv)}")
@@ -131,8 +141,7 @@ def traffic(fetch_dir: str, write_dir: str) -> None:
     print(f"| mean per launch | {tot_alg / len(SHAPES):,.0f} | | | {tot_traffic / tot_alg:.3f} |")
     print()
     print(f"Calibration: a {COPY_BYTES:,} B device-to-device copy reads FETCH_SIZE "
-          f"{sum(fetch[copy_name]) / len(fetch[copy_name]):,.0f} KiB and WRITE_SIZE "
-          f"{sum(write[copy_name]) / len(write[copy_name]):,.0f} KiB per dispatch; factors "
+          f"{copy_f:,.0f} KiB and WRITE_SIZE {copy_w:,.0f} KiB per dispatch; factors "
           f"{f_cal:.4f} (fetch) and {w_cal:.4f} (write) are applied above.")
     print(f"TRAFFIC_PER_LAUNCH_BYTES={tot_traffic / len(SHAPES):.0f}")
 
