@@ -339,6 +339,24 @@ struct Q5K {
     }
 };
 
+// Q5_K in the tiled device layout (q5k_tile_offsets)
+template <int R>
+struct Q5KT : Q5K<R> {
+    static constexpr int kType = MXH_Q5_K_TILED;
+    using Buf = typename Q5K<R>::Buf;
+    static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
+        const Q5KTileOffs o = q5k_tile_offsets(c, (int64_t)(rb / 176));
+        const int h = c & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t* rp = w + (size_t)rows[r] * rb;
+            b.hd[r] = ldg16(rp + o.hd);
+            b.qh[r] = ldg16(rp + o.qh + 16 * h);
+            b.qs[r] = ldg16(rp + o.qs);
+        }
+    }
+};
+
 template <int R>
 struct Q80 {
     static constexpr int kType = MXH_Q8_0;
@@ -1035,6 +1053,7 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);
     case MXH_Q4_K_TILED: return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
+    case MXH_Q5_K_TILED: return launch_gemv<Q5KT, 4>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
     case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
     case MXH_Q5_0: return launch_gemv<Q50, 4>(a, mode, st);

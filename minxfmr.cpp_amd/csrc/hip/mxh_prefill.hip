@@ -351,6 +351,8 @@ int gemm_dispatch(int type, const uint16_t* a, const uint16_t* a_lo, int lda, co
         return gemm_launch<MXH_Q4_K_TILED, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q8_0_TILED:
         return gemm_launch<MXH_Q8_0_TILED, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q5_K_TILED:
+        return gemm_launch<MXH_Q5_K_TILED, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q5_K: return gemm_launch<MXH_Q5_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q8_0: return gemm_launch<MXH_Q8_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q5_0: return gemm_launch<MXH_Q5_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);

@@ -37,6 +37,24 @@ __device__ __forceinline__ void dequant_run32(const uint8_t* __restrict__ rp, in
             q = hi ? (q >> 4) : (q & 15u);
             y[i] = ds * (float)q - ms;
         }
+    } else if constexpr (TYPE == MXH_Q5_K_TILED) {
+        const int j = (int)(run & 7);  // sub-block: the low (even j) or high nibbles of 64-group j/2
+        const Q5KTileOffs o = q5k_tile_offsets((run >> 3) * 8 + 2 * (j >> 1), row_blocks);
+        const uint8_t* hd = rp + o.hd;
+        uint32_t sc, mn;
+        k4_scale_min(rd_u16(hd + 4) | (rd_u16(hd + 6) << 16), rd_u16(hd + 8) | (rd_u16(hd + 10) << 16),
+                     rd_u16(hd + 12) | (rd_u16(hd + 14) << 16), j, form, sc, mn);
+        const float ds = half_bits_to_float(rd_u16(hd)) * (float)sc, ms = half_bits_to_float(rd_u16(hd + 2)) * (float)mn;
+        const int hi = j & 1;
+        const uint8_t* qs = rp + o.qs;  // the group's 32 qs bytes: chunks 2g and 2g+1, adjacent
+        const uint8_t* qh = rp + o.qh;
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) {
+            uint32_t q = rd_u8(qs + i);
+            q = hi ? (q >> 4) : (q & 15u);
+            q |= ((rd_u8(qh + i) >> j) & 1u) << 4;
+            y[i] = ds * (float)q - ms;
+        }
     } else if constexpr (TYPE == MXH_Q8_0_TILED) {
         const Q80TileOffs o = q80_tile_offsets(run, row_blocks);
         const float d = half_bits_to_float(rd_u16(rp + o.d));

@@ -1,5 +1,5 @@
 // mxh_repack.hip — in-place regrouping of device weight rows into the tiled
-// layouts of mxh_types.h (q4k_tile_offsets, q80_tile_offsets).
+// layouts of mxh_types.h (q4k_tile_offsets, q5k_tile_offsets, q80_tile_offsets).
 //
 // A GGUF Q4_K row interleaves 16 header bytes and 128 quant bytes per block,
 // so the 16-byte loads of one wave instruction (one 64-element chunk per
@@ -27,7 +27,7 @@ __device__ __forceinline__ uint4 lds_u16x8(const uint8_t* p) {  // 2-aligned 16 
 template <int TYPE>
 __global__ __launch_bounds__(256) void tile_rows_kernel(uint8_t* __restrict__ w, int64_t rows, int nblocks) {
     extern __shared__ __align__(16) uint8_t row_buf[];
-    constexpr int BB = TYPE == MXH_Q4_K ? 144 : 34;
+    constexpr int BB = TYPE == MXH_Q4_K ? 144 : TYPE == MXH_Q5_K ? 176 : 34;
     const size_t rb = (size_t)nblocks * BB;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         uint8_t* rp = w + (size_t)r * rb;
@@ -42,6 +42,18 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(uint8_t* __restrict__ w,
                 if (g == 0) *reinterpret_cast<uint4*>(rp + o.hd) = *reinterpret_cast<const uint4*>(src);
                 *reinterpret_cast<uint4*>(rp + o.qa) = *reinterpret_cast<const uint4*>(src + 16 + 32 * g);
                 *reinterpret_cast<uint4*>(rp + o.qb) = *reinterpret_cast<const uint4*>(src + 32 + 32 * g);
+            }
+        } else if constexpr (TYPE == MXH_Q5_K) {
+            for (int c = threadIdx.x; c < 8 * nblocks; c += blockDim.x) {
+                const Q5KTileOffs o = q5k_tile_offsets(c, nblocks);
+                const uint8_t* src = row_buf + (size_t)(c >> 3) * 176;
+                const int p = c & 7;
+                if (p == 0) {
+                    *reinterpret_cast<uint4*>(rp + o.hd) = *reinterpret_cast<const uint4*>(src);
+                    *reinterpret_cast<uint4*>(rp + o.qh) = *reinterpret_cast<const uint4*>(src + 16);
+                    *reinterpret_cast<uint4*>(rp + o.qh + 16) = *reinterpret_cast<const uint4*>(src + 32);
+                }
+                *reinterpret_cast<uint4*>(rp + o.qs) = *reinterpret_cast<const uint4*>(src + 48 + 16 * p);
             }
         } else {
             for (int b = threadIdx.x; b < nblocks; b += blockDim.x) {
@@ -63,6 +75,7 @@ int tiled_type(int type, int64_t cols) {
     // are 16-byte aligned, as the tiled loads need, when K is a multiple of 256
     if (type == MXH_Q4_K && cols % 256 == 0 && cols <= 15360) return MXH_Q4_K_TILED;
     if (type == MXH_Q8_0 && cols % 256 == 0 && cols <= 15360) return MXH_Q8_0_TILED;
+    if (type == MXH_Q5_K && cols % 256 == 0 && cols <= 15360) return MXH_Q5_K_TILED;
     return type;
 }
 
@@ -73,6 +86,8 @@ int tile_rows_launch(int type, void* w, int64_t rows, int64_t cols, hipStream_t 
     const unsigned grid = (unsigned)(rows < 4096 ? rows : 4096);
     if (type == MXH_Q4_K)
         hipLaunchKernelGGL(tile_rows_kernel<MXH_Q4_K>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
+    else if (type == MXH_Q5_K)
+        hipLaunchKernelGGL(tile_rows_kernel<MXH_Q5_K>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
     else
         hipLaunchKernelGGL(tile_rows_kernel<MXH_Q8_0>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
     return hipGetLastError() == hipSuccess ? MXH_OK : MXH_ERR_HIP;

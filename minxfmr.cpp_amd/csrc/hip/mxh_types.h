@@ -22,11 +22,12 @@ struct BlockGeom {
 constexpr int kTiledFlag = 0x100;
 constexpr int MXH_Q4_K_TILED = kTiledFlag | MXH_Q4_K;
 constexpr int MXH_Q8_0_TILED = kTiledFlag | MXH_Q8_0;
+constexpr int MXH_Q5_K_TILED = kTiledFlag | MXH_Q5_K;
 
 __host__ __device__ constexpr int storage_type(int type) { return type & (kTiledFlag - 1); }
 
 __host__ __device__ constexpr BlockGeom block_geom(int t) {
-    const int type = t == MXH_Q4_K_TILED || t == MXH_Q8_0_TILED ? storage_type(t) : t;
+    const int type = t == MXH_Q4_K_TILED || t == MXH_Q8_0_TILED || t == MXH_Q5_K_TILED ? storage_type(t) : t;
     return type == MXH_Q4_K   ? BlockGeom{256, 144}
            : type == MXH_Q5_K ? BlockGeom{256, 176}
            : type == MXH_Q8_0 ? BlockGeom{32, 34}
@@ -56,6 +57,21 @@ __host__ __device__ constexpr Q4KTileOffs q4k_tile_offsets(int64_t chunk, int64_
     const uint32_t base = (uint32_t)(j * 2304);
     return Q4KTileOffs{base + 16u * (uint32_t)(l >> 2), base + 16u * (uint32_t)(nb + l),
                        base + 16u * (uint32_t)(5 * nb + l)};
+}
+
+// Q5_K tiles of 8 blocks (64 chunks of 32 elements, 1408 bytes; the last may
+// hold fewer, nb): the nb 16-byte headers, the nb 32-byte high-bit planes
+// (qh), then for each 32-element chunk l = 8 b + p the 16 qs bytes it reads
+// (qs bytes 16p..16p+15 of block b).
+struct Q5KTileOffs {
+    uint32_t hd, qh, qs;
+};
+__host__ __device__ constexpr Q5KTileOffs q5k_tile_offsets(int64_t chunk, int64_t nblocks) {
+    const int64_t j = chunk >> 6, l = chunk & 63;
+    const int64_t nb = nblocks - 8 * j < 8 ? nblocks - 8 * j : 8;
+    const uint32_t base = (uint32_t)(j * 1408);
+    return Q5KTileOffs{base + 16u * (uint32_t)(l >> 3), base + 16u * (uint32_t)nb + 32u * (uint32_t)(l >> 3),
+                       base + 16u * (uint32_t)(3 * nb + l)};
 }
 
 // Q8_0 tiles of 64 blocks (2176 bytes; the last may hold fewer, nb): the

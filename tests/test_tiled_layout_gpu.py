@@ -5,7 +5,8 @@ wave's 16-byte loads read whole cache lines; the arithmetic on the bytes is
 unchanged.  Opening the same file with MXH_MODEL_GGUF_LAYOUT keeps the GGUF
 block order, and both must give bit-identical logits and greedy ids, through
 the batched prefill (matrix-core GEMM) and the decode step (GEMV), including
-rows whose last tile is partial (K = 4608: 18 Q4_K blocks, tiles of 16 and 2).
+rows whose last tile is partial (K = 4608: 18 Q4_K blocks, tiles of 16 and 2;
+Q5_K tiles of 8, 8 and 2).
 """
 from __future__ import annotations
 
@@ -23,6 +24,10 @@ CASES = {
     "q4k-mixed-q5k": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K, qk_norm=False,
                           attn_v_type=mxhip.Q5_K, ffn_down_type=mxhip.Q5_K, arch="llama", rope_theta=5e5),
     "q4k-partial-tiles": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True,
+                              n_embd=512, n_ff=4608, head_dim=128),
+    # Q5_K down projection with K = 4608: 18 blocks, tiles of 8, 8 and 2
+    "q5k-partial-tiles": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K, qk_norm=False,
+                              attn_v_type=mxhip.Q5_K, ffn_down_type=mxhip.Q5_K, arch="llama", rope_theta=5e5,
                               n_embd=512, n_ff=4608, head_dim=128),
 }
 
