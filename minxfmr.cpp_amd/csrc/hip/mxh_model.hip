@@ -32,7 +32,7 @@ struct DevW {
 
 struct Layer {
     DevW qkv;         // fused [Wq; Wk; Wv] when all three share a type
-    DevW q, k, v;     // otherwise separate
+    DevW q, k, v;     // otherwise separate (q covering k too, and k empty, when only q and k share a type)
     bool qkv_fused = false;
     DevW o, gu, g, u, down;
     bool gu_fused = false;
@@ -121,7 +121,7 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
             rc |= gemv(L.qkv, m->x, m->qkv, nullptr, m->form, st, L.attn_norm, c.eps);
         } else {
             rc |= gemv(L.q, m->x, m->qkv, nullptr, m->form, st, L.attn_norm, c.eps);
-            rc |= gemv(L.k, m->x, m->qkv + qd, nullptr, m->form, st, L.attn_norm, c.eps);
+            if (L.k.p) rc |= gemv(L.k, m->x, m->qkv + qd, nullptr, m->form, st, L.attn_norm, c.eps);
             rc |= gemv(L.v, m->x, m->qkv + qd + kvd, nullptr, m->form, st, L.attn_norm, c.eps);
         }
         AttnArgs aa{};
@@ -300,7 +300,7 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     struct LOff {
         size_t qkv, q, k, v, o, gu, g, u, down, an, fn, qn, kn, bias;
         const GgufTensor *tq, *tk, *tv, *to, *tg, *tu, *td, *bq, *bk, *bv;
-        bool fq, fgu;
+        bool fq, fqk, fgu;
     };
     std::vector<LOff> lo((size_t)c.n_layer);
     for (int l = 0; l < c.n_layer; ++l) {
@@ -318,11 +318,16 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
         for (const GgufTensor* t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
             if (!gemv_type_ok(t->type)) return fail(MXH_ERR_UNSUPPORTED, t->name + ": unsupported type " + std::to_string(t->type));
         L.fq = L.tq->type == L.tk->type && L.tk->type == L.tv->type;
+        L.fqk = !L.fq && L.tq->type == L.tk->type;  // q and k rows share one GEMV, v has its own type
         if (L.fq) {
             L.qkv = put_run({L.tq, L.tk, L.tv});
         } else {
-            L.q = put(L.tq);
-            L.k = put(L.tk);
+            if (L.fqk) {
+                L.q = put_run({L.tq, L.tk});
+            } else {
+                L.q = put(L.tq);
+                L.k = put(L.tk);
+            }
             L.v = put(L.tv);
         }
         L.o = put(L.to);
@@ -383,8 +388,9 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
         D.qkv_fused = L.fq;
         if (L.fq) D.qkv = dw(L.qkv, L.tq->type, qd + 2 * kvd, c.n_embd);
         else {
-            D.q = dw(L.q, L.tq->type, qd, c.n_embd);
-            D.k = dw(L.k, L.tk->type, kvd, c.n_embd);
+            // with q and k fused, D.q covers both row ranges and D.k is empty
+            D.q = dw(L.q, L.tq->type, L.fqk ? qd + kvd : qd, c.n_embd);
+            if (!L.fqk) D.k = dw(L.k, L.tk->type, kvd, c.n_embd);
             D.v = dw(L.v, L.tv->type, kvd, c.n_embd);
         }
         D.o = dw(L.o, L.to->type, c.n_embd, qd);
@@ -592,7 +598,7 @@ int enqueue_prefill_chunk(mxh_model* m, int p0, int rows, hipStream_t st) {
             rc |= gemm(m, L.qkv, d, m->pf_qkv, ldq, nullptr, rows, st);
         } else {
             rc |= gemm(m, L.q, d, m->pf_qkv, ldq, nullptr, rows, st);
-            rc |= gemm(m, L.k, d, m->pf_qkv + qd, ldq, nullptr, rows, st);
+            if (L.k.p) rc |= gemm(m, L.k, d, m->pf_qkv + qd, ldq, nullptr, rows, st);
             rc |= gemm(m, L.v, d, m->pf_qkv + qd + kvd, ldq, nullptr, rows, st);
         }
         rc |= qkv_prep_rows_launch(m->pf_qkv, ldq, L.bias, L.q_norm, L.k_norm, m->rope_cs, p0, rows, m->pf_q, L.kc,
