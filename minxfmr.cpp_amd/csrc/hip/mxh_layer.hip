@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     // (q head, 4 dims) items; the splits of an item are shared by `per`
     // threads.  The first kPre splits of each thread are requested together
     // with the (max, sum) pairs, so most merges cost one memory round trip.
-    constexpr int kPre = 8;
+    constexpr int kPre = 16;
     const int items = group * HD / 4, per = 256 / items;
     const int item = tid % items, part = tid / items;
     const int hi = item / (HD / 4), d4 = item % (HD / 4);
