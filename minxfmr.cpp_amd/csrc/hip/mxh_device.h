@@ -190,6 +190,19 @@ __device__ __forceinline__ void st_agent(int* p, int v) {
 __device__ __forceinline__ int add_agent(int* p, int v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16-byte load with the cache policy of ld_agent (sc1, as agent-scope atomic
+// loads carry it) through a buffer descriptor over [base, base + bytes): one
+// instruction where four ld_agent would be four.  Descriptor dword 3 is the
+// CDNA raw-buffer setting (32-bit data format); out-of-range offsets read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 ld_agent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* sc1 */));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // wait until every memory operation this thread issued has completed
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 

@@ -338,13 +338,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     const int items = group * HD / 4, per = 256 / items;
     const int item = tid % items, part = tid / items;
     const int hi = item / (HD / 4), d4 = item % (HD / 4);
-    const float* src = part_v + ((size_t)g * group + hi) * S * HD + 4 * d4;
+    // byte offsets into the V partials, read as 16-byte agent-coherent loads
+    const __amdgpu_buffer_rsrc_t prs = agent_rsrc(part_v, (int)((size_t)a.nh * S * HD * sizeof(float)));
+    const int src = (int)((((size_t)g * group + hi) * S * HD + 4 * d4) * sizeof(float));
     float4 pre[kPre];
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
         const int i = part + per * k;
-        const float* q = src + (size_t)i * HD;
-        pre[k] = part < per && i < sact ? make_float4(ld_agent(q), ld_agent(q + 1), ld_agent(q + 2), ld_agent(q + 3))
+        pre[k] = part < per && i < sact ? ld_agent4(prs, src + i * HD * (int)sizeof(float))
                                         : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     for (int h = wave; h < group; h += 4) {
@@ -370,14 +371,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
                 s4.w = fmaf(w, pre[k].w, s4.w);
             }
         }
-#pragma unroll 4
+#pragma unroll 8
         for (int i = part + per * kPre; i < sact; i += per) {
-            const float* q = src + (size_t)i * HD;
+            const float4 v = ld_agent4(prs, src + i * HD * (int)sizeof(float));
             const float w = wgt[hi][i];
-            s4.x = fmaf(w, ld_agent(q), s4.x);
-            s4.y = fmaf(w, ld_agent(q + 1), s4.y);
-            s4.z = fmaf(w, ld_agent(q + 2), s4.z);
-            s4.w = fmaf(w, ld_agent(q + 3), s4.w);
+            s4.x = fmaf(w, v.x, s4.x);
+            s4.y = fmaf(w, v.y, s4.y);
+            s4.z = fmaf(w, v.z, s4.z);
+            s4.w = fmaf(w, v.w, s4.w);
         }
     }
     float4* r4 = reinterpret_cast<float4*>(&red[0][0][0]);  // 256 float4 fit: 4 * 8 * HD floats >= 1024
