@@ -131,6 +131,14 @@ int mxh_host_matmul_rhs_t(int type, const float *a, int64_t m, int64_t k, const 
  * operands (cuda_backend.h:24). */
 int mxh_host_matmul_f32(const float *a, const float *b, float *out, int64_t m, int64_t k, int64_t n);
 
+/* out[m x n] = A[m x k] . dequant(B[k x n]) with B quantized along its rows
+ * (each of its k rows holds n columns as `type` blocks; F32 accepted too).
+ * B is cached on the device keyed by (host pointer, b_bytes), decoded there
+ * bit-exactly to fp32 and multiplied in fp32.  Replaces cuda_backend_matmul
+ * for quantized B (cuda_backend.h:24; CPU semantics cpu_backend.cpp:119-200). */
+int mxh_host_matmul_q(int type, const float *a, int64_t m, int64_t k, const void *b, size_t b_bytes, int64_t n,
+                      float *out, int form);
+
 /* out[n] = sum_k vec[k] * mat[k * stride + n].
  * Replaces cuda_backend_matvec_strided (cuda_backend.h:26). */
 int mxh_host_matvec_strided(const float *vec, const float *mat, float *out, size_t K, size_t N, size_t stride);

@@ -294,7 +294,7 @@ int mxh_host_matmul_rhs_t(int type, const float* a, int64_t m, int64_t k, const 
     const size_t rb = type >= kTiledFlag ? 0 : row_bytes(type, k);
     if (!rb || w_bytes < rb * (size_t)n) return set_error(MXH_ERR_ARG, "matmul_rhs_t: weight bytes too small");
     const void* dw = nullptr;
-    if (int rc = device_weight(w, rb * (size_t)n, &dw)) return rc;
+    if (int rc = device_weight(w, w_bytes, &dw)) return rc;  // the key mxh_preload(w, w_bytes) uses
     void *da = nullptr, *dout = nullptr;
     if (int rc = stage(0, sizeof(float) * (size_t)(m * k), &da)) return rc;
     if (int rc = stage(1, sizeof(float) * (size_t)(m * n), &dout)) return rc;
@@ -321,11 +321,37 @@ int mxh_host_matmul_f32(const float* a, const float* b, float* out, int64_t m, i
     return check_hip(hipStreamSynchronize(g_ctx.stream), "matmul");
 }
 
+int mxh_host_matmul_q(int type, const float* a, int64_t m, int64_t k, const void* b, size_t b_bytes, int64_t n,
+                      float* out, int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (!a || !b || !out || m <= 0 || k <= 0 || n <= 0) return set_error(MXH_ERR_ARG, "matmul: bad arguments");
+    if (type == MXH_F32) {
+        if (b_bytes < sizeof(float) * (size_t)k * (size_t)n) return set_error(MXH_ERR_ARG, "matmul: B too small");
+        return mxh_host_matmul_f32(a, static_cast<const float*>(b), out, m, k, n);
+    }
+    const size_t rb = type >= kTiledFlag ? 0 : row_bytes(type, n);
+    if (!rb) return set_error(MXH_ERR_ARG, "matmul: n=%lld is not a whole number of type-%d blocks", (long long)n, type);
+    if (b_bytes < rb * (size_t)k) return set_error(MXH_ERR_ARG, "matmul: B holds %zu bytes, %zu needed", b_bytes, rb * (size_t)k);
+    const void* db = nullptr;
+    if (int rc = device_weight(b, b_bytes, &db)) return rc;
+    void *da = nullptr, *dbf = nullptr, *dout = nullptr;
+    if (int rc = stage(0, sizeof(float) * (size_t)(m * k), &da)) return rc;
+    if (int rc = stage(2, sizeof(float) * (size_t)(k * n), &dbf)) return rc;
+    if (int rc = stage(1, sizeof(float) * (size_t)(m * n), &dout)) return rc;
+    if (int rc = check_hip(hipMemcpyAsync(da, a, sizeof(float) * m * k, hipMemcpyHostToDevice, g_ctx.stream), "copy")) return rc;
+    if (int rc = dequant_launch(type, db, (float*)dbf, k, n, form, g_ctx.stream))
+        return set_error(rc, "matmul: type %d with rows of %lld columns is not supported", type, (long long)n);
+    if (int rc = matmul_f32_launch((const float*)da, (const float*)dbf, (float*)dout, m, k, n, g_ctx.stream))
+        return set_error(rc, "matmul: unsupported shape");
+    if (int rc = check_hip(hipMemcpyAsync(out, dout, sizeof(float) * m * n, hipMemcpyDeviceToHost, g_ctx.stream), "copy")) return rc;
+    return check_hip(hipStreamSynchronize(g_ctx.stream), "matmul");
+}
+
 int mxh_host_vec_mul_rows_cols(const float* vec, const float* rows, float* out, size_t nrows, size_t ncols,
                                size_t stride) {
     if (int rc = ensure_ready()) return rc;
-    if (!vec || !rows || !out || !nrows || !ncols || stride < ncols)
-        return set_error(MXH_ERR_ARG, "vec_mul_rows_cols: bad arguments");
+    // any stride is accepted, as in cpu_backend.cpp:379-393 (rows may overlap)
+    if (!vec || !rows || !out || !nrows || !ncols) return set_error(MXH_ERR_ARG, "vec_mul_rows_cols: bad arguments");
     const size_t span = (nrows - 1) * stride + ncols;
     void *dv, *dr, *dout;
     if (int rc = stage(0, sizeof(float) * nrows, &dv)) return rc;
@@ -349,7 +375,9 @@ int mxh_host_matvec_strided(const float* vec, const float* mat, float* out, size
 int mxh_host_vec_dot_rows_ring(const float* vec, const float* ring, size_t head, size_t seq_max, size_t len, size_t K,
                                size_t stride, float* out) {
     if (int rc = ensure_ready()) return rc;
-    if (!vec || !ring || !out || !K || !len || !seq_max || len > seq_max || stride < K)
+    // cpu_backend.cpp:364-377 accepts any stride and len > seq_max (the ring
+    // is walked again); so does the kernel
+    if (!vec || !ring || !out || !K || !len || !seq_max)
         return set_error(MXH_ERR_ARG, "vec_dot_rows_ring: bad arguments");
     const size_t span = (seq_max - 1) * stride + K;
     void *dv, *dr, *dout;

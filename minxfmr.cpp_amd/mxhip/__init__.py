@@ -80,6 +80,7 @@ def _load() -> C.CDLL:
         "mxh_release_resources": (None, []),
         "mxh_host_matmul_rhs_t": (ip, [ip, vp, i64, i64, vp, sz, i64, vp, ip]),
         "mxh_host_matmul_f32": (ip, [vp, vp, vp, i64, i64, i64]),
+        "mxh_host_matmul_q": (ip, [ip, vp, i64, i64, vp, sz, i64, vp, ip]),
         "mxh_host_matvec_strided": (ip, [vp, vp, vp, sz, sz, sz]),
         "mxh_host_vec_dot_rows": (ip, [vp, vp, vp, sz, sz, sz]),
         "mxh_host_vec_dot_rows_ring": (ip, [vp, vp, sz, sz, sz, sz, sz, vp]),
@@ -109,7 +110,7 @@ lib = _load()
 EXPORTED = (
     "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
     "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
-    "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matvec_strided "
+    "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matmul_q mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_sample mxh_model_generate mxh_model_close "
     "mxh_write_synthetic_gguf mxh_model_decode mxh_model_bench_gemv"
