@@ -44,6 +44,15 @@ constexpr int kShortSteps = 3;  // steps per wave of the short form
 constexpr int kThreads = 64 * kWaves;
 
 // sum of the per-wave partials in a fixed order
+// 1 / sqrt(v) in double, v > 0: the hardware estimate and two Newton steps
+// (each squares the relative error), so the float rounding the callers take
+// is that of the exact quotient
+__device__ __forceinline__ double rsqrt_d(double v) {
+    double r = __builtin_amdgcn_rsq(v);
+    r = r * (1.5 - 0.5 * v * r * r);
+    return r * (1.5 - 0.5 * v * r * r);
+}
+
 __device__ __forceinline__ double block_sum(const double* red) {
     double s = 0.0;
 #pragma unroll
@@ -537,8 +546,11 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 
 // Quantize 4 consecutive staged values of thread `threadIdx.x` (elements e..e+3,
 // part of a 32-element sub-block shared by 8 consecutive threads) into the
-// limb layout.  Runs with the whole wave active (DPP); `store` guards the
-// LDS writes.
+// limb layout at `smem` (XQ order: lo, hi, scale, sum16, then one spare dword).
+// Runs with the whole wave active (DPP) and without branches, so the chains
+// of a thread's units interleave: every lane stores, those of a unit past k
+// into the spare dword, and the scale / sum16 entries are stored by every
+// lane of their sub-block / quad (the same value to the same address).
 //
 // X = rint(x / s) with s = max|x| / 32512 fits 16 bits.  v_cvt_pknorm_i16_f32
 // converts two values at once (rint(clamp(v, -1, 1) * 32767) into the two
@@ -546,10 +558,17 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // Y = X + 128 (a packed 16-bit add) the signed limbs of X = 256 hi + lo are
 // hi = byte 1 of Y and lo = byte 0 of Y xor 0x80, gathered by byte permutes;
 // the sub-block sums of X come from v_dot2 with (1, 1), exact in int32.
-__device__ __forceinline__ void quantize4(float4 w4, int e, bool store, uint32_t* lo, uint32_t* hi, float* scale,
-                                          float* sum16) {
-    const float m = max8_dpp(fmaxf(fmaxf(fabsf(w4.x), fabsf(w4.y)), fmaxf(fabsf(w4.z), fabsf(w4.w))));
-    // sub-blocks below 1e-30 in magnitude are staged as zero (keeps 1/m finite)
+__device__ __forceinline__ void quantize4(float4 w4, int e, int k, bool store, uint32_t* smem) {
+    // |x| as integers: for non-negative floats the integer order is the
+    // float order, and v_max_u32 takes a DPP operand directly
+    const uint32_t a = max(max(__float_as_uint(fabsf(w4.x)), __float_as_uint(fabsf(w4.y))),
+                           max(__float_as_uint(fabsf(w4.z)), __float_as_uint(fabsf(w4.w))));
+    uint32_t mb = max(a, (uint32_t)dpp_i<0xb1>((int)a));   // quad_perm [1,0,3,2]
+    mb = max(mb, (uint32_t)dpp_i<0x4e>((int)mb));           // quad_perm [2,3,0,1]
+    mb = max(mb, (uint32_t)dpp_i<0x141>((int)mb));          // row_half_mirror: the other quad of the 8
+    const float m = __uint_as_float(mb);
+    // sub-blocks below 1e-30 in magnitude are staged as zero (a NaN among
+    // the |x| bit patterns is the largest, so such a sub-block is too)
     const bool live = m > 1e-30f;
     const float sc = live ? m * (1.0f / 32512.0f) : 0.f;
     const float is = live ? __builtin_amdgcn_rcpf(m) * (32512.0f / 32767.0f) : 0.f;
@@ -559,14 +578,14 @@ __device__ __forceinline__ void quantize4(float4 w4, int e, bool store, uint32_t
     const uint32_t y23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x23) + (ushort2v){128, 128});
     const uint32_t plo = __builtin_amdgcn_perm(y23, y01, 0x06040200u) ^ 0x80808080u;
     const uint32_t phi = __builtin_amdgcn_perm(y23, y01, 0x07050301u);
-    // sum of the 16 X of this thread's quad
+    // sum of the 16 X of this thread's quad (every lane of the quad holds it)
     const int t = sum4_dpp(__builtin_amdgcn_sdot2(x23, (short2v){1, 1}, __builtin_amdgcn_sdot2(x01, (short2v){1, 1}, 0, false), false));
-    if (store) {
-        lo[limb(e >> 2)] = plo;
-        hi[limb(e >> 2)] = phi;
-        if (((e >> 2) & 3) == 0) sum16[e >> 4] = sc * (float)t;
-        if (((e >> 2) & 7) == 0) scale[e >> 5] = sc;
-    }
+    const int n = limb_dwords(k), spare = 2 * n + k / 32 + k / 16;
+    const int dl = limb(e >> 2);
+    smem[store ? dl : spare] = plo;
+    smem[store ? n + dl : spare] = phi;
+    smem[store ? 2 * n + (e >> 5) : spare] = __float_as_uint(sc);
+    smem[store ? 2 * n + k / 32 + (e >> 4) : spare] = __float_as_uint(sc * (float)t);
 }
 
 // Stage x as 16-bit block fixed point (see the file comment).  Thread t
@@ -581,9 +600,6 @@ template <int NB, bool NORM, class F>
 __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
                                             int k, float eps, double* red, F&& after_loads) {
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
-    uint32_t* hi = lo + limb_dwords(k);
-    float* scale = reinterpret_cast<float*>(lo + 2 * limb_dwords(k));
-    float* sum16 = scale + k / 32;
     constexpr int kStep = kThreads * 4;
     const int base = threadIdx.x * 4;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -612,7 +628,7 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict
         const double ss = wave_sum_d_lane63((double)sf);
         if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
-        const float inv = (float)(1.0 / sqrt(block_sum(red) / (double)k + (double)eps));
+        const float inv = (float)rsqrt_d(block_sum(red) / (double)k + (double)eps);
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             v[u].x = v[u].x * inv * g[u].x;
@@ -626,7 +642,7 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict
         // no branch per unit: the units are independent, so their DPP and
         // conversion chains interleave; units past k hold zeros and skip
         // their stores
-        quantize4(v[u], base + u * kStep, base + u * kStep < k, lo, hi, scale, sum16);
+        quantize4(v[u], base + u * kStep, k, base + u * kStep < k, lo);
     __syncthreads();
 }
 
@@ -636,9 +652,6 @@ __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict
                                             int k, float eps, double* red) {
     // (the first weight steps are issued by the caller before this call)
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
-    uint32_t* hi = lo + limb_dwords(k);
-    float* scale = reinterpret_cast<float*>(lo + 2 * limb_dwords(k));
-    float* sum16 = scale + k / 32;
     constexpr int kStep = kThreads * 4;
     double inv = 1.0;
     if (nw) {
@@ -665,7 +678,7 @@ __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict
             v.z = (float)((double)v.z * inv) * g.z;
             v.w = (float)((double)v.w * inv) * g.w;
         }
-        quantize4(v, e, e < k, lo, hi, scale, sum16);
+        quantize4(v, e, k, e < k, lo);
     }
     __syncthreads();
 }
@@ -983,7 +996,7 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const int64_t need = (n_groups + kWaves - 1) / kWaves;
     const int64_t cpl = ((a.k >> T<R>::kChunkShift) + 63) >> 6;  // chunk steps per row group
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
-    const size_t lds = T<R>::kIntX ? (size_t)(2 * limb_dwords(a.k) + a.k / 32 + a.k / 16) * 4
+    const size_t lds = T<R>::kIntX ? (size_t)(2 * limb_dwords(a.k) + a.k / 32 + a.k / 16 + 1) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
     const int n_cu = device_cus();
     // Short form: when every wave can finish in at most NS steps with a
