@@ -135,11 +135,19 @@ struct XQ {
 // dword index of limb dword d (elements 4d..4d+3) in the padded arrays
 __device__ __forceinline__ int limb(int d) { return d + ((d >> 4) << 2); }
 __host__ __device__ constexpr int limb_dwords(int k) { return k / 4 + k / 16; }
+// The arrays are sized for K rounded up to whole staging passes (1024
+// elements: 4 per thread), so a pass past K writes zeros into padding
+// instead of needing a per-lane guard.
+__host__ __device__ constexpr int xq_cap(int k) { return (k + kThreads * 4 - 1) / (kThreads * 4) * (kThreads * 4); }
+__host__ __device__ constexpr int xq_dwords(int k) {
+    return 2 * limb_dwords(xq_cap(k)) + xq_cap(k) / 32 + xq_cap(k) / 16;
+}
 
 __device__ __forceinline__ XQ xq_view(const float* smem, int k) {
     const uint32_t* lo = reinterpret_cast<const uint32_t*>(smem);
-    const int n = limb_dwords(k);
-    return XQ{lo, lo + n, reinterpret_cast<const float*>(lo + 2 * n), reinterpret_cast<const float*>(lo + 2 * n) + k / 32};
+    const int n = limb_dwords(xq_cap(k));
+    return XQ{lo, lo + n, reinterpret_cast<const float*>(lo + 2 * n),
+              reinterpret_cast<const float*>(lo + 2 * n) + xq_cap(k) / 32};
 }
 
 __device__ __forceinline__ uint4 lds16(const uint32_t* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -544,13 +552,15 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
     __syncthreads();
 }
 
-// Quantize 4 consecutive staged values of thread `threadIdx.x` (elements e..e+3,
-// part of a 32-element sub-block shared by 8 consecutive threads) into the
-// limb layout at `smem` (XQ order: lo, hi, scale, sum16, then one spare dword).
-// Runs with the whole wave active (DPP) and without branches, so the chains
-// of a thread's units interleave: every lane stores, those of a unit past k
-// into the spare dword, and the scale / sum16 entries are stored by every
-// lane of their sub-block / quad (the same value to the same address).
+// Quantize NB units of 4 consecutive staged values of thread `threadIdx.x`
+// (unit u: elements e0 + 1024 u .. +3, part of a 32-element sub-block shared
+// by 8 consecutive threads) into the limb layout at `smem` (the XQ arrays).
+// Runs with the whole wave active (DPP) and without per-lane branches, one
+// phase for all units at a time, so the units' dependent chains interleave:
+// every lane stores (units past k hold zeros and land in the arrays'
+// padding; whole passes past it are skipped), and the
+// scale / sum16 entries are stored by every lane of their sub-block / quad
+// (the same value to the same address).
 //
 // X = rint(x / s) with s = max|x| / 32512 fits 16 bits.  v_cvt_pknorm_i16_f32
 // converts two values at once (rint(clamp(v, -1, 1) * 32767) into the two
@@ -558,34 +568,60 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // Y = X + 128 (a packed 16-bit add) the signed limbs of X = 256 hi + lo are
 // hi = byte 1 of Y and lo = byte 0 of Y xor 0x80, gathered by byte permutes;
 // the sub-block sums of X come from v_dot2 with (1, 1), exact in int32.
-__device__ __forceinline__ void quantize4(float4 w4, int e, int k, bool store, uint32_t* smem) {
+template <int NB>
+__device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, int k, uint32_t* smem) {
     // |x| as integers: for non-negative floats the integer order is the
-    // float order, and v_max_u32 takes a DPP operand directly
-    const uint32_t a = max(max(__float_as_uint(fabsf(w4.x)), __float_as_uint(fabsf(w4.y))),
-                           max(__float_as_uint(fabsf(w4.z)), __float_as_uint(fabsf(w4.w))));
-    uint32_t mb = max(a, (uint32_t)dpp_i<0xb1>((int)a));   // quad_perm [1,0,3,2]
-    mb = max(mb, (uint32_t)dpp_i<0x4e>((int)mb));           // quad_perm [2,3,0,1]
-    mb = max(mb, (uint32_t)dpp_i<0x141>((int)mb));          // row_half_mirror: the other quad of the 8
-    const float m = __uint_as_float(mb);
-    // sub-blocks below 1e-30 in magnitude are staged as zero (a NaN among
-    // the |x| bit patterns is the largest, so such a sub-block is too)
-    const bool live = m > 1e-30f;
-    const float sc = live ? m * (1.0f / 32512.0f) : 0.f;
-    const float is = live ? __builtin_amdgcn_rcpf(m) * (32512.0f / 32767.0f) : 0.f;
-    const short2v x01 = __builtin_amdgcn_cvt_pknorm_i16(w4.x * is, w4.y * is);
-    const short2v x23 = __builtin_amdgcn_cvt_pknorm_i16(w4.z * is, w4.w * is);
-    const uint32_t y01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x01) + (ushort2v){128, 128});
-    const uint32_t y23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x23) + (ushort2v){128, 128});
-    const uint32_t plo = __builtin_amdgcn_perm(y23, y01, 0x06040200u) ^ 0x80808080u;
-    const uint32_t phi = __builtin_amdgcn_perm(y23, y01, 0x07050301u);
-    // sum of the 16 X of this thread's quad (every lane of the quad holds it)
-    const int t = sum4_dpp(__builtin_amdgcn_sdot2(x23, (short2v){1, 1}, __builtin_amdgcn_sdot2(x01, (short2v){1, 1}, 0, false), false));
-    const int n = limb_dwords(k), spare = 2 * n + k / 32 + k / 16;
-    const int dl = limb(e >> 2);
-    smem[store ? dl : spare] = plo;
-    smem[store ? n + dl : spare] = phi;
-    smem[store ? 2 * n + (e >> 5) : spare] = __float_as_uint(sc);
-    smem[store ? 2 * n + k / 32 + (e >> 4) : spare] = __float_as_uint(sc * (float)t);
+    // float order, and v_max_u32 takes a DPP operand directly; a NaN among
+    // the bit patterns is the largest, so its sub-block is staged as zero
+    uint32_t mb[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+        mb[u] = max(max(__float_as_uint(fabsf(v[u].x)), __float_as_uint(fabsf(v[u].y))),
+                    max(__float_as_uint(fabsf(v[u].z)), __float_as_uint(fabsf(v[u].w))));
+#pragma unroll
+    for (int u = 0; u < NB; ++u) mb[u] = max(mb[u], (uint32_t)dpp_i<0xb1>((int)mb[u]));   // quad_perm [1,0,3,2]
+#pragma unroll
+    for (int u = 0; u < NB; ++u) mb[u] = max(mb[u], (uint32_t)dpp_i<0x4e>((int)mb[u]));   // quad_perm [2,3,0,1]
+#pragma unroll
+    for (int u = 0; u < NB; ++u) mb[u] = max(mb[u], (uint32_t)dpp_i<0x141>((int)mb[u]));  // the other quad of the 8
+    float sc[NB];
+    short2v x01[NB], x23[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        // sub-blocks below 1e-30 in magnitude are staged as zero
+        const float m = __uint_as_float(mb[u]);
+        const bool live = m > 1e-30f;
+        sc[u] = live ? m * (1.0f / 32512.0f) : 0.f;
+        const float is = live ? __builtin_amdgcn_rcpf(m) * (32512.0f / 32767.0f) : 0.f;
+        x01[u] = __builtin_amdgcn_cvt_pknorm_i16(v[u].x * is, v[u].y * is);
+        x23[u] = __builtin_amdgcn_cvt_pknorm_i16(v[u].z * is, v[u].w * is);
+    }
+    // sums of the 16 X of each quad (every lane of the quad holds its sum)
+    int t[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+        t[u] = __builtin_amdgcn_sdot2(x23[u], (short2v){1, 1}, __builtin_amdgcn_sdot2(x01[u], (short2v){1, 1}, 0, false), false);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) t[u] += dpp_i<0xb1>(t[u]);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) t[u] += dpp_i<0x4e>(t[u]);
+    // unit u sits 1024 u elements on: 320 u padded limb dwords, 32 u scales
+    // and 64 u sums further, so one address per array serves every unit
+    const int cap = xq_cap(k), n = limb_dwords(cap);
+    uint32_t* lo = smem + limb(e0 >> 2);
+    uint32_t* hi = lo + n;
+    uint32_t* scale = smem + 2 * n + (e0 >> 5);
+    uint32_t* sum16 = smem + 2 * n + cap / 32 + (e0 >> 4);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        if (u > 0 && 1024 * u >= cap) break;  // (uniform) passes beyond the arrays
+        const uint32_t y01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x01[u]) + (ushort2v){128, 128});
+        const uint32_t y23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x23[u]) + (ushort2v){128, 128});
+        lo[320 * u] = __builtin_amdgcn_perm(y23, y01, 0x06040200u) ^ 0x80808080u;
+        hi[320 * u] = __builtin_amdgcn_perm(y23, y01, 0x07050301u);
+        scale[32 * u] = __float_as_uint(sc[u]);
+        sum16[64 * u] = __float_as_uint(sc[u] * (float)t[u]);
+    }
 }
 
 // Stage x as 16-bit block fixed point (see the file comment).  Thread t
@@ -637,12 +673,8 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict
             v[u].w = v[u].w * inv * g[u].w;
         }
     }
-#pragma unroll
-    for (int u = 0; u < NB; ++u)
-        // no branch per unit: the units are independent, so their DPP and
-        // conversion chains interleave; units past k hold zeros and skip
-        // their stores
-        quantize4(v[u], base + u * kStep, k, base + u * kStep < k, lo);
+    // units past k hold zeros and store into the spare dword
+    quantize_units<NB>(v, base, k, lo);
     __syncthreads();
 }
 
@@ -678,7 +710,8 @@ __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict
             v.z = (float)((double)v.z * inv) * g.z;
             v.w = (float)((double)v.w * inv) * g.w;
         }
-        quantize4(v, e, k, e < k, lo);
+        const float4 u1[1] = {v};
+        quantize_units<1>(u1, e, k, lo);
     }
     __syncthreads();
 }
@@ -996,7 +1029,7 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const int64_t need = (n_groups + kWaves - 1) / kWaves;
     const int64_t cpl = ((a.k >> T<R>::kChunkShift) + 63) >> 6;  // chunk steps per row group
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
-    const size_t lds = T<R>::kIntX ? (size_t)(2 * limb_dwords(a.k) + a.k / 32 + a.k / 16 + 1) * 4
+    const size_t lds = T<R>::kIntX ? (size_t)xq_dwords(a.k) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
     const int n_cu = device_cus();
     // Short form: when every wave can finish in at most NS steps with a
