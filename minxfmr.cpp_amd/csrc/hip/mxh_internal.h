@@ -74,9 +74,9 @@ struct AttnArgs {
     float eps, scale;
 };
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st);
-int attention_splits(int n_ctx);
+int attention_splits(int n_ctx, int nh, int nkv, int hd);
 bool attention_supported(int nh, int nkv, int hd);
-size_t attention_scratch_floats(int nh, int hd, int n_ctx);
+size_t attention_scratch_floats(int nh, int nkv, int hd, int n_ctx);
 int silu_mul_launch(const float* gu, float* h, int n, hipStream_t st);
 int embed_launch(int type, const void* w, const int* tokens, const int* pos, float* x, int cols, int form,
                  hipStream_t st);

@@ -52,7 +52,7 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
 
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
 constexpr int kAttnChunk = 64;      // positions per pass of a workgroup (one per lane in the softmax)
-constexpr int kAttnMaxSplits = 64;  // workgroups per kv head (one lane each in the merge)
+constexpr int kAttnMaxSplits = 128;  // workgroups per kv head (two per lane in the merge)
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
 // wave; `src` is the raw projection, the result goes to dst (LDS).
@@ -145,8 +145,9 @@ __device__ __forceinline__ float fold_position_groups(float v) {
 // position pos, so no workgroup reads a cache row written in this launch.
 // With one active workgroup the normalised output is written directly;
 // otherwise each writes (max, sum, V sums) per q head and the last to finish
-// merges them.
-template <int LPP>
+// merges them.  GM (4 or 8) bounds the q heads per kv head held in registers;
+// GM = 4 keeps the kernel near 128 VGPRs, so more workgroups are resident.
+template <int LPP, int GM>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     constexpr int HD = LPP * 8, NPG = 256 / LPP, NP = kAttnChunk / NPG;
     __shared__ float qs[kAttnMaxGroup][HD];
@@ -215,9 +216,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    float qreg[kAttnMaxGroup][8], acc[kAttnMaxGroup][8];
+    float qreg[GM][8], acc[GM][8];
 #pragma unroll
-    for (int h = 0; h < kAttnMaxGroup; ++h)
+    for (int h = 0; h < GM; ++h)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             qreg[h][e] = h < group ? qs[h][sub * 8 + e] : 0.f;
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             float kf[8];
             half8_to_float(kraw[i], kf);
 #pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) {
+            for (int h = 0; h < GM; ++h) {
                 if (h >= group) break;
                 float d = 0.f;
 #pragma unroll
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         __syncthreads();
         // exp-weighted V
 #pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) {
+        for (int h = 0; h < GM; ++h) {
             if (h >= group) break;
             const float al = alpha[h];
 #pragma unroll
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             float vf[8];
             half8_to_float(vraw[i], vf);
 #pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) {
+            for (int h = 0; h < GM; ++h) {
                 if (h >= group) break;
                 const float p = sc[h][i * NPG + pg];
 #pragma unroll
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     // sum the V partials of the position groups: lanes of a wave with the
     // same `sub`, then the four waves through LDS
 #pragma unroll
-    for (int h = 0; h < kAttnMaxGroup; ++h) {
+    for (int h = 0; h < GM; ++h) {
         if (h >= group) break;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[h][e] = fold_position_groups<LPP>(acc[h][e]);
@@ -349,13 +350,19 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
                                         : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     for (int h = wave; h < group; h += 4) {
+        // splits lane and lane + 64
         const float* ml = part_ml + ((size_t)g * group + h) * S * 2;
-        const float mi = lane < sact ? ld_agent(ml + 2 * lane) : -INFINITY;
-        const float li = lane < sact ? ld_agent(ml + 2 * lane + 1) : 0.f;
-        const float M = wave_max_all(mi);
-        const float wi = lane < sact ? __builtin_amdgcn_exp2f(mi - M) : 0.f;
-        const float den = wave_sum_all(wi * li);
-        wgt[h][lane] = wi / den;
+        const bool in0 = lane < sact, in1 = lane + 64 < sact;
+        const float m0 = in0 ? ld_agent(ml + 2 * lane) : -INFINITY;
+        const float l0 = in0 ? ld_agent(ml + 2 * lane + 1) : 0.f;
+        const float m1 = in1 ? ld_agent(ml + 2 * lane + 128) : -INFINITY;
+        const float l1 = in1 ? ld_agent(ml + 2 * lane + 129) : 0.f;
+        const float M = wave_max_all(fmaxf(m0, m1));
+        const float w0 = in0 ? __builtin_amdgcn_exp2f(m0 - M) : 0.f;
+        const float w1 = in1 ? __builtin_amdgcn_exp2f(m1 - M) : 0.f;
+        const float den = wave_sum_all(w0 * l0 + w1 * l1);
+        wgt[h][lane] = w0 / den;
+        wgt[h][lane + 64] = w1 / den;
     }
     __syncthreads();
     float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -644,11 +651,35 @@ int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, h
     return MXH_OK;
 }
 
-// Workgroups per kv head: one per 64-position chunk of the context, at most
-// kAttnMaxSplits (longer contexts give each several chunks).
-int attention_splits(int n_ctx) {
-    const int S = (n_ctx + kAttnChunk - 1) / kAttnChunk;
-    return S < 1 ? 1 : (S > kAttnMaxSplits ? kAttnMaxSplits : S);
+namespace {
+
+const void* attention_kernel_for(int nh, int nkv, int hd) {
+    const bool g4 = nh / nkv <= 4;
+    switch (hd) {
+    case 32: return g4 ? (const void*)attention_kernel<4, 4> : (const void*)attention_kernel<4, 8>;
+    case 64: return g4 ? (const void*)attention_kernel<8, 4> : (const void*)attention_kernel<8, 8>;
+    default: return g4 ? (const void*)attention_kernel<16, 4> : (const void*)attention_kernel<16, 8>;
+    }
+}
+
+}  // namespace
+
+// Workgroups per kv head: one per 64-position chunk of the context up to 64
+// chunks.  Beyond that, enough for at most two chunks each (a workgroup's
+// chunks run one after another), as far as all of them stay resident at
+// once (more would run in a second round), and at most kAttnMaxSplits.
+int attention_splits(int n_ctx, int nh, int nkv, int hd) {
+    const int nch = (n_ctx + kAttnChunk - 1) / kAttnChunk;
+    if (nch <= 64) return nch < 1 ? 1 : nch;
+    int dev = 0, n_cu = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_kernel_for(nh, nkv, hd), 256, 0) != hipSuccess)
+        n_cu = per_cu = 0;
+    const int cap = nkv > 0 ? per_cu * n_cu / nkv : 0;
+    int S = (nch + 1) / 2;
+    if (S > cap) S = cap;
+    if (S > kAttnMaxSplits) S = kAttnMaxSplits;
+    return S < 64 ? 64 : S;
 }
 
 // head_dim 32, 64 or 128 (8 dims per lane, a power-of-two lane count per
@@ -659,18 +690,28 @@ bool attention_supported(int nh, int nkv, int hd) {
 
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
-    const dim3 grid(a.nkv, attention_splits(n_ctx));
+    const dim3 grid(a.nkv, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
+    const bool g4 = a.nh / a.nkv <= 4;
     switch (a.hd) {
-    case 32: hipLaunchKernelGGL(attention_kernel<4>, grid, dim3(256), 0, st, a); break;
-    case 64: hipLaunchKernelGGL(attention_kernel<8>, grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(attention_kernel<16>, grid, dim3(256), 0, st, a); break;
+    case 32:
+        if (g4) hipLaunchKernelGGL((attention_kernel<4, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((attention_kernel<4, 8>), grid, dim3(256), 0, st, a);
+        break;
+    case 64:
+        if (g4) hipLaunchKernelGGL((attention_kernel<8, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((attention_kernel<8, 8>), grid, dim3(256), 0, st, a);
+        break;
+    default:
+        if (g4) hipLaunchKernelGGL((attention_kernel<16, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((attention_kernel<16, 8>), grid, dim3(256), 0, st, a);
+        break;
     }
     return MXH_OK;
 }
 
 // V partials [nh][S][hd] followed by (max, sum) pairs [nh][S][2]
-size_t attention_scratch_floats(int nh, int hd, int n_ctx) {
-    return (size_t)nh * attention_splits(n_ctx) * (hd + 2);
+size_t attention_scratch_floats(int nh, int nkv, int hd, int n_ctx) {
+    return (size_t)nh * attention_splits(n_ctx, nh, nkv, hd) * (hd + 2);
 }
 
 int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,

@@ -468,7 +468,7 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     if (!rc) rc = dalloc(&m->gu, 2 * (size_t)c.n_ff);
     if (!rc) rc = dalloc(&m->h, (size_t)c.n_ff);
     if (!rc) rc = dalloc(&m->logits, (size_t)c.n_vocab);
-    if (!rc) rc = dalloc(&m->part, attention_scratch_floats(c.n_head, c.head_dim, n_ctx));
+    if (!rc) rc = dalloc(&m->part, attention_scratch_floats(c.n_head, c.n_head_kv, c.head_dim, n_ctx));
     if (!rc) rc = dalloc(&m->trace, (size_t)(c.n_layer + 1) * c.n_embd);
     if (!rc) rc = dalloc(&m->tokens, (size_t)n_ctx + 1);
     if (!rc) rc = dalloc(&m->pos, 1);
