@@ -14,6 +14,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -75,6 +76,11 @@ struct mxh_model {
     int pf_rows = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_gu = nullptr;
     uint16_t *pf_a = nullptr, *pf_a_lo = nullptr;  // GEMM input as split bf16 (hi, lo)
+    // GEMM input of the Q4_K fp16 kernel: fp16 hi / lo of a * 2^e per row,
+    // split sub-block sums, 2^-e per row
+    uint16_t *pf_h16 = nullptr, *pf_l16 = nullptr, *pf_sh = nullptr, *pf_sl = nullptr;
+    float* pf_rscale = nullptr;
+    bool bf16_prefill = false;  // every prefill GEMM in the split-bf16 form
     float* pf_part = nullptr;                        // split-K partial tiles
     size_t pf_part_floats = 0;
 };
@@ -203,7 +209,7 @@ int free_model(mxh_model* m) {
     void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
                     m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
                     m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part,
-                    m->sprm, m->scand};
+                    m->pf_h16, m->pf_l16, m->pf_sh, m->pf_sl, m->pf_rscale, m->sprm, m->scand};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -490,6 +496,7 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
         return rc;
     }
     m->token_prefill = (flags & MXH_MODEL_TOKEN_PREFILL) != 0;
+    m->bf16_prefill = (flags & MXH_MODEL_BF16_PREFILL) != 0;
     if (!(flags & MXH_MODEL_NO_GRAPH)) {
         if ((rc = capture(m, false, &m->g_prefill)) || (rc = capture(m, true, &m->g_decode))) {
             free_model(m);
@@ -569,6 +576,11 @@ int ensure_prefill_buffers(mxh_model* m) {
     if (!rc) rc = dalloc(&m->pf_gu, (size_t)rows * 2 * c.n_ff);
     if (!rc) rc = dalloc(&m->pf_a, (size_t)rows * widest);
     if (!rc) rc = dalloc(&m->pf_a_lo, (size_t)rows * widest);
+    if (!rc) rc = dalloc(&m->pf_h16, (size_t)rows * widest);
+    if (!rc) rc = dalloc(&m->pf_l16, (size_t)rows * widest);
+    if (!rc) rc = dalloc(&m->pf_sh, (size_t)rows * (widest / 32));
+    if (!rc) rc = dalloc(&m->pf_sl, (size_t)rows * (widest / 32));
+    if (!rc) rc = dalloc(&m->pf_rscale, (size_t)rows);
     // split-K partials: up to 4 splits of the narrower outputs (x, q|k|v)
     m->pf_part_floats = 4 * (size_t)rows * std::max((size_t)c.n_embd, qd + 2 * kvd);
     if (!rc) rc = dalloc(&m->pf_part, m->pf_part_floats);
@@ -576,10 +588,35 @@ int ensure_prefill_buffers(mxh_model* m) {
     return rc;
 }
 
-// split-bf16 GEMM over the prefill input buffers (pf_a, pf_a_lo)
+// Which input form a prefill GEMM reads: the exact-weight fp16 kernel for
+// Q4_K rows (pf_h16 / pf_l16 / pf_sh / pf_sl / pf_rscale), the split-bf16
+// kernel otherwise (pf_a, pf_a_lo).
+bool f16_gemm(const mxh_model* m, const DevW& w) {
+    return w.p && !m->bf16_prefill && gemm_q4k_f16_supported(w.type, (int)w.cols);
+}
+
 int gemm(mxh_model* m, const DevW& w, int lda, float* out, int ldo, const float* res, int rows, hipStream_t st) {
+    if (f16_gemm(m, w))
+        return gemm_q4k_f16_run(w.type, m->pf_h16, m->pf_l16, lda, m->pf_sh, m->pf_sl, lda / 32, m->pf_rscale, w.p,
+                                out, ldo, res, rows, (int)w.rows, (int)w.cols, m->form, m->pf_part,
+                                m->pf_part_floats, st);
     return gemm_bf16_run(w.type, m->pf_a, m->pf_a_lo, lda, w.p, out, ldo, res, rows, (int)w.rows, (int)w.cols,
                          m->form, m->pf_part, m->pf_part_floats, st);
+}
+
+// GEMM inputs from rows of x (normed with nw when given) in the forms the
+// consumers `ws` read
+int prep_rows(mxh_model* m, std::initializer_list<const DevW*> ws, const float* x, int ldx, const float* nw, float eps,
+              int k, int rows, hipStream_t st) {
+    bool need16 = false, needbf = false;
+    for (const DevW* w : ws)
+        if (w->p) (f16_gemm(m, *w) ? need16 : needbf) = true;
+    int rc = MXH_OK;
+    if (need16)
+        rc |= rows_to_f16_launch(x, ldx, nw, eps, k, m->pf_h16, m->pf_l16, k, m->pf_sh, m->pf_sl, k / 32, m->pf_rscale,
+                                 rows, st);
+    if (needbf) rc |= rows_to_bf16_launch(x, ldx, nw, eps, k, m->pf_a, m->pf_a_lo, k, rows, st);
+    return rc;
 }
 
 // Prompt tokens tokens[p0 .. p0+rows) through every layer at once, the
@@ -593,7 +630,7 @@ int enqueue_prefill_chunk(mxh_model* m, int p0, int rows, hipStream_t st) {
     int rc = embed_rows_launch(m->embd.type, m->embd.p, m->tokens, p0, rows, m->pf_x, d, m->form, st);
     for (int l = 0; l < c.n_layer && !rc; ++l) {
         const Layer& L = m->layers[(size_t)l];
-        rc |= rows_to_bf16_launch(m->pf_x, d, L.attn_norm, c.eps, d, m->pf_a, m->pf_a_lo, d, rows, st);
+        rc |= prep_rows(m, {&L.qkv, &L.q, &L.k, &L.v}, m->pf_x, d, L.attn_norm, c.eps, d, rows, st);
         if (L.qkv_fused) {
             rc |= gemm(m, L.qkv, d, m->pf_qkv, ldq, nullptr, rows, st);
         } else {
@@ -604,16 +641,19 @@ int enqueue_prefill_chunk(mxh_model* m, int p0, int rows, hipStream_t st) {
         rc |= qkv_prep_rows_launch(m->pf_qkv, ldq, L.bias, L.q_norm, L.k_norm, m->rope_cs, p0, rows, m->pf_q, L.kc,
                                    L.vc, nh, nkv, hd, m->neox, c.eps, st);
         rc |= attention_rows_launch(m->pf_q, L.kc, L.vc, m->pf_att, p0, rows, nh, nkv, hd, 1.0f / sqrtf((float)hd), st);
-        rc |= rows_to_bf16_launch(m->pf_att, qd, nullptr, 0.f, qd, m->pf_a, m->pf_a_lo, qd, rows, st);
+        rc |= prep_rows(m, {&L.o}, m->pf_att, qd, nullptr, 0.f, qd, rows, st);
         rc |= gemm(m, L.o, qd, m->pf_x, d, m->pf_x, rows, st);
-        rc |= rows_to_bf16_launch(m->pf_x, d, L.ffn_norm, c.eps, d, m->pf_a, m->pf_a_lo, d, rows, st);
+        rc |= prep_rows(m, {&L.gu, &L.g, &L.u}, m->pf_x, d, L.ffn_norm, c.eps, d, rows, st);
         if (L.gu_fused) {
             rc |= gemm(m, L.gu, d, m->pf_gu, 2 * f, nullptr, rows, st);
         } else {
             rc |= gemm(m, L.g, d, m->pf_gu, 2 * f, nullptr, rows, st);
             rc |= gemm(m, L.u, d, m->pf_gu + f, 2 * f, nullptr, rows, st);
         }
-        rc |= silu_mul_bf16_launch(m->pf_gu, f, m->pf_a, m->pf_a_lo, rows, st);
+        if (f16_gemm(m, L.down))
+            rc |= silu_mul_f16_launch(m->pf_gu, f, m->pf_h16, m->pf_l16, m->pf_sh, m->pf_sl, m->pf_rscale, rows, st);
+        else
+            rc |= silu_mul_bf16_launch(m->pf_gu, f, m->pf_a, m->pf_a_lo, rows, st);
         rc |= gemm(m, L.down, f, m->pf_x, d, m->pf_x, rows, st);
     }
     if (!rc) rc = add_int_launch(m->pos, rows, st);

@@ -1,0 +1,488 @@
+// mxh_prefill_q4k.hip — the prefill GEMM for Q4_K weights on the fp16 matrix
+// cores, with every weight exact.
+//
+// out[m][n] = sum_k a[m][k] w[n][k] over Q4_K rows w = d sc_j q - dmin m_j
+// (tensor.cpp:405-432; sub-block j of 32 elements inside a 256-element
+// super-block with one d, dmin) regrouped as
+//
+//   sum_b d_b[n] . sum_{k in b} a[m][k] (sc_j q_k)          main MFMAs
+//   - sum_j dmin[n] m_j . S_j[m],   S_j = sum_{k in j} a[m][k]   correction MFMAs
+//
+// sc_j q_k is an integer below 1024, exact in fp16, so no weight is rounded:
+// the tile holds those integers, d is applied once per super-block to a
+// per-block accumulator, and the min terms are a small second contraction
+// over sub-blocks (16 at a time).  Activations come as a' = a 2^e (e per
+// row, so max |a'| lies in [128, 256)) split into fp16 hi + lo (about 22
+// significant bits), with the sub-block sums S of the same values split the
+// same way (rows_to_f16 / silu_mul_f16 below); the output is scaled back by
+// 2^-e.  Reference op: backend_matmul_rhs_transposed with m > 1
+// (src/backend/backend_runtime.cpp:302-319).
+//
+// Tiles: 128 x 128 outputs per workgroup of 4 waves, each wave 64 x 64 as
+// 2 x 2 blocks of v_mfma_f32_32x32x16_f16 (lane l supplies row / column
+// l % 32 at k = 8 (l / 32) .. +8; accumulator register i of lane l is row
+// 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32).  K steps of 64 elements
+// (two sub-blocks); the next step's global loads fly during the MFMAs.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "mxh_device.h"
+#include "mxh_internal.h"
+
+namespace mxh {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kQM = 128, kQN = 128, kQK = 64;
+constexpr int kQLd = kQK + 8;   // tile row stride in fp16 (144 bytes)
+constexpr int kRing = 16;       // sub-blocks per correction round
+constexpr int kRLd = kRing + 8; // ring row stride in fp16 (48 bytes)
+constexpr size_t kQLds = (size_t)(3 * kQM * kQLd + 4 * kQM * kRLd) * 2 + kQN * sizeof(float);
+
+__device__ __forceinline__ uint16_t f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
+
+// fp16 hi + lo of v (lo = v - hi rounded again) as hi | lo << 16
+__device__ __forceinline__ uint32_t split_f16(float v) {
+    const __half h = __float2half_rn(v);
+    return (uint32_t)__half_as_ushort(h) | ((uint32_t)f16_bits(v - __half2float(h)) << 16);
+}
+
+// the three 16-byte pieces of 64-element chunk k0 / 64 of a Q4_K row
+template <bool TILED>
+struct Q4Chunk {
+    uint4 hd, qa, qb;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0) {
+        const uint8_t* rp = w + (size_t)row * rb;
+        if constexpr (TILED) {
+            const Q4KTileOffs o = q4k_tile_offsets(k0 >> 6, (int64_t)(rb / 144));
+            hd = *reinterpret_cast<const uint4*>(rp + o.hd);
+            qa = *reinterpret_cast<const uint4*>(rp + o.qa);
+            qb = *reinterpret_cast<const uint4*>(rp + o.qb);
+        } else {
+            const uint8_t* blk = rp + (size_t)(k0 >> 8) * 144;
+            const int g = (k0 & 255) >> 6;
+            hd = *reinterpret_cast<const uint4*>(blk);
+            qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
+            qb = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
+        }
+    }
+};
+
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+    // both are integers below 2048: round-toward-zero packing is exact
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// Split K: workgroup z takes K steps [z * ksteps, (z + 1) * ksteps), a
+// multiple of 4 (whole super-blocks), and with more than one split writes
+// its scaled partial tile to part[z][m][n] for gemm_reduce.
+template <bool TILED>
+__global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __restrict__ a_hi,
+                                                           const uint16_t* __restrict__ a_lo, int lda,
+                                                           const uint16_t* __restrict__ s_hi,
+                                                           const uint16_t* __restrict__ s_lo, int lds,
+                                                           const float* __restrict__ rscale,
+                                                           const uint8_t* __restrict__ w, float* out, int ldo,
+                                                           const float* res, int m, int n, int k, int form, int ksteps,
+                                                           float* __restrict__ part) {
+    extern __shared__ __align__(16) uint16_t smem[];
+    uint16_t* Ah = smem;              // [128][kQLd] activations, hi
+    uint16_t* Al = Ah + kQM * kQLd;   // lo
+    uint16_t* Ws = Al + kQM * kQLd;   // [128][kQLd] weights sc q
+    uint16_t* Sh = Ws + kQN * kQLd;   // [128][kRLd] sub-block sums, hi (ring of 16 sub-blocks)
+    uint16_t* Sl = Sh + kQM * kRLd;
+    uint16_t* Bh = Sl + kQM * kRLd;   // [128][kRLd] -dmin m_j per weight row, hi
+    uint16_t* Bl = Bh + kQN * kRLd;
+    float* dcol = reinterpret_cast<float*>(Bl + kQN * kRLd);  // [128] d of the current super-block
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int m0 = blockIdx.y * kQM, n0 = blockIdx.x * kQN;
+    const int kb = blockIdx.z * ksteps * kQK, ke = min(k, kb + ksteps * kQK);
+    const size_t rb = (size_t)(k / 256) * 144;
+    // staging role: thread t owns row t / 2 of each tile and sub-block half t % 2 of the step
+    const int t = threadIdx.x, r = t >> 1, h = t & 1;
+    const int wrow = min(n0 + r, n - 1);
+    const bool arow = m0 + r < m;
+    const int lr = lane & 31, lk = 8 * (lane >> 5);
+
+    f32x16 acc[2][2], P[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = P[i][j][e] = 0.f;
+
+    // rows past m read row m - 1 and are zeroed when staged
+    const int arow_c = min(m0 + r, m - 1);
+    const uint16_t* pa_h = a_hi + (size_t)arow_c * lda + 32 * h;
+    const uint16_t* pa_l = a_lo + (size_t)arow_c * lda + 32 * h;
+    const uint16_t* ps_h = s_hi + (size_t)arow_c * lds + h;
+    const uint16_t* ps_l = s_lo + (size_t)arow_c * lds + h;
+    uint4 ah0, ah1, ah2, ah3, al0, al1, al2, al3;
+    uint32_t sh_g, sl_g;
+    Q4Chunk<TILED> wq;
+#define MXH_Q4F16_FETCH(K0)                                                   \
+    do {                                                                     \
+        const uint4* qh_ = reinterpret_cast<const uint4*>(pa_h + (K0));      \
+        const uint4* ql_ = reinterpret_cast<const uint4*>(pa_l + (K0));      \
+        ah0 = qh_[0]; ah1 = qh_[1]; ah2 = qh_[2]; ah3 = qh_[3];              \
+        al0 = ql_[0]; al1 = ql_[1]; al2 = ql_[2]; al3 = ql_[3];              \
+        sh_g = ps_h[(K0) >> 5];                                              \
+        sl_g = ps_l[(K0) >> 5];                                              \
+        wq.fetch(w, rb, wrow, (K0));                                         \
+    } while (0)
+    MXH_Q4F16_FETCH(kb);
+
+    int step = 0;
+    for (int k0 = kb; k0 < ke; k0 += kQK, ++step) {
+        const int slot = 2 * (step & 7) + h;
+        {
+            uint4* dh = reinterpret_cast<uint4*>(Ah + r * kQLd + 32 * h);
+            uint4* dl = reinterpret_cast<uint4*>(Al + r * kQLd + 32 * h);
+            const uint32_t am = arow ? 0xffffffffu : 0u;
+            auto msk = [am](uint4 v) { return make_uint4(v.x & am, v.y & am, v.z & am, v.w & am); };
+            dh[0] = msk(ah0);
+            dh[1] = msk(ah1);
+            dh[2] = msk(ah2);
+            dh[3] = msk(ah3);
+            dl[0] = msk(al0);
+            dl[1] = msk(al1);
+            dl[2] = msk(al2);
+            dl[3] = msk(al3);
+            Sh[r * kRLd + slot] = (uint16_t)(sh_g & am);
+            Sl[r * kRLd + slot] = (uint16_t)(sl_g & am);
+            // weights of sub-block j = 2 g + h as the integers sc_j q (tensor.cpp:395-432
+            // with the scale form `form`); bytes i of the chunk's 32 qs hold element i
+            // (low nibble) and element 32 + i (high nibble)
+            const int j = 2 * ((k0 & 255) >> 6) + h;
+            uint32_t sc, mn;
+            k4_scale_min(wq.hd.y, wq.hd.z, wq.hd.w, j, form, sc, mn);
+            const float scf = (float)sc;
+            const uint32_t qv[8] = {wq.qa.x, wq.qa.y, wq.qa.z, wq.qa.w, wq.qb.x, wq.qb.y, wq.qb.z, wq.qb.w};
+            uint32_t o[16];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t nb = (qv[i] >> (4 * h)) & 0x0f0f0f0fu;
+                o[2 * i] = pk_f16((float)(nb & 0xffu) * scf, (float)((nb >> 8) & 0xffu) * scf);
+                o[2 * i + 1] = pk_f16((float)((nb >> 16) & 0xffu) * scf, (float)(nb >> 24) * scf);
+            }
+            uint4* dw = reinterpret_cast<uint4*>(Ws + r * kQLd + 32 * h);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dw[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+            const uint32_t bsplit = split_f16(-(half_bits_to_float(wq.hd.x >> 16) * (float)mn));
+            Bh[r * kRLd + slot] = (uint16_t)bsplit;
+            Bl[r * kRLd + slot] = (uint16_t)(bsplit >> 16);
+            if (h == 0) dcol[r] = half_bits_to_float(wq.hd.x & 0xffffu);
+        }
+        __syncthreads();
+        if (k0 + kQK < ke) MXH_Q4F16_FETCH(k0 + kQK);
+
+#pragma unroll
+        for (int ks = 0; ks < kQK; ks += 16) {
+            f16x8 ah[2], al[2], bw[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int ao = (wr * 64 + i * 32 + lr) * kQLd + ks + lk;
+                const int bo = (wc * 64 + i * 32 + lr) * kQLd + ks + lk;
+                ah[i] = *reinterpret_cast<const f16x8*>(Ah + ao);
+                al[i] = *reinterpret_cast<const f16x8*>(Al + ao);
+                bw[i] = *reinterpret_cast<const f16x8*>(Ws + bo);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], P[i][j], 0, 0, 0);
+                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], P[i][j], 0, 0, 0);
+                }
+        }
+        const bool last = k0 + kQK >= ke;
+        if (((k0 + kQK) & 255) == 0 || last) {
+            // end of a super-block: acc += d[n] . P (each lane's accumulators share one column)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float dc = dcol[wc * 64 + j * 32 + lr];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        acc[i][j][e] = fmaf(dc, P[i][j][e], acc[i][j][e]);
+                        P[i][j][e] = 0.f;
+                    }
+            }
+        }
+        if ((step & 7) == 7 || last) {
+            // correction round over the sub-blocks staged since the last one;
+            // ring slots past `used` hold older values and are zeroed here
+            const int used = 2 * ((step & 7) + 1);
+            f16x8 sh[2], sl[2], bh[2], bl[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                sh[i] = *reinterpret_cast<const f16x8*>(Sh + (wr * 64 + i * 32 + lr) * kRLd + lk);
+                sl[i] = *reinterpret_cast<const f16x8*>(Sl + (wr * 64 + i * 32 + lr) * kRLd + lk);
+                bh[i] = *reinterpret_cast<const f16x8*>(Bh + (wc * 64 + i * 32 + lr) * kRLd + lk);
+                bl[i] = *reinterpret_cast<const f16x8*>(Bl + (wc * 64 + i * 32 + lr) * kRLd + lk);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (lk + e >= used) sh[i][e] = sl[i][e] = bh[i][e] = bl[i][e] = (_Float16)0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl[i], bh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bl[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bh[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        __syncthreads();
+    }
+
+    const bool partial = gridDim.z > 1;
+    float* dst = partial ? part + (size_t)blockIdx.z * m * n : out;
+    const int ld = partial ? n : ldo;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wc * 64 + j * 32 + lr;
+            if (col >= n) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (row < m) {
+                    const size_t o = (size_t)row * ld + col;
+                    const float v = acc[i][j][e] * rscale[row];
+                    if (partial) dst[o] = v;
+                    else dst[o] = res ? v + res[o] : v;
+                }
+            }
+        }
+}
+
+#undef MXH_Q4F16_FETCH
+
+__global__ void gemm_f16_reduce_kernel(const float* __restrict__ part, int splits, float* out, int ldo,
+                                       const float* res, int m, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * n) return;
+    const int r = i / n, c = i % n;
+    float v = 0.f;
+    for (int s = 0; s < splits; ++s) v += part[(size_t)s * m * n + i];
+    const size_t o = (size_t)r * ldo + c;
+    out[o] = res ? v + res[o] : v;
+}
+
+// power-of-two scale 2^e that brings the row maximum into [128, 256)
+__device__ __forceinline__ int row_exponent(float maxv) {
+    if (!(maxv > 0.f) || maxv > 3.0e38f) return 0;
+    int ex;
+    (void)frexpf(maxv, &ex);  // maxv in [2^(ex-1), 2^ex)
+    const int e = 8 - ex;
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
+// block-wide max of non-negative floats (256 threads)
+__device__ __forceinline__ float block_max_256(float v, float* red) {
+    v = wave_max_all(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return r;
+}
+
+// Writes row values v (sub-block sb of 32, thread-owned) as a' = v 2^e split
+// into fp16 hi / lo, and the split sum of each sub-block's hi + lo.
+__device__ __forceinline__ void emit_subblock(const float* v, float scale, uint16_t* ah, uint16_t* al, uint16_t* sh,
+                                              uint16_t* sl) {
+    float s = 0.f;
+    uint32_t ph[16], pl[16];
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        const uint32_t p0 = split_f16(v[i] * scale), p1 = split_f16(v[i + 1] * scale);
+        s += (__half2float(__ushort_as_half((uint16_t)p0)) + __half2float(__ushort_as_half((uint16_t)(p0 >> 16)))) +
+             (__half2float(__ushort_as_half((uint16_t)p1)) + __half2float(__ushort_as_half((uint16_t)(p1 >> 16))));
+        ph[i / 2] = (p0 & 0xffffu) | (p1 << 16);
+        pl[i / 2] = (p0 >> 16) | (p1 & 0xffff0000u);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        reinterpret_cast<uint4*>(ah)[q] = make_uint4(ph[4 * q], ph[4 * q + 1], ph[4 * q + 2], ph[4 * q + 3]);
+        reinterpret_cast<uint4*>(al)[q] = make_uint4(pl[4 * q], pl[4 * q + 1], pl[4 * q + 2], pl[4 * q + 3]);
+    }
+    const uint32_t ps = split_f16(s);
+    *sh = (uint16_t)ps;
+    *sl = (uint16_t)(ps >> 16);
+}
+
+// Rows of x (optionally the reference rmsnorm x / sqrt(mean(x^2) + eps) * w,
+// rmsnorm.cpp:5-26, sum of squares in double, the same float products as
+// rows_to_bf16) as GEMM input of gemm_q4k_f16.  One workgroup per row; k a
+// multiple of 32 and at most 2 * 256 * 32.
+constexpr int kRowSub = 2;  // sub-blocks per thread
+__global__ __launch_bounds__(256) void rows_to_f16_kernel(const float* __restrict__ x, int ldx,
+                                                          const float* __restrict__ nw, float eps, int k,
+                                                          uint16_t* __restrict__ a_hi, uint16_t* __restrict__ a_lo,
+                                                          int lda, uint16_t* __restrict__ s_hi,
+                                                          uint16_t* __restrict__ s_lo, int lds,
+                                                          float* __restrict__ rscale) {
+    __shared__ double red[4];
+    __shared__ float redf[4];
+    const int row = blockIdx.x, nsb = k / 32;
+    const float* xr = x + (size_t)row * ldx;
+    float v[kRowSub][32];
+    double ss = 0.0;
+    float mx = 0.f;
+#pragma unroll
+    for (int u = 0; u < kRowSub; ++u) {
+        const int sb = threadIdx.x + 256 * u;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[u][i] = 0.f;
+        if (sb < nsb) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = reinterpret_cast<const float4*>(xr + 32 * sb)[q];
+                v[u][4 * q] = f.x;
+                v[u][4 * q + 1] = f.y;
+                v[u][4 * q + 2] = f.z;
+                v[u][4 * q + 3] = f.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) ss += (double)v[u][i] * v[u][i];
+    }
+    float inv = 1.f;
+    if (nw) {
+        ss = wave_sum_d_lane63(ss);
+        if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        inv = (float)(1.0 / sqrt(((red[0] + red[1]) + (red[2] + red[3])) / (double)k + (double)eps));
+    }
+#pragma unroll
+    for (int u = 0; u < kRowSub; ++u) {
+        const int sb = threadIdx.x + 256 * u;
+        if (nw && sb < nsb) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[u][i] = v[u][i] * inv * nw[32 * sb + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(v[u][i]));
+    }
+    const int e = row_exponent(block_max_256(mx, redf));
+    const float scale = ldexpf(1.f, e);
+    if (threadIdx.x == 0) rscale[row] = ldexpf(1.f, -e);
+#pragma unroll
+    for (int u = 0; u < kRowSub; ++u) {
+        const int sb = threadIdx.x + 256 * u;
+        if (sb < nsb)
+            emit_subblock(v[u], scale, a_hi + (size_t)row * lda + 32 * sb, a_lo + (size_t)row * lda + 32 * sb,
+                          s_hi + (size_t)row * lds + sb, s_lo + (size_t)row * lds + sb);
+    }
+}
+
+// h = silu(gate) * up (transformer.cpp:183-185) as gemm_q4k_f16 input; gu
+// rows are [gate | up], f a multiple of 32 and at most 2 * 256 * 32.
+__global__ __launch_bounds__(256) void silu_mul_f16_kernel(const float* __restrict__ gu, int f,
+                                                           uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo,
+                                                           uint16_t* __restrict__ s_hi, uint16_t* __restrict__ s_lo,
+                                                           float* __restrict__ rscale) {
+    __shared__ float redf[4];
+    const int row = blockIdx.x, nsb = f / 32, lds = nsb;
+    const float* g = gu + (size_t)row * 2 * f;
+    float v[kRowSub][32];
+    float mx = 0.f;
+#pragma unroll
+    for (int u = 0; u < kRowSub; ++u) {
+        const int sb = threadIdx.x + 256 * u;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            float hv = 0.f;
+            if (sb < nsb) {
+                const float gv = g[32 * sb + i], uv = g[f + 32 * sb + i];
+                hv = gv / (1.0f + expf(-gv)) * uv;
+            }
+            v[u][i] = hv;
+            mx = fmaxf(mx, fabsf(hv));
+        }
+    }
+    const int e = row_exponent(block_max_256(mx, redf));
+    const float scale = ldexpf(1.f, e);
+    if (threadIdx.x == 0) rscale[row] = ldexpf(1.f, -e);
+#pragma unroll
+    for (int u = 0; u < kRowSub; ++u) {
+        const int sb = threadIdx.x + 256 * u;
+        if (sb < nsb)
+            emit_subblock(v[u], scale, h_hi + (size_t)row * f + 32 * sb, h_lo + (size_t)row * f + 32 * sb,
+                          s_hi + (size_t)row * lds + sb, s_lo + (size_t)row * lds + sb);
+    }
+}
+
+template <bool TILED>
+int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+                        const uint16_t* s_lo, int lds, const float* rscale, const uint8_t* w, float* out, int ldo,
+                        const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
+                        hipStream_t st) {
+    static bool attr_set = false;  // above 64 KiB of LDS needs the opt-in, once per kernel
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)gemm_q4k_f16_kernel<TILED>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)kQLds) != hipSuccess)
+            return MXH_ERR_HIP;
+        attr_set = true;
+    }
+    const int tn = (n + kQN - 1) / kQN, tm = (m + kQM - 1) / kQM, steps = k / kQK;
+    // split K (whole super-blocks, at most 4 ways) while the tile grid leaves CUs idle
+    int splits = 1;
+    while (splits < 4 && tn * tm * splits * 2 <= 512 && steps % (splits * 2 * 4) == 0 &&
+           (size_t)(splits * 2) * m * n <= part_floats)
+        splits *= 2;
+    const dim3 grid(tn, tm, splits);
+    hipLaunchKernelGGL((gemm_q4k_f16_kernel<TILED>), grid, dim3(256), kQLds, st, a_hi, a_lo, lda, s_hi, s_lo, lds,
+                       rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
+    if (splits > 1)
+        hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
+                           res, m, n);
+    return MXH_OK;
+}
+
+}  // namespace
+
+bool gemm_q4k_f16_supported(int type, int k) {
+    return (type == MXH_Q4_K || type == MXH_Q4_K_TILED) && k % 256 == 0 && k <= kRowSub * 256 * 32;
+}
+
+int gemm_q4k_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+                     const uint16_t* s_lo, int lds, const float* rscale, const void* w, float* out, int ldo,
+                     const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
+                     hipStream_t st) {
+    if (m <= 0 || n <= 0 || !gemm_q4k_f16_supported(type, k) || lda < k || lds < k / 32 || ldo < n) return MXH_ERR_ARG;
+    if (!part) part_floats = 0;
+    const uint8_t* wb = (const uint8_t*)w;
+    return type == MXH_Q4_K_TILED
+               ? gemm_q4k_f16_launch<true>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
+                                           part, part_floats, st)
+               : gemm_q4k_f16_launch<false>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
+                                            part, part_floats, st);
+}
+
+int rows_to_f16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a_hi, uint16_t* a_lo,
+                       int lda, uint16_t* s_hi, uint16_t* s_lo, int lds, float* rscale, int m, hipStream_t st) {
+    if (m <= 0 || k % 32 || k > kRowSub * 256 * 32 || lda < k || lds < k / 32) return MXH_ERR_ARG;
+    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(m), dim3(256), 0, st, x, ldx, nw, eps, k, a_hi, a_lo, lda, s_hi, s_lo,
+                       lds, rscale);
+    return MXH_OK;
+}
+
+int silu_mul_f16_launch(const float* gu, int f, uint16_t* h_hi, uint16_t* h_lo, uint16_t* s_hi, uint16_t* s_lo,
+                        float* rscale, int m, hipStream_t st) {
+    if (m <= 0 || f % 32 || f > kRowSub * 256 * 32) return MXH_ERR_ARG;
+    hipLaunchKernelGGL(silu_mul_f16_kernel, dim3(m), dim3(256), 0, st, gu, f, h_hi, h_lo, s_hi, s_lo, rscale);
+    return MXH_OK;
+}
+
+}  // namespace mxh

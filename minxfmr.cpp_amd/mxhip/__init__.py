@@ -51,6 +51,7 @@ class SynthArch(C.Structure):
 
 
 MODEL_ROPE_NEOX, MODEL_GGML_FORM, MODEL_NO_QK_NORM, MODEL_NO_GRAPH, MODEL_TOKEN_PREFILL, MODEL_GGUF_LAYOUT = 1, 4, 8, 16, 32, 64
+MODEL_BF16_PREFILL = 128
 
 
 def _load() -> C.CDLL:

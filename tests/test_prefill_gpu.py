@@ -74,15 +74,18 @@ from test_model_gpu import TINY, VARIANTS, build, close_enough  # noqa: E402
 
 @pytest.mark.parametrize("name", list(VARIANTS))
 @pytest.mark.parametrize("n_ctx,n_prompt", [(128, 70), (600, 530)])
-def test_batched_prefill_then_step(mxh, tmp_path, name, n_ctx, n_prompt):
+@pytest.mark.parametrize("flags", [0, mxhip.MODEL_BF16_PREFILL], ids=["default", "bf16split"])
+def test_batched_prefill_then_step(mxh, tmp_path, name, n_ctx, n_prompt, flags):
     """Prompt fed through the matrix-core prefill (one chunk of 70, or 512 +
     18), then one decode step: its per-layer hidden states and logits are
-    within the parity bar of the oracle run token by token (fp16 cache)."""
+    within the parity bar of the oracle run token by token (fp16 cache).
+    Default: Q4_K projections on the exact-weight fp16 GEMM, the rest split
+    bf16; MODEL_BF16_PREFILL: every projection split bf16."""
     p = build(tmp_path, name)
     rng = np.random.default_rng(17)
     prompt = rng.integers(0, TINY["n_vocab"], n_prompt).astype(np.int32)
     nxt = int(rng.integers(0, TINY["n_vocab"]))
-    gm = mxhip.Model(p, n_ctx)
+    gm = mxhip.Model(p, n_ctx, flags)
     gm.prefill(prompt)
     lg, tr = gm.step(nxt, trace=True)
     om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
@@ -93,7 +96,7 @@ def test_batched_prefill_then_step(mxh, tmp_path, name, n_ctx, n_prompt):
     assert ok, f"hidden trace error {e1}"
     ok, e2 = close_enough(lg, olg)
     assert ok, f"logits error {e2}"
-    # split-bf16 operands keep ~16 bits: far inside the bar, as the fp32 path
+    # split operands keep 16 (bf16) to 22 (fp16) bits: far inside the bar, as the fp32 path
     worst = max(e1 / max(1.0, float(np.abs(otr).max())), e2)
     assert worst < 1e-3, worst
     gm.close()
