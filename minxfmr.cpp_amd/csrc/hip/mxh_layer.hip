@@ -52,7 +52,7 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
 
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
 constexpr int kAttnChunk = 64;      // positions per pass of a workgroup (one per lane in the softmax)
-constexpr int kAttnMaxSplits = 128;  // workgroups per kv head (two per lane in the merge)
+constexpr int kAttnMaxSplits = 128;  // partials per kv head (two per lane in the merge)
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
 // wave; `src` is the raw projection, the result goes to dst (LDS).
@@ -140,12 +140,13 @@ __device__ __forceinline__ float fold_position_groups(float v) {
 // softmax (max, sum) across chunks, and the exp-weighted V sums stay in
 // registers, rescaled per chunk.
 //
-// The workgroup holding chunk pos/64 also prepares k and v of the current
-// token: it appends them (fp16) to the cache and uses its LDS copies for
-// position pos, so no workgroup reads a cache row written in this launch.
-// With one active workgroup the normalised output is written directly;
-// otherwise each writes (max, sum, V sums) per q head and the last to finish
-// merges them.  GM (4 or 8) bounds the q heads per kv head held in registers;
+// The current token's k and v are prepared, appended (fp16) to the cache and
+// used from LDS copies for position pos, so no workgroup reads a cache row
+// written in this launch: by the workgroup holding chunk pos/64 when the
+// context is one chunk (it then writes the normalised output directly), else
+// by an extra workgroup per kv head (blockIdx.y == S) whose partial is that
+// one position.  Each partial is (max, sum, V sums) per q head; the last
+// workgroup to finish merges them.  GM (4 or 8) bounds the q heads per kv head held in registers;
 // GM = 4 keeps the kernel near 128 VGPRs, so more workgroups are resident.
 template <int LPP, int GM>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
@@ -159,16 +160,28 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     __shared__ float wgt[kAttnMaxGroup][kAttnMaxSplits];
     __shared__ int last;
 
-    const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    // blockIdx.y < S: chunk splits; blockIdx.y == S: the current-token
+    // workgroup (see `sep`)
+    const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y - 1;
     const int group = a.nh / a.nkv, kvd = a.nkv * HD, qd = a.nh * HD;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = tid % LPP, pg = tid / LPP;
     const int pos = *a.pos, L = pos + 1;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk;
-    const int sact = nch < S ? nch : S;  // workgroups with work
-    if (s >= sact) return;
+    // With more than one chunk the partials are merged anyway, and the
+    // current token (q, k and v preparation, its k/v append and its own
+    // score) goes to a workgroup of its own instead of the chunk holding pos,
+    // which would otherwise finish a preparation round after the others.
+    // The chunks then cover the cached positions [0, pos) only (every chunk
+    // holds at least one of them).
+    const bool sep = L > kAttnChunk;
+    const int nch = ((sep ? pos : L) + kAttnChunk - 1) / kAttnChunk;
+    const int sact = nch < S ? nch : S;        // chunk workgroups with work
+    const int nparts = sact + (sep ? 1 : 0);  // partials to merge
+    const bool cur = s == S;
+    if (cur ? !sep : s >= sact) return;
     const int own_chunk = pos / kAttnChunk;
-    const bool owns = own_chunk % S == s;
+    const bool owns = cur || (!sep && own_chunk % S == s);
+    const int lim = sep ? pos : L;  // chunk positions below lim
     const size_t col = (size_t)g * HD + sub * 8;
 
     uint4 kraw[NP], vraw[NP];
@@ -181,8 +194,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             raw[i] = j < pos ? *reinterpret_cast<const uint4*>(cache + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
         }
     };
-    load(kraw, a.kc, s);
-    load(vraw, a.vc, s);
+    if (!cur) {
+        load(kraw, a.kc, s);
+        load(vraw, a.vc, s);
+    }
 
     // q heads (and k, v of the current token) of this kv head
     const double* cs = a.rope_cs + (size_t)pos * HD;  // (hd/2) pairs of (cos, sin)
@@ -228,8 +243,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     // scores in base-2 units (exp(x - m) == exp2(x log2 e - m log2 e)): the
     // running max and the split maxima below are in the same units
     const float scale2 = a.scale * 1.4426950408889634f;
-    for (int c = s; c < nch; c += S) {
-        if (c == own_chunk) {
+    for (int c = cur ? nch : s; c < nch; c += S) {
+        if (!sep && c == own_chunk) {
 #pragma unroll
             for (int i = 0; i < NP; ++i)
                 if (c * kAttnChunk + i * NPG + pg == pos) {
@@ -250,7 +265,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
                 d = lane_group_sum<LPP>(d);
-                if (sub == 0) sc[h][jl] = j < L ? d * scale2 : -INFINITY;
+                if (sub == 0) sc[h][jl] = j < lim ? d * scale2 : -INFINITY;
             }
         }
         if (c + S < nch) load(kraw, a.kc, c + S);
@@ -293,43 +308,61 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         __syncthreads();  // sc and alpha are rewritten by the next chunk
     }
 
-    // sum the V partials of the position groups: lanes of a wave with the
-    // same `sub`, then the four waves through LDS
-#pragma unroll
-    for (int h = 0; h < GM; ++h) {
-        if (h >= group) break;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = fold_position_groups<LPP>(acc[h][e]);
-        if (lane < LPP) {
-            float4* dst = reinterpret_cast<float4*>(&red[wave][h][sub * 8]);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
-    }
-    __syncthreads();
-    float* part_v = a.part;                                 // [nh][S][hd]
-    float* part_ml = a.part + (size_t)a.nh * S * HD;        // [nh][S][2]
-    for (int i = tid; i < group * HD; i += 256) {
-        const int h = i / HD, t = i % HD;
-        const float v = red[0][h][t] + red[1][h][t] + red[2][h][t] + red[3][h][t];
-        const size_t qh = (size_t)g * group + h;
-        if (sact == 1) {
-            a.att[qh * HD + t] = v / run_l[h];
-        } else {
-            st_agent(part_v + (qh * S + s) * HD + t, v);
-            if (t == 0) {
-                st_agent(part_ml + (qh * S + s) * 2, run_m[h]);
-                st_agent(part_ml + (qh * S + s) * 2 + 1, run_l[h]);
+    const int SP = S + 1;                                   // partial slots per q head
+    float* part_v = a.part;                                 // [nh][SP][hd]
+    float* part_ml = a.part + (size_t)a.nh * SP * HD;       // [nh][SP][2]
+    if (cur) {
+        // the current token's partial (slot sact): score q_h . k with k and v
+        // rounded through fp16 as every cached position, max = that score,
+        // sum 1, V sums = v
+        for (int h = wave; h < group; h += 4) {
+            float d = 0.f;
+            for (int t = lane; t < HD; t += 64) d = fmaf(qs[h][t], __half2float(kvh[0][t]), d);
+            d = wave_sum_all(d) * scale2;
+            const size_t slot = ((size_t)g * group + h) * SP + sact;
+            for (int t = lane; t < HD; t += 64) st_agent(part_v + slot * HD + t, __half2float(kvh[1][t]));
+            if (lane == 0) {
+                st_agent(part_ml + slot * 2, d);
+                st_agent(part_ml + slot * 2 + 1, 1.0f);
             }
         }
+    } else {
+        // sum the V partials of the position groups: lanes of a wave with the
+        // same `sub`, then the four waves through LDS
+#pragma unroll
+        for (int h = 0; h < GM; ++h) {
+            if (h >= group) break;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h][e] = fold_position_groups<LPP>(acc[h][e]);
+            if (lane < LPP) {
+                float4* dst = reinterpret_cast<float4*>(&red[wave][h][sub * 8]);
+                dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+                dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+            }
+        }
+        __syncthreads();
+        for (int i = tid; i < group * HD; i += 256) {
+            const int h = i / HD, t = i % HD;
+            const float v = red[0][h][t] + red[1][h][t] + red[2][h][t] + red[3][h][t];
+            const size_t qh = (size_t)g * group + h;
+            if (nparts == 1) {
+                a.att[qh * HD + t] = v / run_l[h];
+            } else {
+                st_agent(part_v + (qh * SP + s) * HD + t, v);
+                if (t == 0) {
+                    st_agent(part_ml + (qh * SP + s) * 2, run_m[h]);
+                    st_agent(part_ml + (qh * SP + s) * 2 + 1, run_l[h]);
+                }
+            }
+        }
+        if (nparts == 1) return;
     }
-    if (sact == 1) return;
 
     // the last workgroup of kv head g to finish merges the partials; they
     // were stored device-coherently and are complete before the count
     wait_mem();
     __syncthreads();
-    if (tid == 0) last = add_agent(a.counter + g, 1) == sact - 1;
+    if (tid == 0) last = add_agent(a.counter + g, 1) == nparts - 1;
     __syncthreads();
     if (!last) return;
     // (q head, 4 dims) items; the splits of an item are shared by `per`
@@ -340,19 +373,19 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     const int item = tid % items, part = tid / items;
     const int hi = item / (HD / 4), d4 = item % (HD / 4);
     // byte offsets into the V partials, read as 16-byte agent-coherent loads
-    const __amdgpu_buffer_rsrc_t prs = agent_rsrc(part_v, (int)((size_t)a.nh * S * HD * sizeof(float)));
-    const int src = (int)((((size_t)g * group + hi) * S * HD + 4 * d4) * sizeof(float));
+    const __amdgpu_buffer_rsrc_t prs = agent_rsrc(part_v, (int)((size_t)a.nh * SP * HD * sizeof(float)));
+    const int src = (int)((((size_t)g * group + hi) * SP * HD + 4 * d4) * sizeof(float));
     float4 pre[kPre];
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
         const int i = part + per * k;
-        pre[k] = part < per && i < sact ? ld_agent4(prs, src + i * HD * (int)sizeof(float))
+        pre[k] = part < per && i < nparts ? ld_agent4(prs, src + i * HD * (int)sizeof(float))
                                         : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     for (int h = wave; h < group; h += 4) {
         // splits lane and lane + 64
-        const float* ml = part_ml + ((size_t)g * group + h) * S * 2;
-        const bool in0 = lane < sact, in1 = lane + 64 < sact;
+        const float* ml = part_ml + ((size_t)g * group + h) * SP * 2;
+        const bool in0 = lane < nparts, in1 = lane + 64 < nparts;
         const float m0 = in0 ? ld_agent(ml + 2 * lane) : -INFINITY;
         const float l0 = in0 ? ld_agent(ml + 2 * lane + 1) : 0.f;
         const float m1 = in1 ? ld_agent(ml + 2 * lane + 128) : -INFINITY;
@@ -370,7 +403,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int k = 0; k < kPre; ++k) {
             const int i = part + per * k;
-            if (i < sact) {
+            if (i < nparts) {
                 const float w = wgt[hi][i];
                 s4.x = fmaf(w, pre[k].x, s4.x);
                 s4.y = fmaf(w, pre[k].y, s4.y);
@@ -379,7 +412,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             }
         }
 #pragma unroll 8
-        for (int i = part + per * kPre; i < sact; i += per) {
+        for (int i = part + per * kPre; i < nparts; i += per) {
             const float4 v = ld_agent4(prs, src + i * HD * (int)sizeof(float));
             const float w = wgt[hi][i];
             s4.x = fmaf(w, v.x, s4.x);
@@ -675,10 +708,10 @@ int attention_splits(int n_ctx, int nh, int nkv, int hd) {
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_kernel_for(nh, nkv, hd), 256, 0) != hipSuccess)
         n_cu = per_cu = 0;
-    const int cap = nkv > 0 ? per_cu * n_cu / nkv : 0;
+    const int cap = nkv > 0 ? per_cu * n_cu / nkv - 1 : 0;  // (one current-token workgroup per kv head)
     int S = (nch + 1) / 2;
     if (S > cap) S = cap;
-    if (S > kAttnMaxSplits) S = kAttnMaxSplits;
+    if (S > kAttnMaxSplits - 1) S = kAttnMaxSplits - 1;  // partials: S chunk splits and the current token
     return S < 64 ? 64 : S;
 }
 
@@ -690,7 +723,8 @@ bool attention_supported(int nh, int nkv, int hd) {
 
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
-    const dim3 grid(a.nkv, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
+    // chunk splits plus the current-token workgroup
+    const dim3 grid(a.nkv, attention_splits(n_ctx, a.nh, a.nkv, a.hd) + 1);
     const bool g4 = a.nh / a.nkv <= 4;
     switch (a.hd) {
     case 32:
@@ -709,9 +743,9 @@ int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     return MXH_OK;
 }
 
-// V partials [nh][S][hd] followed by (max, sum) pairs [nh][S][2]
+// V partials [nh][S + 1][hd] followed by (max, sum) pairs [nh][S + 1][2]
 size_t attention_scratch_floats(int nh, int nkv, int hd, int n_ctx) {
-    return (size_t)nh * attention_splits(n_ctx, nh, nkv, hd) * (hd + 2);
+    return (size_t)nh * (attention_splits(n_ctx, nh, nkv, hd) + 1) * (hd + 2);
 }
 
 int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,

@@ -76,9 +76,9 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
 
-// Split K: workgroup z takes K steps [z * ksteps, (z + 1) * ksteps), a
+// Split K: split z takes K steps [z * ksteps, (z + 1) * ksteps), a
 // multiple of 4 (whole super-blocks), and with more than one split writes
-// its scaled partial tile to part[z][m][n] for gemm_reduce.
+// its scaled partial tile to part[z][m][n] for gemm_f16_reduce.
 template <bool TILED>
 __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __restrict__ a_hi,
                                                            const uint16_t* __restrict__ a_lo, int lda,
@@ -98,10 +98,19 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __
     uint16_t* Bl = Bh + kQN * kRLd;
     float* dcol = reinterpret_cast<float*>(Bl + kQN * kRLd);  // [128] d of the current super-block
 
+    // Work item w = (split z, row tile y, column tile x), x fastest, and
+    // workgroup ids dealt so that XCD q (ids q, q + 8, ...) takes the
+    // contiguous range [q * per, (q + 1) * per) of items: the workgroups of
+    // one XCD share their activation rows (and K range) in its L2.
+    const int tn = (n + kQN - 1) / kQN, tm = (m + kQM - 1) / kQM, splits = (k / kQK + ksteps - 1) / ksteps;
+    const int total = tn * tm * splits, per = (int)gridDim.x / 8;
+    const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (wi >= total) return;
+    const int tx = wi % tn, ty = (wi / tn) % tm, tz = wi / (tn * tm);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wr = wave >> 1, wc = wave & 1;
-    const int m0 = blockIdx.y * kQM, n0 = blockIdx.x * kQN;
-    const int kb = blockIdx.z * ksteps * kQK, ke = min(k, kb + ksteps * kQK);
+    const int m0 = ty * kQM, n0 = tx * kQN;
+    const int kb = tz * ksteps * kQK, ke = min(k, kb + ksteps * kQK);
     const size_t rb = (size_t)(k / 256) * 144;
     // staging role: thread t owns row t / 2 of each tile and sub-block half t % 2 of the step
     const int t = threadIdx.x, r = t >> 1, h = t & 1;
@@ -243,8 +252,8 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __
         __syncthreads();
     }
 
-    const bool partial = gridDim.z > 1;
-    float* dst = partial ? part + (size_t)blockIdx.z * m * n : out;
+    const bool partial = splits > 1;
+    float* dst = partial ? part + (size_t)tz * m * n : out;
     const int ld = partial ? n : ldo;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -441,7 +450,9 @@ int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, con
     while (splits < 4 && tn * tm * splits * 2 <= 512 && steps % (splits * 2 * 4) == 0 &&
            (size_t)(splits * 2) * m * n <= part_floats)
         splits *= 2;
-    const dim3 grid(tn, tm, splits);
+    // one dimension of workgroup ids, a multiple of 8 (the kernel's XCD mapping)
+    const int items = tn * tm * splits;
+    const dim3 grid((unsigned)((items + 7) / 8 * 8));
     hipLaunchKernelGGL((gemm_q4k_f16_kernel<TILED>), grid, dim3(256), kQLds, st, a_hi, a_lo, lda, s_hi, s_lo, lds,
                        rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
     if (splits > 1)
