@@ -256,7 +256,9 @@ def main() -> int:
         "prefill_roofline": {"bound": "mfma", "achieved": round(pf_flops / (prefill_ms * 1e-3) / 1e12, 1),
                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(pf_flops / (prefill_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-                             "flops": pf_flops, "kernel": "dequant-to-bf16 MFMA GEMM (split hi+lo operands)"},
+                             "flops": pf_flops,
+                             "kernel": "whole prefill pass; projections on fp16 MFMA (exact Q4_K weight integers, "
+                                       "split hi+lo activations)"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(g_bytes_launch),
                      "kernel": "Q4_K dequant-GEMV, tiled weight layout (gemv_kernel<Q4KT>)",
