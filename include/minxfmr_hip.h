@@ -112,6 +112,16 @@ int mxh_dequant(int type, const void *w, float *out, int64_t rows, int64_t cols,
  * inputs for bf16 ones. */
 int mxh_gemm_q_bf16(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out, int form);
 
+/* Causal attention of m consecutive prompt tokens at positions p0 .. p0+m-1
+ * (transformer.cpp:529-629, per token: softmax of q.k / sqrt(hd) over cache
+ * positions 0 .. pos, then the weighted sum of V rows), on the fp16 matrix
+ * cores; device pointers.  q: [m][nh*hd] fp32 (after RoPE); kc, vc: the fp16
+ * cache [>= p0+m][nkv*hd] with rows 0 .. p0+m-1 written; att: [m][nh*hd].
+ * nh a multiple of nkv with at most 8 q heads per kv head, hd 32, 64 or 128.
+ * The batched prefill's attention step. */
+int mxh_attention_prefill(const float *q, const void *kc, const void *vc, float *att, int p0, int m, int nh, int nkv,
+                          int hd);
+
 /* ---- per-op backend interface (host pointers) ------------------------- */
 /* These keep the reference op semantics for drop-in use: host pointers in
  * and out, one synchronous device round trip per call.  Quantized weights

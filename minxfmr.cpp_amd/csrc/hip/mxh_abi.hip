@@ -242,6 +242,19 @@ int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t 
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
+int mxh_attention_prefill(const float* q, const void* kc, const void* vc, float* att, int p0, int m, int nh, int nkv,
+                          int hd) {
+    if (int rc = ensure_ready()) return rc;
+    if (!q || !kc || !vc || !att) return set_error(MXH_ERR_ARG, "attention_prefill: null pointer");
+    if (m <= 0 || p0 < 0 || !attention_supported(nh, nkv, hd))
+        return set_error(MXH_ERR_ARG, "attention_prefill: unsupported m %d p0 %d nh %d nkv %d hd %d", m, p0, nh, nkv,
+                         hd);
+    if (int rc = attention_rows_mfma_launch(q, (const __half*)kc, (const __half*)vc, att, p0, m, nh, nkv, hd,
+                                            1.0f / sqrtf((float)hd), g_ctx.stream))
+        return set_error(rc, "attention_prefill: launch");
+    return check_hip(hipGetLastError(), "attention_prefill launch");
+}
+
 int mxh_sample(const float* logits, int n, int top_k, double temperature, double top_p, double min_p, uint64_t seed,
                uint64_t draw, int* token) {
     if (int rc = ensure_ready()) return rc;

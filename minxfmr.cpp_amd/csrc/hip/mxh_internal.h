@@ -120,8 +120,10 @@ int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint
 int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,
                          const double* rope_cs, int p0, int m, float* q_out, __half* kc, __half* vc, int nh, int nkv,
                          int hd, int neox, float eps, hipStream_t st);
-int attention_rows_launch(const float* q, const __half* kc, const __half* vc, float* att, int p0, int m, int nh,
-                          int nkv, int hd, float scale, hipStream_t st);
+// causal attention of prompt tokens p0 .. p0+m-1 over the fp16 cache, on the
+// fp16 matrix cores (mxh_prefill_attn.hip)
+int attention_rows_mfma_launch(const float* q, const __half* kc, const __half* vc, float* att, int p0, int m, int nh,
+                               int nkv, int hd, float scale, hipStream_t st);
 int embed_rows_launch(int type, const void* w, const int* tokens, int p0, int m, float* x, int cols, int form,
                       hipStream_t st);
 

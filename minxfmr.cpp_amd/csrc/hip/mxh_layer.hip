@@ -477,128 +477,6 @@ __global__ __launch_bounds__(64) void qkv_prep_rows_kernel(const float* __restri
     }
 }
 
-// Causal attention of prompt tokens p0 .. p0+m-1 (transformer.cpp:529-629):
-// workgroup (g, z) serves the q heads of kv head g for token z over cache
-// positions 0 .. p0+z (the chunk's own rows were written by
-// qkv_prep_rows_kernel), in 64-position chunks with a running softmax, as
-// attention_kernel does for one token.
-template <int LPP>
-__global__ __launch_bounds__(256) void attention_rows_kernel(const float* __restrict__ q, const __half* __restrict__ kc,
-                                                             const __half* __restrict__ vc, float* __restrict__ att,
-                                                             int p0, int nh, int nkv, float scale) {
-    constexpr int HD = LPP * 8, NPG = 256 / LPP, NP = kAttnChunk / NPG;
-    __shared__ float qs[kAttnMaxGroup][HD];
-    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
-    __shared__ float run_m[kAttnMaxGroup], run_l[kAttnMaxGroup], alpha[kAttnMaxGroup];
-    __shared__ __align__(16) float red[4][kAttnMaxGroup][HD];
-    const int g = blockIdx.x, z = blockIdx.y;
-    const int group = nh / nkv, kvd = nkv * HD, qd = nh * HD;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int sub = tid % LPP, pg = tid / LPP;
-    const int L = p0 + z + 1;
-    const int nch = (L + kAttnChunk - 1) / kAttnChunk;
-    const size_t col = (size_t)g * HD + sub * 8;
-    uint4 kraw[NP], vraw[NP];
-    auto load = [&](uint4* raw, const __half* cache, int c) {
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int j = c * kAttnChunk + i * NPG + pg;
-            raw[i] = j < L ? *reinterpret_cast<const uint4*>(cache + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    load(kraw, kc, 0);
-    load(vraw, vc, 0);
-    for (int i = tid; i < group * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)z * qd + (size_t)g * group * HD + i];
-    if (tid < kAttnMaxGroup) {
-        run_m[tid] = -INFINITY;
-        run_l[tid] = 0.f;
-    }
-    __syncthreads();
-    float qreg[kAttnMaxGroup][8], acc[kAttnMaxGroup][8];
-#pragma unroll
-    for (int h = 0; h < kAttnMaxGroup; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            qreg[h][e] = h < group ? qs[h][sub * 8 + e] : 0.f;
-            acc[h][e] = 0.f;
-        }
-    for (int c = 0; c < nch; ++c) {
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int jl = i * NPG + pg, j = c * kAttnChunk + jl;
-            float kf[8];
-            half8_to_float(kraw[i], kf);
-#pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) {
-                if (h >= group) break;
-                float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
-                d = lane_group_sum<LPP>(d);
-                if (sub == 0) sc[h][jl] = j < L ? d * scale : -INFINITY;
-            }
-        }
-        if (c + 1 < nch) load(kraw, kc, c + 1);
-        __syncthreads();
-        for (int h = wave; h < group; h += 4) {
-            const float sv = sc[h][lane];
-            const float mo = run_m[h], mn = fmaxf(mo, wave_max_all(sv));
-            const float p = expf(sv - mn), al = expf(mo - mn);
-            const float ps = wave_sum_all(p);
-            sc[h][lane] = p;
-            if (lane == 0) {
-                run_m[h] = mn;
-                run_l[h] = run_l[h] * al + ps;
-                alpha[h] = al;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h) {
-            if (h >= group) break;
-            const float al = alpha[h];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= al;
-        }
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            float vf[8];
-            half8_to_float(vraw[i], vf);
-#pragma unroll
-            for (int h = 0; h < kAttnMaxGroup; ++h) {
-                if (h >= group) break;
-                const float p = sc[h][i * NPG + pg];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
-            }
-        }
-        if (c + 1 < nch) load(vraw, vc, c + 1);
-        __syncthreads();
-    }
-#pragma unroll
-    for (int h = 0; h < kAttnMaxGroup; ++h) {
-        if (h >= group) break;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = acc[h][e];
-#pragma unroll
-            for (int off = LPP; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-            acc[h][e] = v;
-        }
-        if (lane < LPP) {
-            float4* dst = reinterpret_cast<float4*>(&red[wave][h][sub * 8]);
-            dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-            dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
-    }
-    __syncthreads();
-    for (int i = tid; i < group * HD; i += 256) {
-        const int h = i / HD, t = i % HD;
-        const float v = red[0][h][t] + red[1][h][t] + red[2][h][t] + red[3][h][t];
-        att[(size_t)z * qd + ((size_t)g * group + h) * HD + t] = v / run_l[h];
-    }
-}
-
 // h[i] = silu(g[i]) * u[i], gu = [g | u]
 __global__ void silu_mul_kernel(const float* __restrict__ gu, float* __restrict__ h, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -754,18 +632,6 @@ int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const flo
     if (m <= 0 || !attention_supported(nh, nkv, hd)) return MXH_ERR_ARG;
     hipLaunchKernelGGL(qkv_prep_rows_kernel, dim3(m, nh + 2 * nkv), dim3(64), 0, st, qkv, ldq, bias, q_norm, k_norm,
                        rope_cs, p0, q_out, kc, vc, nh, nkv, hd, neox, eps);
-    return MXH_OK;
-}
-
-int attention_rows_launch(const float* q, const __half* kc, const __half* vc, float* att, int p0, int m, int nh,
-                          int nkv, int hd, float scale, hipStream_t st) {
-    if (m <= 0 || !attention_supported(nh, nkv, hd)) return MXH_ERR_ARG;
-    const dim3 grid(nkv, m);
-    switch (hd) {
-    case 32: hipLaunchKernelGGL(attention_rows_kernel<4>, grid, dim3(256), 0, st, q, kc, vc, att, p0, nh, nkv, scale); break;
-    case 64: hipLaunchKernelGGL(attention_rows_kernel<8>, grid, dim3(256), 0, st, q, kc, vc, att, p0, nh, nkv, scale); break;
-    default: hipLaunchKernelGGL(attention_rows_kernel<16>, grid, dim3(256), 0, st, q, kc, vc, att, p0, nh, nkv, scale); break;
-    }
     return MXH_OK;
 }
 

@@ -640,7 +640,8 @@ int enqueue_prefill_chunk(mxh_model* m, int p0, int rows, hipStream_t st) {
         }
         rc |= qkv_prep_rows_launch(m->pf_qkv, ldq, L.bias, L.q_norm, L.k_norm, m->rope_cs, p0, rows, m->pf_q, L.kc,
                                    L.vc, nh, nkv, hd, m->neox, c.eps, st);
-        rc |= attention_rows_launch(m->pf_q, L.kc, L.vc, m->pf_att, p0, rows, nh, nkv, hd, 1.0f / sqrtf((float)hd), st);
+        rc |= attention_rows_mfma_launch(m->pf_q, L.kc, L.vc, m->pf_att, p0, rows, nh, nkv, hd, 1.0f / sqrtf((float)hd),
+                                          st);
         rc |= prep_rows(m, {&L.o}, m->pf_att, qd, nullptr, 0.f, qd, rows, st);
         rc |= gemm(m, L.o, qd, m->pf_x, d, m->pf_x, rows, st);
         rc |= prep_rows(m, {&L.gu, &L.g, &L.u}, m->pf_x, d, L.ffn_norm, c.eps, d, rows, st);
