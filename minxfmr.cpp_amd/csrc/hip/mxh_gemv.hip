@@ -876,6 +876,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         static_assert(NS * kL <= 63, "short form: every step's loads in flight at once");
         Step sb[NS];
         auto issue_all = [&] {
+            // every wave's x loads are issued before any wave's weight loads,
+            // so x is not queued behind weights in the CU's memory pipeline
+            // (a bare s_barrier: no wait for the loads themselves)
+            __builtin_amdgcn_s_barrier();
 #pragma unroll
             for (int k = 0; k < NS; ++k) issue(ci, sb[k]);
             wait_vmcnt<NS * kL>();

@@ -410,15 +410,21 @@ __global__ __launch_bounds__(256) void silu_mul_f16_kernel(const float* __restri
     for (int u = 0; u < kRowSub; ++u) {
         const int sb = threadIdx.x + 256 * u;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            float hv = 0.f;
-            if (sb < nsb) {
-                const float gv = g[32 * sb + i], uv = g[f + 32 * sb + i];
-                hv = gv / (1.0f + expf(-gv)) * uv;
+        for (int i = 0; i < 32; ++i) v[u][i] = 0.f;
+        if (sb < nsb) {
+            // the sub-block's 32 gate and 32 up values as 16-byte loads
+            const float4* gp = reinterpret_cast<const float4*>(g + 32 * sb);
+            const float4* up = reinterpret_cast<const float4*>(g + f + 32 * sb);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 a = gp[q], b = up[q];
+                const float ga[4] = {a.x, a.y, a.z, a.w}, ub[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[u][4 * q + j] = ga[j] / (1.0f + expf(-ga[j])) * ub[j];
             }
-            v[u][i] = hv;
-            mx = fmaxf(mx, fabsf(hv));
         }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(v[u][i]));
     }
     const int e = row_exponent(block_max_256(mx, redf));
     const float scale = ldexpf(1.f, e);
