@@ -13,10 +13,12 @@
     # per-kernel time table from a --kernel-trace --stats run
     python3 -m mxhip.profiling stats OUT/trace/run_kernel_stats.csv
 
-    # MFMA utilisation of the prefill GEMMs
-    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16 -d OUT/mfma -o run \
-        --output-format csv -- python3 bench.py --steps 1 --warmup 0 --gemv-reps 1 --no-cpu-baseline
-    python3 -m mxhip.profiling mfma OUT/mfma
+    # MFMA utilisation of the prefill kernels: counters in one run, kernel
+    # durations from a --kernel-trace --stats run of the same command
+    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_F16 \
+        SQ_INSTS_VALU_MFMA_MOPS_BF16 -d OUT/mfma -o run --output-format csv -- python3 bench.py --steps 1 \
+        --warmup 0 --gemv-reps 1 --no-cpu-baseline --no-long-context
+    python3 -m mxhip.profiling mfma OUT/mfma OUT/trace/run_kernel_stats.csv
 
 The workload runs every Q4_K GEMV of the model (per layer: fused q|k|v, o,
 fused gate|up, down) `reps` times, as the bench's roofline pass does, and
@@ -146,11 +148,14 @@ def traffic(fetch_dir: str, write_dir: str) -> None:
     print(f"TRAFFIC_PER_LAUNCH_BYTES={tot_traffic / len(SHAPES):.0f}")
 
 
-def mfma(d: str) -> None:
+def mfma(d: str, stats_csv: str | None = None) -> None:
     """Per-kernel MFMA utilisation from a run with
-    --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_BF16:
+    --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_BF16:
     busy cycles / (GUI-active cycles x SIMDs) (rocprofv3's MfmaUtil), and the
-    bf16 MFMA flops issued (512 per MOP)."""
+    fp16 + bf16 MFMA flops issued (512 per MOP).  With the kernel stats CSV of
+    a --kernel-trace --stats run of the same command, also the issued flop
+    rate over each kernel's average duration, against the 2.5 PFLOP/s dense
+    fp16/bf16 peak."""
     rows = _counter_rows(d)
     simds = None
     agent = glob.glob(os.path.join(d, "**", "*agent_info.csv"), recursive=True)
@@ -161,19 +166,36 @@ def mfma(d: str) -> None:
                     simds = int(r.get("Simd_Count") or r.get("SIMD_Count") or 0) or None
     busy = _per_dispatch(rows, "SQ_VALU_MFMA_BUSY_CYCLES")
     gui = _per_dispatch(rows, "GRBM_GUI_ACTIVE", max)
-    mops = _per_dispatch(rows, "SQ_INSTS_VALU_MFMA_MOPS_BF16")
+    mops = {}
+    for cnt in ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_VALU_MFMA_MOPS_BF16"):
+        for name, vals in _per_dispatch(rows, cnt).items():
+            acc = mops.setdefault(name, [0.0] * len(vals))
+            for i, v in enumerate(vals):
+                acc[i] += v
+    dur_us = {}
+    if stats_csv:
+        with open(stats_csv, newline="") as fh:
+            for r in csv.DictReader(fh):
+                dur_us[r["Name"]] = float(r["AverageNs"]) / 1e3
     simds = simds or 1024
-    print(f"| kernel | dispatches | MFMA busy (% of SIMD cycles) | bf16 MFMA GFLOP per dispatch |")
-    print("|---|---:|---:|---:|")
+    short = lambda name: re.sub(r"\([^()]*\)$", "", name.replace("mxh::(anonymous namespace)::", "").replace("void ", ""))
+    print("| kernel | dispatches | MFMA busy (% of SIMD cycles) | MFMA GFLOP issued per dispatch | avg us "
+          "| issued TFLOP/s | % of 2.5 PFLOP/s |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
     for name in busy:
         if name not in gui:
             continue
         b, g = busy[name], gui[name]
         util = 100.0 * sum(b) / (sum(g) * simds) if sum(g) else 0.0
-        fl = sum(mops.get(name, [0])) * 512 / max(1, len(mops.get(name, [1]))) / 1e9
-        short = name.replace("mxh::(anonymous namespace)::", "").replace("void ", "")
-        short = re.sub(r"\([^()]*\)$", "", short)
-        print(f"| `{short}` | {len(b)} | {util:.1f} | {fl:.1f} |")
+        m = mops.get(name, [0.0])
+        fl = sum(m) * 512 / max(1, len(m)) / 1e9
+        us = next((v for k, v in dur_us.items() if short(k) == short(name)), None)
+        if us:
+            tflops = fl / us * 1e3  # GFLOP per us = PFLOP/s
+            print(f"| `{short(name)}` | {len(b)} | {util:.1f} | {fl:.1f} | {us:.1f} | {tflops:.0f} | "
+                  f"{100.0 * tflops / 2500.0:.1f} |")
+        else:
+            print(f"| `{short(name)}` | {len(b)} | {util:.1f} | {fl:.1f} | - | - | - |")
     print(f"\nSIMDs: {simds}")
 
 
@@ -209,7 +231,7 @@ def main(argv: list[str]) -> int:
     elif cmd == "stats":
         stats(argv[1])
     elif cmd == "mfma":
-        mfma(argv[1])
+        mfma(argv[1], argv[2] if len(argv) > 2 else None)
     else:
         print(__doc__)
         return 2
