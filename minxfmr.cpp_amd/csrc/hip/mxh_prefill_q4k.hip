@@ -18,7 +18,8 @@
 // 2^-e.  Reference op: backend_matmul_rhs_transposed with m > 1
 // (src/backend/backend_runtime.cpp:302-319).
 //
-// Tiles: 128 x 128 outputs per workgroup of 4 waves, each wave 64 x 64 as
+// Tiles: 128 x TN outputs per workgroup of 2 TN / 64 waves (TN = 128 or
+// 256 weight rows, q4_wide_tiles below), each wave 64 x 64 as
 // 2 x 2 blocks of v_mfma_f32_32x32x16_f16 (lane l supplies row / column
 // l % 32 at k = 8 (l / 32) .. +8; accumulator register i of lane l is row
 // 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32).  K steps of 64 elements
@@ -36,11 +37,14 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kQM = 128, kQN = 128, kQK = 64;
+constexpr int kQM = 128, kQK = 64;  // tile rows (activations) and K step; TN weight rows per tile
 constexpr int kQLd = kQK + 8;   // tile row stride in fp16 (144 bytes)
 constexpr int kRing = 16;       // sub-blocks per correction round
 constexpr int kRLd = kRing + 8; // ring row stride in fp16 (48 bytes)
-constexpr size_t kQLds = (size_t)(3 * kQM * kQLd + 4 * kQM * kRLd) * 2 + kQN * sizeof(float);
+template <int TN>
+constexpr size_t q4_lds_bytes() {
+    return (size_t)((2 * kQM + TN) * kQLd + 2 * (kQM + TN) * kRLd) * 2 + TN * sizeof(float);
+}
 
 __device__ __forceinline__ uint16_t f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
 
@@ -79,8 +83,8 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
 // Split K: split z takes K steps [z * ksteps, (z + 1) * ksteps), a
 // multiple of 4 (whole super-blocks), and with more than one split writes
 // its scaled partial tile to part[z][m][n] for gemm_f16_reduce.
-template <bool TILED>
-__global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __restrict__ a_hi,
+template <bool TILED, int TN>
+__global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel(const uint16_t* __restrict__ a_hi,
                                                            const uint16_t* __restrict__ a_lo, int lda,
                                                            const uint16_t* __restrict__ s_hi,
                                                            const uint16_t* __restrict__ s_lo, int lds,
@@ -89,33 +93,41 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __
                                                            const float* res, int m, int n, int k, int form, int ksteps,
                                                            float* __restrict__ part) {
     extern __shared__ __align__(16) uint16_t smem[];
+    // waves: 2 (activation row halves) x TN / 64 (weight row quarters of 64)
+    constexpr int WC = TN / 64;
+    // activation staging: APT threads per activation row, EPT elements each
+    constexpr int APT = 2 * TN / kQM, EPT = kQK / APT;
     uint16_t* Ah = smem;              // [128][kQLd] activations, hi
     uint16_t* Al = Ah + kQM * kQLd;   // lo
-    uint16_t* Ws = Al + kQM * kQLd;   // [128][kQLd] weights sc q
-    uint16_t* Sh = Ws + kQN * kQLd;   // [128][kRLd] sub-block sums, hi (ring of 16 sub-blocks)
+    uint16_t* Ws = Al + kQM * kQLd;   // [TN][kQLd] weights sc q
+    uint16_t* Sh = Ws + TN * kQLd;    // [128][kRLd] sub-block sums, hi (ring of 16 sub-blocks)
     uint16_t* Sl = Sh + kQM * kRLd;
-    uint16_t* Bh = Sl + kQM * kRLd;   // [128][kRLd] -dmin m_j per weight row, hi
-    uint16_t* Bl = Bh + kQN * kRLd;
-    float* dcol = reinterpret_cast<float*>(Bl + kQN * kRLd);  // [128] d of the current super-block
+    uint16_t* Bh = Sl + kQM * kRLd;   // [TN][kRLd] -dmin m_j per weight row, hi
+    uint16_t* Bl = Bh + TN * kRLd;
+    float* dcol = reinterpret_cast<float*>(Bl + TN * kRLd);  // [TN] d of the current super-block
 
     // Work item w = (split z, row tile y, column tile x), x fastest, and
     // workgroup ids dealt so that XCD q (ids q, q + 8, ...) takes the
     // contiguous range [q * per, (q + 1) * per) of items: the workgroups of
     // one XCD share their activation rows (and K range) in its L2.
-    const int tn = (n + kQN - 1) / kQN, tm = (m + kQM - 1) / kQM, splits = (k / kQK + ksteps - 1) / ksteps;
+    const int tn = (n + TN - 1) / TN, tm = (m + kQM - 1) / kQM, splits = (k / kQK + ksteps - 1) / ksteps;
     const int total = tn * tm * splits, per = (int)gridDim.x / 8;
     const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (wi >= total) return;
     const int tx = wi % tn, ty = (wi / tn) % tm, tz = wi / (tn * tm);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
-    const int m0 = ty * kQM, n0 = tx * kQN;
+    const int wr = wave / WC, wc = wave % WC;
+    const int m0 = ty * kQM, n0 = tx * TN;
     const int kb = tz * ksteps * kQK, ke = min(k, kb + ksteps * kQK);
     const size_t rb = (size_t)(k / 256) * 144;
-    // staging role: thread t owns row t / 2 of each tile and sub-block half t % 2 of the step
+    // staging roles: thread t owns weight row t / 2 of the tile and sub-block
+    // half t % 2 of the step, and activation row ra = t / APT, elements
+    // EPT aq .. of the step (aq = t % APT), with the sum of sub-block sa
     const int t = threadIdx.x, r = t >> 1, h = t & 1;
+    const int ra = t / APT, aq = t % APT, sa = aq * EPT / 32;
+    const bool s_owner = (aq * EPT) % 32 == 0;
     const int wrow = min(n0 + r, n - 1);
-    const bool arow = m0 + r < m;
+    const bool arow = m0 + ra < m;
     const int lr = lane & 31, lk = 8 * (lane >> 5);
 
     f32x16 acc[2][2], P[2][2];
@@ -127,20 +139,23 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __
             for (int e = 0; e < 16; ++e) acc[i][j][e] = P[i][j][e] = 0.f;
 
     // rows past m read row m - 1 and are zeroed when staged
-    const int arow_c = min(m0 + r, m - 1);
-    const uint16_t* pa_h = a_hi + (size_t)arow_c * lda + 32 * h;
-    const uint16_t* pa_l = a_lo + (size_t)arow_c * lda + 32 * h;
-    const uint16_t* ps_h = s_hi + (size_t)arow_c * lds + h;
-    const uint16_t* ps_l = s_lo + (size_t)arow_c * lds + h;
-    uint4 ah0, ah1, ah2, ah3, al0, al1, al2, al3;
+    const int arow_c = min(m0 + ra, m - 1);
+    const uint16_t* pa_h = a_hi + (size_t)arow_c * lda + EPT * aq;
+    const uint16_t* pa_l = a_lo + (size_t)arow_c * lda + EPT * aq;
+    const uint16_t* ps_h = s_hi + (size_t)arow_c * lds + sa;
+    const uint16_t* ps_l = s_lo + (size_t)arow_c * lds + sa;
+    constexpr int AV = EPT / 8;  // 16-byte pieces per thread and limb
+    uint4 ahv[AV], alv[AV];
     uint32_t sh_g, sl_g;
     Q4Chunk<TILED> wq;
 #define MXH_Q4F16_FETCH(K0)                                                   \
     do {                                                                     \
         const uint4* qh_ = reinterpret_cast<const uint4*>(pa_h + (K0));      \
         const uint4* ql_ = reinterpret_cast<const uint4*>(pa_l + (K0));      \
-        ah0 = qh_[0]; ah1 = qh_[1]; ah2 = qh_[2]; ah3 = qh_[3];              \
-        al0 = ql_[0]; al1 = ql_[1]; al2 = ql_[2]; al3 = ql_[3];              \
+        _Pragma("unroll") for (int v_ = 0; v_ < AV; ++v_) {                  \
+            ahv[v_] = qh_[v_];                                               \
+            alv[v_] = ql_[v_];                                               \
+        }                                                                    \
         sh_g = ps_h[(K0) >> 5];                                              \
         sl_g = ps_l[(K0) >> 5];                                              \
         wq.fetch(w, rb, wrow, (K0));                                         \
@@ -149,22 +164,21 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_f16_kernel(const uint16_t* __
 
     int step = 0;
     for (int k0 = kb; k0 < ke; k0 += kQK, ++step) {
-        const int slot = 2 * (step & 7) + h;
+        const int slot = 2 * (step & 7) + h;  // ring slot of this thread's weight sub-block
         {
-            uint4* dh = reinterpret_cast<uint4*>(Ah + r * kQLd + 32 * h);
-            uint4* dl = reinterpret_cast<uint4*>(Al + r * kQLd + 32 * h);
+            uint4* dh = reinterpret_cast<uint4*>(Ah + ra * kQLd + EPT * aq);
+            uint4* dl = reinterpret_cast<uint4*>(Al + ra * kQLd + EPT * aq);
             const uint32_t am = arow ? 0xffffffffu : 0u;
             auto msk = [am](uint4 v) { return make_uint4(v.x & am, v.y & am, v.z & am, v.w & am); };
-            dh[0] = msk(ah0);
-            dh[1] = msk(ah1);
-            dh[2] = msk(ah2);
-            dh[3] = msk(ah3);
-            dl[0] = msk(al0);
-            dl[1] = msk(al1);
-            dl[2] = msk(al2);
-            dl[3] = msk(al3);
-            Sh[r * kRLd + slot] = (uint16_t)(sh_g & am);
-            Sl[r * kRLd + slot] = (uint16_t)(sl_g & am);
+#pragma unroll
+            for (int v = 0; v < AV; ++v) {
+                dh[v] = msk(ahv[v]);
+                dl[v] = msk(alv[v]);
+            }
+            if (s_owner) {
+                Sh[ra * kRLd + 2 * (step & 7) + sa] = (uint16_t)(sh_g & am);
+                Sl[ra * kRLd + 2 * (step & 7) + sa] = (uint16_t)(sl_g & am);
+            }
             // weights of sub-block j = 2 g + h as the integers sc_j q (tensor.cpp:395-432
             // with the scale form `form`); bytes i of the chunk's 32 qs hold element i
             // (low nibble) and element 32 + i (high nibble)
@@ -438,29 +452,34 @@ __global__ __launch_bounds__(256) void silu_mul_f16_kernel(const float* __restri
     }
 }
 
-template <bool TILED>
+// TN = 128: 4 waves, two workgroups per CU; TN = 256: 8 waves, one per CU,
+// each activation tile staged once for twice the weight rows (half the
+// activation traffic per MFMA)
+template <bool TILED, int TN>
 int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
                         const uint16_t* s_lo, int lds, const float* rscale, const uint8_t* w, float* out, int ldo,
                         const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
                         hipStream_t st) {
+    constexpr size_t lds_bytes = q4_lds_bytes<TN>();
     static bool attr_set = false;  // above 64 KiB of LDS needs the opt-in, once per kernel
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)gemm_q4k_f16_kernel<TILED>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kQLds) != hipSuccess)
+        if (hipFuncSetAttribute((const void*)gemm_q4k_f16_kernel<TILED, TN>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess)
             return MXH_ERR_HIP;
         attr_set = true;
     }
-    const int tn = (n + kQN - 1) / kQN, tm = (m + kQM - 1) / kQM, steps = k / kQK;
+    const int tn = (n + TN - 1) / TN, tm = (m + kQM - 1) / kQM, steps = k / kQK;
     // split K (whole super-blocks, at most 4 ways) while the tile grid leaves CUs idle
+    constexpr int target = TN == 128 ? 512 : 256;  // resident workgroups
     int splits = 1;
-    while (splits < 4 && tn * tm * splits * 2 <= 512 && steps % (splits * 2 * 4) == 0 &&
+    while (splits < 4 && tn * tm * splits * 2 <= target && steps % (splits * 2 * 4) == 0 &&
            (size_t)(splits * 2) * m * n <= part_floats)
         splits *= 2;
     // one dimension of workgroup ids, a multiple of 8 (the kernel's XCD mapping)
     const int items = tn * tm * splits;
     const dim3 grid((unsigned)((items + 7) / 8 * 8));
-    hipLaunchKernelGGL((gemm_q4k_f16_kernel<TILED>), grid, dim3(256), kQLds, st, a_hi, a_lo, lda, s_hi, s_lo, lds,
-                       rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
+    hipLaunchKernelGGL((gemm_q4k_f16_kernel<TILED, TN>), grid, dim3(2 * TN), lds_bytes, st, a_hi, a_lo, lda, s_hi,
+                       s_lo, lds, rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
     if (splits > 1)
         hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
                            res, m, n);
@@ -468,6 +487,15 @@ int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, con
 }
 
 }  // namespace
+
+// Wide (256-row) weight tiles stage each activation tile once for twice the
+// weight rows; with one 8-wave workgroup per CU they are worth it only when
+// the whole tile grid fits in one round (measured at M = 512: o, down and
+// q|k|v 3-5% faster, gate|up with 384 tiles 13% slower).
+bool q4_wide_tiles(int m, int n) {
+    const int tiles = ((n + 255) / 256) * ((m + kQM - 1) / kQM);
+    return m > kQM && n >= 2048 && tiles <= 256;
+}
 
 bool gemm_q4k_f16_supported(int type, int k) {
     return (type == MXH_Q4_K || type == MXH_Q4_K_TILED) && k % 256 == 0 && k <= kRowSub * 256 * 32;
@@ -480,11 +508,17 @@ int gemm_q4k_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int l
     if (m <= 0 || n <= 0 || !gemm_q4k_f16_supported(type, k) || lda < k || lds < k / 32 || ldo < n) return MXH_ERR_ARG;
     if (!part) part_floats = 0;
     const uint8_t* wb = (const uint8_t*)w;
+    if (q4_wide_tiles(m, n))
+        return type == MXH_Q4_K_TILED
+                   ? gemm_q4k_f16_launch<true, 256>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n,
+                                                    k, form, part, part_floats, st)
+                   : gemm_q4k_f16_launch<false, 256>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m,
+                                                     n, k, form, part, part_floats, st);
     return type == MXH_Q4_K_TILED
-               ? gemm_q4k_f16_launch<true>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
-                                           part, part_floats, st)
-               : gemm_q4k_f16_launch<false>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
-                                            part, part_floats, st);
+               ? gemm_q4k_f16_launch<true, 128>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
+                                                form, part, part_floats, st)
+               : gemm_q4k_f16_launch<false, 128>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
+                                                 form, part, part_floats, st);
 }
 
 int rows_to_f16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a_hi, uint16_t* a_lo,

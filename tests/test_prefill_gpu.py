@@ -81,7 +81,20 @@ def test_batched_prefill_then_step(mxh, tmp_path, name, n_ctx, n_prompt, flags):
     within the parity bar of the oracle run token by token (fp16 cache).
     Default: Q4_K projections on the exact-weight fp16 GEMM, the rest split
     bf16; MODEL_BF16_PREFILL: every projection split bf16."""
-    p = build(tmp_path, name)
+    prefill_vs_oracle(tmp_path, name, n_ctx, n_prompt, flags)
+
+
+def test_batched_prefill_wide_tiles(mxh, tmp_path):
+    """Projections of at least 2048 rows with more than 128 prompt rows take
+    the Q4_K GEMM's 256-row weight tiles (8 waves per workgroup); the tiny
+    shapes above take the 128-row tiles.  Hidden size 2048 puts q|k|v, o,
+    gate|up and down on the wide tiles."""
+    prefill_vs_oracle(tmp_path, "q4k-qknorm", 600, 530, 0, n_embd=2048, n_head=16, n_head_kv=4, head_dim=128,
+                      n_ff=2048)
+
+
+def prefill_vs_oracle(tmp_path, name, n_ctx, n_prompt, flags, **over):
+    p = build(tmp_path, name, **over)
     rng = np.random.default_rng(17)
     prompt = rng.integers(0, TINY["n_vocab"], n_prompt).astype(np.int32)
     nxt = int(rng.integers(0, TINY["n_vocab"]))
