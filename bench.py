@@ -14,7 +14,9 @@ dominant kernel, the Q4_K dequant-GEMV, timed with HIP events over every
 Q4_K GEMV of the model on its own HBM-resident weights (`traffic` is the
 HBM bytes per launch that rocprofv3 counters measured for the same shapes,
 profiles/gemv_q4k_traffic.json); `cpu_baseline` is the CPU oracle decoding a
-bounded sample of the same model on the host cores.
+bounded sample of the same model on the host cores.  Also reported:
+`gemv_microbench` (the isolated Q4_K GEMV shapes),
+`long_context`, and with --all-configs configs[0] and [3].
 """
 from __future__ import annotations
 
@@ -130,6 +132,51 @@ def run_long_context(mxhip, path: Path, seed: int) -> dict:
     return out
 
 
+def run_gemv_microbench(mxhip, seed: int) -> dict:
+    """the isolated Q4_K dequant-GEMV at batch 1 over the
+    four listed shapes, with the weights regrouped into the tiled layout
+    (mxh_tile_rows) as the model holds them.  Each shape rotates over at least
+    512 MB of distinct weight copies (more than the 256 MB Infinity Cache), so
+    every launch streams from HBM; 200 launches back to back on the library
+    stream, timed with HIP events.  The block bytes are random with small
+    finite d, dmin (timing does not depend on the values; parity at these
+    shapes is in tests/test_gemv_gpu.py)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed + 2)
+    out = []
+    for n, k in ((4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)):
+        rb = k // 256 * 144
+        wbytes = n * rb
+        blocks = rng.integers(0, 256, wbytes, dtype=np.uint8).reshape(-1, 144)
+        blocks[:, 0:4] = np.frombuffer(np.array([0x1400, 0x1000], np.uint16).tobytes(), np.uint8)  # d, dmin
+        copies = max(2, -(-(512 << 20) // wbytes))
+        bufs = []
+        for _ in range(copies):
+            b = mxhip.DeviceBuffer(wbytes)
+            b.upload(blocks)
+            tiled = mxhip.tile_rows(mxhip.Q4_K, b, n, k)
+            bufs.append(b)
+        x = mxhip.DeviceBuffer.from_array(rng.standard_normal(k, dtype=np.float32))
+        y = mxhip.DeviceBuffer(4 * n)
+        for i in range(10):
+            mxhip.gemv(tiled, bufs[i % copies], x, y, n, k)
+        mxhip.synchronize()
+        launches = 200
+        with mxhip.Timer() as tm:
+            for i in range(launches):
+                mxhip.gemv(tiled, bufs[i % copies], x, y, n, k)
+        us = tm.ms * 1e3 / launches
+        alg = wbytes + 4 * k + 4 * n
+        out.append({"shape": f"{n}x{k}", "algorithmic_bytes": alg, "us": round(us, 2),
+                    "gbs": round(alg / us / 1e3, 1), "frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4),
+                    "copies": copies})
+        for b in bufs + [x, y]:
+            b.close()
+    log(f"GEMV microbench: " + ", ".join(f"{r['shape']} {r['us']} us {r['gbs']} GB/s" for r in out))
+    return {"type": "Q4_K (tiled layout)", "launches": 200, "shapes": out}
+
+
 def run_extra_configs(mxhip, seed: int) -> dict:
     """BASELINE configs 0 and 3: Qwen3-0.6B Q8_0 greedy (32-token prompt, 128
     tokens) and Llama-3-8B mixed Q4_K/Q5_K with seeded top-k 8, T 0.8 sampling
@@ -181,6 +228,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="enqueue kernels directly instead of replaying HIP graphs")
     ap.add_argument("--no-long-context", action="store_true", help="skip the 8192-token context measurement")
+    ap.add_argument("--no-microbench", action="store_true", help="skip the isolated Q4_K GEMV shapes")
     ap.add_argument("--all-configs", action="store_true",
                     help="also run BASELINE configs 0 (Qwen3-0.6B Q8_0) and 3 (Llama-3-8B mixed, sampled)")
     args = ap.parse_args()
@@ -264,6 +312,8 @@ def main() -> int:
                      "kernel": "Q4_K dequant-GEMV, tiled weight layout (gemv_kernel<Q4KT>)",
                      "per_launch_bytes": int(g_bytes_launch), "avg_launch_us": round(g_avg_us, 3)},
     }
+    if not args.no_microbench:
+        out["gemv_microbench"] = run_gemv_microbench(mxhip, args.seed)
     if not args.no_long_context:
         out["long_context"] = run_long_context(mxhip, path, args.seed)
     if args.all_configs:

@@ -34,6 +34,9 @@ enum {
     MXH_Q5_K = 13
 };
 
+/* flag of the tiled weight layout (mxh_tile_rows): MXH_TILED_FLAG | type */
+#define MXH_TILED_FLAG 0x100
+
 /* Q4_K/Q5_K 6-bit scale unpacking.  MXH_FORM_REF is the reference CPU
  * decoder (src/tensor/tensor.cpp:395-403) and the default; MXH_FORM_GGML is
  * the ggml decoder used by the reference CUDA kernels
@@ -89,10 +92,22 @@ int mxh_timer_end(float *ms);
 
 /* y[n] = sum_k x[k] * dequant(W[n, k]) for W a row-major [n x k] tensor of
  * raw GGUF blocks (k a multiple of the block size).  W must be 16-byte
- * aligned for Q4_K/Q5_K/F32 and 4-byte aligned for Q8_0/Q5_0.
+ * aligned for Q4_K/Q5_K/F32 and 4-byte aligned for Q8_0/Q5_0.  `type` may
+ * also be the tiled id mxh_tile_rows returned for W's rows (16-byte aligned).
  * Replaces the m == 1 case of backend_matmul_rhs_transposed
  * (src/backend/backend_runtime.cpp:266-376, cuda_backend.cu:1198-1415). */
 int mxh_gemv(int type, const void *w, const float *x, float *y, int64_t n, int64_t k, int form);
+
+/* Regroups the bytes of each of `rows` device rows of `cols` elements in
+ * place into the tiled order the GEMV reads fastest (every 16-byte load of a
+ * wave within whole cache lines), and sets *tiled to the type id to pass to
+ * mxh_gemv from then on: MXH_TILED_FLAG | type for Q4_K, Q5_K and Q8_0 with
+ * cols a multiple of 256 up to 15360; otherwise the rows are left as they
+ * are and *tiled = type.  W must be 16-byte aligned.  Results through the
+ * tiled rows are identical to those through the GGUF rows.  No reference
+ * counterpart: the reference has one weight layout, the GGUF block order the
+ * CUDA backend uploads (cuda_backend.cu:364-394). */
+int mxh_tile_rows(int type, void *w, int64_t rows, int64_t cols, int *tiled);
 
 /* out[m x n] = A[m x k] . dequant(W[n x k])^T for any m (prefill).
  * Replaces backend_matmul_rhs_transposed (src/backend/backend_runtime.h:37). */

@@ -201,12 +201,30 @@ int mxh_gemv(int type, const void* w, const float* x, float* y, int64_t n, int64
     if (int rc = ensure_ready()) return rc;
     if (int rc = check_weight_ptr(type, w)) return rc;
     if (!x || !y || !aligned(x, 16)) return set_error(MXH_ERR_ARG, "x must be non-null and 16-byte aligned");
-    if (n <= 0 || k <= 0 || type >= kTiledFlag || row_bytes(type, k) == 0)
+    if (type >= kTiledFlag && (type != (kTiledFlag | storage_type(type)) || tiled_type(storage_type(type), k) != type))
+        return set_error(MXH_ERR_ARG, "gemv: type %d is not the tiled form of rows of %lld columns", type, (long long)k);
+    if (n <= 0 || k <= 0 || row_bytes(type, k) == 0)
         return set_error(MXH_ERR_ARG, "gemv: k=%lld is not a whole number of type-%d blocks", (long long)k, type);
     int rc = gemv_launch(type, w, x, y, nullptr, n, k, form, g_ctx.stream);
     if (rc == MXH_ERR_ARG) return set_error(rc, "gemv: unsupported shape n=%lld k=%lld", (long long)n, (long long)k);
     if (rc == MXH_ERR_UNSUPPORTED) return set_error(rc, "gemv: unsupported type %d", type);
     return check_hip(hipGetLastError(), "gemv launch");
+}
+
+static_assert(MXH_TILED_FLAG == kTiledFlag, "public and internal tiled flags differ");
+
+int mxh_tile_rows(int type, void* w, int64_t rows, int64_t cols, int* tiled) {
+    if (int rc = ensure_ready()) return rc;
+    if (!w || !tiled || rows <= 0 || cols <= 0 || type >= kTiledFlag || row_bytes(type, cols) == 0)
+        return set_error(MXH_ERR_ARG, "tile_rows: bad arguments (type %d, %lld x %lld)", type, (long long)rows,
+                         (long long)cols);
+    if (!aligned(w, 16)) return set_error(MXH_ERR_ARG, "tile_rows: weight pointer must be 16-byte aligned");
+    const int t = tiled_type(type, cols);
+    if (t != type) {
+        if (int rc = tile_rows_launch(type, w, rows, cols, g_ctx.stream)) return set_error(rc, "tile_rows: launch");
+    }
+    *tiled = t;
+    return check_hip(hipGetLastError(), "tile_rows launch");
 }
 
 int mxh_matmul_rhs_t(int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k, float* out, int form) {

@@ -18,7 +18,8 @@ struct BlockGeom {
 // Device-resident layouts that no GGUF file holds: the blocks of each row
 // regrouped in tiles so that the 16-byte loads of one wave instruction read
 // whole cache lines (see q4k_tile_offsets / q80_tile_offsets).  A row keeps
-// the byte count of its GGUF type; the C ABI never accepts these ids.
+// the byte count of its GGUF type.  The C ABI takes these ids only in
+// mxh_gemv, for rows that mxh_tile_rows regrouped (MXH_TILED_FLAG == kTiledFlag).
 constexpr int kTiledFlag = 0x100;
 constexpr int MXH_Q4_K_TILED = kTiledFlag | MXH_Q4_K;
 constexpr int MXH_Q8_0_TILED = kTiledFlag | MXH_Q8_0;

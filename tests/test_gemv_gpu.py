@@ -104,6 +104,38 @@ def test_gemv_vs_oracle(mxh, name, n, k):
         check_close(got, want)
 
 
+TILE_CASES = [("Q4_K", 12288, 4096, True), ("Q4_K", 1000, 14336, True), ("Q4_K", 24, 2816, True),
+              ("Q5_K", 4096, 14336, True), ("Q8_0", 1024, 4096, True),
+              ("Q8_0", 3, 32, False), ("Q5_0", 7, 256, False)]
+
+
+@pytest.mark.parametrize("name,n,k,tiles", TILE_CASES, ids=[f"{a}-{b}x{c}" for a, b, c, _ in TILE_CASES])
+def test_tiled_rows_give_identical_gemv(mxh, name, n, k, tiles):
+    """mxh_tile_rows regroups rows in place into the tiled order (Q4_K, Q5_K,
+    Q8_0 with k a multiple of 256 up to 15360) and returns the id mxh_gemv then
+    takes; the products are bit-identical to those over the GGUF rows.  Other
+    shapes and types (Q8_0 rows of 32, Q5_0) are left as they are and keep
+    their id; every Q4_K shape the GEMV takes is tileable."""
+    t = TYPES[name]
+    rng = np.random.default_rng(n * 7 + k)
+    w = mxo.quantize(t, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    x = rng.standard_normal(k, dtype=np.float32)
+    wb, xb, yb = mxh.DeviceBuffer.from_array(w), mxh.DeviceBuffer.from_array(x), mxh.DeviceBuffer(4 * n)
+    mxh.gemv(t, wb, xb, yb, n, k)
+    y0 = yb.download(np.float32, n)
+    tt = mxh.tile_rows(t, wb, n, k)
+    assert tt == ((t | mxh.TILED_FLAG) if tiles else t)
+    if tiles:
+        assert not np.array_equal(wb.download(np.uint8, w.size), w.ravel()), "rows were not regrouped"
+    mxh.gemv(tt, wb, xb, yb, n, k)
+    assert np.array_equal(yb.download(np.float32, n), y0)
+    if not tiles:
+        with pytest.raises(mxh.MxhError, match="tiled form"):
+            mxh.gemv(t | mxh.TILED_FLAG, wb, xb, yb, n, k)
+    for b in (wb, xb, yb):
+        b.close()
+
+
 def test_gemv_reference_kat_blocks(mxh):
     """Crafted blocks of the reference parity test, every row the same, x = ones."""
     import json
