@@ -84,6 +84,50 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
                       f"by the C oracle with {threads} OpenMP threads, {el:.1f}s"}
 
 
+def cpu_reference_gemv(budget_s: float, seed: int) -> dict | None:
+    """The reference's own CPU GEMV (backend_matmul_rhs_transposed from its
+    sources, built into oracle/_ref/libmxref.so with OpenMP) on the four
+    Q4_K shapes of BASELINE config 1, random blocks with small finite d, dmin,
+    x ~ N(0, 1); each shape repeated within an equal share of the time budget.
+    None when the library was not built."""
+    import numpy as np
+
+    import mxo
+
+    ref = mxo.load_ref()
+    if ref is None:
+        return None
+    rng = np.random.default_rng(seed + 3)
+    shapes, tot_bytes, tot_s = [], 0, 0.0
+    for n, k in ((4096, 4096), (12288, 4096), (4096, 12288), (151936, 4096)):
+        w = rng.integers(0, 256, n * (k // 256) * 144, dtype=np.uint8).reshape(-1, 144)
+        w[:, 0:4] = np.frombuffer(np.array([0x1400, 0x1000], np.uint16).tobytes(), np.uint8)
+        x = rng.standard_normal(k, dtype=np.float32)
+        y = np.empty(n, np.float32)
+        args = (mxo.Q4_K, x.ctypes.data, 1, k, w.ctypes.data, n, y.ctypes.data)
+        if ref.ref_matmul_rhs_t(*args) != 0:
+            return None
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            ref.ref_matmul_rhs_t(*args)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el > budget_s / 4 or calls >= 200:
+                break
+        alg = w.nbytes + 4 * k + 4 * n
+        shapes.append({"shape": f"{n}x{k}", "us": round(el / calls * 1e6, 1), "gbs": round(alg / (el / calls) / 1e9, 2),
+                       "calls": calls})
+        tot_bytes += alg
+        tot_s += el / calls
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    return {"value": round(tot_bytes / tot_s / 1e9, 2),
+            "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": "the reference's backend_matmul_rhs_transposed (its CPU sources, OpenMP) on the four Q4_K shapes "
+                      "of BASELINE config 1, each repeated for about a quarter of the budget; value = algorithmic bytes "
+                      "of one call per shape over the summed per-call times",
+            "shapes": shapes}
+
+
 LLAMA3_MIXED = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336, n_vocab=128256,
                     ctx=8192, rope_theta=5e5, eps=1e-5, qk_norm=False, tied=False)
 QWEN3_06B = dict(n_layer=28, n_embd=1024, n_head=16, n_head_kv=8, head_dim=128, n_ff=3072, n_vocab=151936,
@@ -320,6 +364,10 @@ def main() -> int:
         out["configs"] = run_extra_configs(mxhip, args.seed)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(path, prompt, args.cpu_seconds, min(16, os.cpu_count() or 8))
+        if not args.no_microbench:
+            ref_gemv = cpu_reference_gemv(8.0, args.seed)
+            if ref_gemv:
+                out["cpu_baseline_gemv_reference"] = ref_gemv
     print(json.dumps(out), flush=True)
     return 0
 
