@@ -757,7 +757,17 @@ __device__ __forceinline__ void consume_steps(F&& consume_k, int total) {
 // NS = 0: persistent loop, two steps of loads ahead.  NS > 0: short form,
 // at most NS steps per wave (the launcher sizes the grid for it).
 template <template <int> class T, int R, int MODE, int NS>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+// The arguments a wave needs first (weights, x, norm weight, n, k) also come
+// as leading scalars, which the command processor preloads into SGPRs
+// (-amdgpu-kernarg-preload-count), so the first loads do not wait for a
+// kernel-argument fetch; the rest stay in GemvArgs.
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const float* px, const float* pnw, int pn,
+                                                        int pk, GemvArgs a) {
+    a.w = pw;
+    a.x = px;
+    a.norm_w = pnw;
+    a.n = pn;
+    a.k = pk;
     using Ty = T<R>;
     using Buf = typename Ty::Buf;
     extern __shared__ float xs[];
@@ -1057,10 +1067,10 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
                     if (grid > resident_grid(ks, lds)) return false;
                     if (mode == GEMV_PLAIN)
                         hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, NSv>), dim3((unsigned)grid), dim3(kThreads),
-                                           lds, st, a);
+                                           lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
                     else
                         hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, NSv>), dim3((unsigned)grid), dim3(kThreads),
-                                           lds, st, a);
+                                           lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
                     return true;
                 }
             };
@@ -1079,12 +1089,15 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
         cap = n_cu;
     const unsigned grid = (unsigned)(need < cap ? need : cap);
     if (mode == GEMV_PLAIN)
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, 0>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
+                           a.n, a.k, a);
     else if (mode == GEMV_SILU)
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, 0>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
+                           a.n, a.k, a);
     else {
         if ((int)grid > a.red_cap) return MXH_ERR_ARG;
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, 0>), dim3(grid), dim3(kThreads), lds, st, a);
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
+                           a.n, a.k, a);
         hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, st, a.red_val, a.red_idx, (int)grid, a.tokens,
                            a.pos);
     }

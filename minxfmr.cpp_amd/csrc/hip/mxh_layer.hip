@@ -149,7 +149,14 @@ __device__ __forceinline__ float fold_position_groups(float v) {
 // workgroup to finish merges them.  GM (4 or 8) bounds the q heads per kv head held in registers;
 // GM = 4 keeps the kernel near 128 VGPRs, so more workgroups are resident.
 template <int LPP, int GM>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+// pos, the caches and q|k|v, needed first, also come as leading scalars that
+// the command processor preloads into SGPRs (-amdgpu-kernarg-preload-count).
+__global__ __launch_bounds__(256) void attention_kernel(const int* ppos, __half* pkc, __half* pvc, const float* pqkv,
+                                                        AttnArgs a) {
+    a.pos = ppos;
+    a.kc = pkc;
+    a.vc = pvc;
+    a.qkv = pqkv;
     constexpr int HD = LPP * 8, NPG = 256 / LPP, NP = kAttnChunk / NPG;
     __shared__ float qs[kAttnMaxGroup][HD];
     __shared__ float kvt[HD];
@@ -606,16 +613,16 @@ int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     const bool g4 = a.nh / a.nkv <= 4;
     switch (a.hd) {
     case 32:
-        if (g4) hipLaunchKernelGGL((attention_kernel<4, 4>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((attention_kernel<4, 8>), grid, dim3(256), 0, st, a);
+        if (g4) hipLaunchKernelGGL((attention_kernel<4, 4>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
+        else hipLaunchKernelGGL((attention_kernel<4, 8>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
         break;
     case 64:
-        if (g4) hipLaunchKernelGGL((attention_kernel<8, 4>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((attention_kernel<8, 8>), grid, dim3(256), 0, st, a);
+        if (g4) hipLaunchKernelGGL((attention_kernel<8, 4>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
+        else hipLaunchKernelGGL((attention_kernel<8, 8>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
         break;
     default:
-        if (g4) hipLaunchKernelGGL((attention_kernel<16, 4>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((attention_kernel<16, 8>), grid, dim3(256), 0, st, a);
+        if (g4) hipLaunchKernelGGL((attention_kernel<16, 4>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
+        else hipLaunchKernelGGL((attention_kernel<16, 8>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
         break;
     }
     return MXH_OK;
