@@ -492,7 +492,7 @@ int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, con
 // weight rows; with one 8-wave workgroup per CU they are worth it only when
 // the whole tile grid fits in one round (measured at M = 512: o, down and
 // q|k|v 3-5% faster, gate|up with 384 tiles 13% slower).
-bool q4_wide_tiles(int m, int n) {
+static bool q4_wide_tiles(int m, int n) {
     const int tiles = ((n + 255) / 256) * ((m + kQM - 1) / kQM);
     return m > kQM && n >= 2048 && tiles <= 256;
 }
