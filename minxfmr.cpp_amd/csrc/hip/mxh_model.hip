@@ -250,8 +250,9 @@ int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out)
     c.eps = (float)f.arch_num("attention.layer_norm_rms_epsilon", 1e-6);
     c.rope_theta = (float)f.arch_num("rope.freq_base", 10000.0);
     c.n_ctx = n_ctx;
-    // head width from key_length when present (the reference
-    // derives it from n_embd / n_head, wrong for Qwen3-0.6B)
+    // head width from key_length when present (the reference derives it as
+    // n_embd / n_head, minxfmr.cpp:1119-1122, which is wrong for Qwen3-0.6B:
+    // 16 heads of 128 over a hidden size of 1024)
     c.head_dim = (int)f.arch_num("attention.key_length", c.n_head > 0 ? c.n_embd / c.n_head : 0);
     m->form = (flags & MXH_MODEL_GGML_FORM) ? MXH_FORM_GGML : MXH_FORM_REF;
     m->neox = (flags & MXH_MODEL_ROPE_NEOX) ? 1 : 0;

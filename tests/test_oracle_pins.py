@@ -44,7 +44,8 @@ def test_q4k_kat_reference_form():
 
 
 def test_q4k_kat_ggml_form():
-    """The ggml decoder gives -17 at [128]: sc = 0, m = 17."""
+    """The ggml decoder gives -17 at [128] where the reference CPU form gives
+    -1 (test_cuda_quantized_matmul.cpp:18-42 pins -1): sc = 0, m = 17."""
     blk = np.frombuffer(bytes.fromhex(KAT["Q4_K"]["block_hex"]), np.uint8)
     y = mxo.dequant(mxo.Q4_K, blk, 1, 256, mxo.FORM_GGML)[0]
     want = np.zeros(256, np.float32)
