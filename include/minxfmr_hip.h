@@ -127,6 +127,18 @@ int mxh_dequant(int type, const void *w, float *out, int64_t rows, int64_t cols,
  * inputs for bf16 ones. */
 int mxh_gemm_q_bf16(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out, int form);
 
+/* out[m x n] = a[m x k] . dequant(w[n x k])^T on the fp16 matrix cores with
+ * every weight exact: the MFMAs multiply the integer codes (Q4_K / Q5_K:
+ * sc * q; Q8_0: q; Q5_0: q - 16), exact in fp16, and the block scales are
+ * applied to fp32 partial sums (K-quant mins by a second contraction over
+ * sub-block sums).  a enters as fp16 hi + lo of a * 2^e per row (about 22
+ * significant bits).  Device pointers, a and w 16-byte aligned; type Q4_K,
+ * Q5_K, Q8_0 or Q5_0 (or a tiled id of mxh_tile_rows), k a multiple of 256 up
+ * to 16384.  The prefill contraction the model runs: the reference's
+ * backend_matmul_rhs_transposed with m > 1
+ * (src/backend/backend_runtime.cpp:302-319). */
+int mxh_gemm_q_f16(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out, int form);
+
 /* Causal attention of m consecutive prompt tokens at positions p0 .. p0+m-1
  * (transformer.cpp:529-629, per token: softmax of q.k / sqrt(hd) over cache
  * positions 0 .. pos, then the weighted sum of V rows), on the fp16 matrix

@@ -260,6 +260,32 @@ int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t 
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
+int mxh_gemm_q_f16(int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k, float* out, int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (!a || !w || !out) return set_error(MXH_ERR_ARG, "gemm_f16: null pointer");
+    if (m <= 0 || n <= 0 || k <= 0 || m > INT32_MAX || n > INT32_MAX || !gemm_q_f16_supported(type, (int)k))
+        return set_error(MXH_ERR_ARG, "gemm_f16: bad shape %lldx%lldx%lld for type %d", (long long)m, (long long)n,
+                         (long long)k, type);
+    if (((uintptr_t)w & 15) || ((uintptr_t)a & 15))
+        return set_error(MXH_ERR_ARG, "gemm_f16: a and w must be 16-byte aligned");
+    // staging: a as fp16 hi / lo of a 2^e, the split sub-block sums, 2^-e per row
+    const size_t mk = (size_t)m * (size_t)k, nsb = mk / 32;
+    void* buf = nullptr;
+    if (int rc = stage(2, 4 * mk + 4 * nsb + 4 * (size_t)m, &buf)) return rc;
+    uint16_t* a_hi = static_cast<uint16_t*>(buf);
+    uint16_t* a_lo = a_hi + mk;
+    uint16_t* s_hi = a_lo + mk;
+    uint16_t* s_lo = s_hi + nsb;
+    float* rscale = reinterpret_cast<float*>(s_lo + nsb);
+    if (int rc = rows_to_f16_launch(a, (int)k, nullptr, 0.f, (int)k, a_hi, a_lo, (int)k, s_hi, s_lo, (int)k / 32, rscale,
+                                    (int)m, g_ctx.stream))
+        return set_error(rc, "gemm_f16: conversion launch");
+    if (int rc = gemm_q_f16_run(type, a_hi, a_lo, (int)k, s_hi, s_lo, (int)k / 32, rscale, w, out, (int)n, nullptr,
+                                (int)m, (int)n, (int)k, form, nullptr, 0, g_ctx.stream))
+        return set_error(rc, "gemm_f16: launch");
+    return check_hip(hipGetLastError(), "gemm_f16 launch");
+}
+
 int mxh_attention_prefill(const float* q, const void* kc, const void* vc, float* att, int p0, int m, int nh, int nkv,
                           int hd) {
     if (int rc = ensure_ready()) return rc;

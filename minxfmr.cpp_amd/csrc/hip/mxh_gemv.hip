@@ -18,15 +18,19 @@
 // decoding happens in registers.  A row's 64 lane partials are reduced with
 // cross-lane shuffles.
 //
-// Integer inner products.  For the quantized formats x is staged as 16-bit
+// Integer inner products.  For the quantized formats x is staged as 24-bit
 // block fixed point: per 32-element sub-block j, X_i = rint(x_i / s_j) with
-// s_j = max|x| / 32512 (up to one float rounding of x_i / s_j before the
-// rint), split into two signed bytes X = 256*hi + lo.  The
-// codes q are small integers, so sum_i X_i q_i is exact in int32 and costs
-// two v_dot4_i32_i8 per four elements (no per-element conversion).  With
+// s_j = max|x| / kXMax (kXMax = 8355000, so |X| < 0x7f7f7f), split into three
+// signed bytes X = 65536 hi + 256 mid + lo.  The codes q are small integers,
+// so each limb's sum_i L_i q_i is exact in int32 at three v_dot4_i32_i8 per
+// four elements (no per-element conversion), and 256 hi-sum + mid-sum is
+// still exact in int32.  With
 //   sum_i x_i (d*sc*q_i - dmin*m) = d*sc*s_j * sum_i X_i q_i - dmin*m * s_j * sum_i X_i
-// the only approximation is x's 16-bit rounding (relative 2^-16 of the
-// sub-block maximum); the weights are used exactly.
+// the approximations are x's rounding to 24 bits (half a unit of 2^-23 of
+// the sub-block maximum, the size of a float rounding of that maximum) and
+// float roundings of the per-sub-block sums: errors of the order of an fp32
+// dot product's, while the weights are used exactly.  A NaN in x makes its
+// sub-block scale NaN, so it reaches the outputs as in fp32 arithmetic.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -61,8 +65,6 @@ __device__ __forceinline__ double block_sum(const double* red) {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef short short2v __attribute__((ext_vector_type(2)));
-typedef unsigned short ushort2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // x index -> padded LDS index (4 floats of padding after every 64)
@@ -121,16 +123,22 @@ __device__ __forceinline__ void load_block_2aligned(const uint8_t* base, size_t 
 }
 
 // ---- staged x in LDS ------------------------------------------------------
-// Quantized formats: lo/hi limb bytes (K each, 4 per dword, with 4 dwords of
-// padding after every 16 so that lanes reading consecutive 64-element runs
-// hit distinct banks), per-32 scales (K/32) and per-16 scaled sums
-// s_j * sum X_i (K/16).
+// Quantized formats: lo/mid/hi limb bytes (K each, 4 per dword, with 4
+// dwords of padding after every 16 so that lanes reading consecutive
+// 64-element runs hit distinct banks), per-32 scales (K/32) and per-16 scaled
+// sums s_j * sum X_i (K/16).
 struct XQ {
     const uint32_t* lo;
+    const uint32_t* mid;
     const uint32_t* hi;
     const float* scale;
     const float* sum16;
 };
+
+// 24-bit fixed point: X = rint(x * kXMax / max|x|) stays within
+// [-0x7f7f7f, 0x7f7f7f] (kXMax leaves room for the reciprocal's error), the
+// range in which X + 0x808080 has three bytes that are the limbs plus 128
+constexpr float kXMax = 8355000.0f;
 
 // dword index of limb dword d (elements 4d..4d+3) in the padded arrays
 __device__ __forceinline__ int limb(int d) { return d + ((d >> 4) << 2); }
@@ -140,17 +148,25 @@ __host__ __device__ constexpr int limb_dwords(int k) { return k / 4 + k / 16; }
 // instead of needing a per-lane guard.
 __host__ __device__ constexpr int xq_cap(int k) { return (k + kThreads * 4 - 1) / (kThreads * 4) * (kThreads * 4); }
 __host__ __device__ constexpr int xq_dwords(int k) {
-    return 2 * limb_dwords(xq_cap(k)) + xq_cap(k) / 32 + xq_cap(k) / 16;
+    return 3 * limb_dwords(xq_cap(k)) + xq_cap(k) / 32 + xq_cap(k) / 16;
 }
 
 __device__ __forceinline__ XQ xq_view(const float* smem, int k) {
     const uint32_t* lo = reinterpret_cast<const uint32_t*>(smem);
     const int n = limb_dwords(xq_cap(k));
-    return XQ{lo, lo + n, reinterpret_cast<const float*>(lo + 2 * n),
-              reinterpret_cast<const float*>(lo + 2 * n) + xq_cap(k) / 32};
+    return XQ{lo, lo + n, lo + 2 * n, reinterpret_cast<const float*>(lo + 3 * n),
+              reinterpret_cast<const float*>(lo + 3 * n) + xq_cap(k) / 32};
 }
 
 __device__ __forceinline__ uint4 lds16(const uint32_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// the three limbs of 16 staged elements (limb dwords d .. d+3)
+struct XP {
+    uint4 l, m, h;
+};
+__device__ __forceinline__ XP xp_load(const XQ& x, int d) {
+    return XP{lds16(x.lo + limb(d)), lds16(x.mid + limb(d)), lds16(x.hi + limb(d))};
+}
 
 // s_waitcnt vmcnt(N): wait until at most N vector memory operations of this
 // wave are outstanding (they complete in issue order for loads); expcnt and
@@ -167,17 +183,38 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// sum over 16 elements of X_i q_i given the four dwords of lo/hi limbs and q bytes
-__device__ __forceinline__ float dot16(uint4 xl, uint4 xh, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3) {
-    int l = sdot4(xl.x, q0, 0);
-    l = sdot4(xl.y, q1, l);
-    l = sdot4(xl.z, q2, l);
-    l = sdot4(xl.w, q3, l);
-    int h = sdot4(xh.x, q0, 0);
-    h = sdot4(xh.y, q1, h);
-    h = sdot4(xh.z, q2, h);
-    h = sdot4(xh.w, q3, h);
-    return (float)(h * 256 + l);  // |result| < 2^24: exact
+// per-limb integer sums of X_i q_i
+struct LimbSum {
+    int l, m, h;
+};
+__device__ __forceinline__ LimbSum limb_zero() { return LimbSum{0, 0, 0}; }
+// add 16 elements: the limbs of x against the code bytes q0..q3
+__device__ __forceinline__ void limb_acc(LimbSum& a, const XP& x, uint32_t q0, uint32_t q1, uint32_t q2,
+                                         uint32_t q3) {
+    a.l = sdot4(x.l.x, q0, a.l);
+    a.m = sdot4(x.m.x, q0, a.m);
+    a.h = sdot4(x.h.x, q0, a.h);
+    a.l = sdot4(x.l.y, q1, a.l);
+    a.m = sdot4(x.m.y, q1, a.m);
+    a.h = sdot4(x.h.y, q1, a.h);
+    a.l = sdot4(x.l.z, q2, a.l);
+    a.m = sdot4(x.m.z, q2, a.m);
+    a.h = sdot4(x.h.z, q2, a.h);
+    a.l = sdot4(x.l.w, q3, a.l);
+    a.m = sdot4(x.m.w, q3, a.m);
+    a.h = sdot4(x.h.w, q3, a.h);
+}
+// sum_i X_i q_i = 65536 h + 256 m + l.  Over at most 32 elements with
+// |q| <= 128 each limb sum is at most 2^19 in magnitude, so 256 h + m is exact
+// in int32; the float result takes one rounding (two for codes above 16)
+__device__ __forceinline__ float limb_total(const LimbSum& a) {
+    return fmaf((float)(a.h * 256 + a.m), 256.0f, (float)a.l);
+}
+// sum over 16 elements of X_i q_i
+__device__ __forceinline__ float dot16(const XP& x, uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3) {
+    LimbSum a = limb_zero();
+    limb_acc(a, x, q0, q1, q2, q3);
+    return limb_total(a);
 }
 
 // 6-bit (scale, min) of sub-blocks 2g and 2g+1 as byte pairs, without
@@ -238,10 +275,7 @@ struct Q4K {
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int form, float (&acc)[R]) {
         const int blk = c >> 2, g = c & 3;
         const int d0 = 64 * blk + 16 * g;  // limb dword of element e0 = 256 blk + 64 g
-        const uint4 xl0 = lds16(x.lo + limb(d0)), xl1 = lds16(x.lo + limb(d0 + 4));
-        const uint4 xl2 = lds16(x.lo + limb(d0 + 8)), xl3 = lds16(x.lo + limb(d0 + 12));
-        const uint4 xh0 = lds16(x.hi + limb(d0)), xh1 = lds16(x.hi + limb(d0 + 4));
-        const uint4 xh2 = lds16(x.hi + limb(d0 + 8)), xh3 = lds16(x.hi + limb(d0 + 12));
+        const XP x0 = xp_load(x, d0), x1 = xp_load(x, d0 + 4), x2 = xp_load(x, d0 + 8), x3 = xp_load(x, d0 + 12);
         const int j0 = d0 >> 3;  // sub-block 2g of the row
         const float sa = x.scale[j0], sb = x.scale[j0 + 1];
         const float ta = x.sum16[2 * j0] + x.sum16[2 * j0 + 1], tb = x.sum16[2 * j0 + 2] + x.sum16[2 * j0 + 3];
@@ -259,24 +293,13 @@ struct Q4K {
             const uint32_t mnp = (B & mA) | ((C >> 4) & mC) | ((B >> 2) & mT);
             const uint4 qa = b.qa[r], qb = b.qb[r];
             // low nibbles: elements e0..e0+31; high nibbles: e0+32..e0+63
-            int la = sdot4(xl0.x, qa.x & 0x0f0f0f0fu, 0), ha = sdot4(xh0.x, qa.x & 0x0f0f0f0fu, 0);
-            la = sdot4(xl0.y, qa.y & 0x0f0f0f0fu, la); ha = sdot4(xh0.y, qa.y & 0x0f0f0f0fu, ha);
-            la = sdot4(xl0.z, qa.z & 0x0f0f0f0fu, la); ha = sdot4(xh0.z, qa.z & 0x0f0f0f0fu, ha);
-            la = sdot4(xl0.w, qa.w & 0x0f0f0f0fu, la); ha = sdot4(xh0.w, qa.w & 0x0f0f0f0fu, ha);
-            la = sdot4(xl1.x, qb.x & 0x0f0f0f0fu, la); ha = sdot4(xh1.x, qb.x & 0x0f0f0f0fu, ha);
-            la = sdot4(xl1.y, qb.y & 0x0f0f0f0fu, la); ha = sdot4(xh1.y, qb.y & 0x0f0f0f0fu, ha);
-            la = sdot4(xl1.z, qb.z & 0x0f0f0f0fu, la); ha = sdot4(xh1.z, qb.z & 0x0f0f0f0fu, ha);
-            la = sdot4(xl1.w, qb.w & 0x0f0f0f0fu, la); ha = sdot4(xh1.w, qb.w & 0x0f0f0f0fu, ha);
-            int lb = sdot4(xl2.x, (qa.x >> 4) & 0x0f0f0f0fu, 0), hb = sdot4(xh2.x, (qa.x >> 4) & 0x0f0f0f0fu, 0);
-            lb = sdot4(xl2.y, (qa.y >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh2.y, (qa.y >> 4) & 0x0f0f0f0fu, hb);
-            lb = sdot4(xl2.z, (qa.z >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh2.z, (qa.z >> 4) & 0x0f0f0f0fu, hb);
-            lb = sdot4(xl2.w, (qa.w >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh2.w, (qa.w >> 4) & 0x0f0f0f0fu, hb);
-            lb = sdot4(xl3.x, (qb.x >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.x, (qb.x >> 4) & 0x0f0f0f0fu, hb);
-            lb = sdot4(xl3.y, (qb.y >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.y, (qb.y >> 4) & 0x0f0f0f0fu, hb);
-            lb = sdot4(xl3.z, (qb.z >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.z, (qb.z >> 4) & 0x0f0f0f0fu, hb);
-            lb = sdot4(xl3.w, (qb.w >> 4) & 0x0f0f0f0fu, lb); hb = sdot4(xh3.w, (qb.w >> 4) & 0x0f0f0f0fu, hb);
-            // |256 h + l| <= 32 * 32512 * 15 < 2^24: exact as float
-            const float da = (float)(ha * 256 + la), db = (float)(hb * 256 + lb);
+            constexpr uint32_t kN = 0x0f0f0f0fu;
+            LimbSum la = limb_zero(), lb = limb_zero();
+            limb_acc(la, x0, qa.x & kN, qa.y & kN, qa.z & kN, qa.w & kN);
+            limb_acc(la, x1, qb.x & kN, qb.y & kN, qb.z & kN, qb.w & kN);
+            limb_acc(lb, x2, (qa.x >> 4) & kN, (qa.y >> 4) & kN, (qa.z >> 4) & kN, (qa.w >> 4) & kN);
+            limb_acc(lb, x3, (qb.x >> 4) & kN, (qb.y >> 4) & kN, (qb.z >> 4) & kN, (qb.w >> 4) & kN);
+            const float da = limb_total(la), db = limb_total(lb);
             float a = acc[r];
             a = fmaf(dd.x * (float)(scp & 0xffu) * sa, da, a);
             a = fmaf(-(dd.y * (float)(mnp & 0xffu)), ta, a);
@@ -327,8 +350,7 @@ struct Q5K {
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int form, float (&acc)[R]) {
         const int blk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
         const int e0 = 256 * blk + 64 * g + 16 * h;
-        const uint4 xla = lds16(x.lo + limb(e0 / 4)), xha = lds16(x.hi + limb(e0 / 4));
-        const uint4 xlb = lds16(x.lo + limb(e0 / 4 + 8)), xhb = lds16(x.hi + limb(e0 / 4 + 8));
+        const XP xa = xp_load(x, e0 / 4), xb = xp_load(x, e0 / 4 + 8);
         const float sa = x.scale[e0 >> 5], sb = x.scale[(e0 >> 5) + 1];
         const float ta = x.sum16[e0 >> 4], tb = x.sum16[(e0 >> 4) + 2];
 #pragma unroll
@@ -344,8 +366,8 @@ struct Q5K {
                 lo[i] = (q[i] & 0x0f0f0f0fu) | (((hb[i] >> (2 * g)) & 0x01010101u) << 4);
                 hi[i] = ((q[i] >> 4) & 0x0f0f0f0fu) | (((hb[i] >> (2 * g + 1)) & 0x01010101u) << 4);
             }
-            const float da = dot16(xla, xha, lo[0], lo[1], lo[2], lo[3]);
-            const float db = dot16(xlb, xhb, hi[0], hi[1], hi[2], hi[3]);
+            const float da = dot16(xa, lo[0], lo[1], lo[2], lo[3]);
+            const float db = dot16(xb, hi[0], hi[1], hi[2], hi[3]);
             float a = acc[r];
             a = fmaf(dd.x * (float)(scp & 0xffu) * sa, da, a);
             a = fmaf(-(dd.y * (float)(mnp & 0xffu)), ta, a);
@@ -389,8 +411,7 @@ struct Q80 {
     }
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        const uint4 xl0 = lds16(x.lo + limb(e0 / 4)), xh0 = lds16(x.hi + limb(e0 / 4));
-        const uint4 xl1 = lds16(x.lo + limb(e0 / 4 + 4)), xh1 = lds16(x.hi + limb(e0 / 4 + 4));
+        const XP x0 = xp_load(x, e0 / 4), x1 = xp_load(x, e0 / 4 + 4);
         const float s = x.scale[c];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -399,8 +420,10 @@ struct Q80 {
             uint32_t q[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) q[i] = (b.bd[r][i] >> 16) | (b.bd[r][i + 1] << 16);
-            const float v = dot16(xl0, xh0, q[0], q[1], q[2], q[3]) + dot16(xl1, xh1, q[4], q[5], q[6], q[7]);
-            acc[r] = fmaf(d * s, v, acc[r]);
+            LimbSum ls = limb_zero();
+            limb_acc(ls, x0, q[0], q[1], q[2], q[3]);
+            limb_acc(ls, x1, q[4], q[5], q[6], q[7]);
+            acc[r] = fmaf(d * s, limb_total(ls), acc[r]);
         }
     }
 };
@@ -429,14 +452,14 @@ struct Q80T {
     }
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        const uint4 xl0 = lds16(x.lo + limb(e0 / 4)), xh0 = lds16(x.hi + limb(e0 / 4));
-        const uint4 xl1 = lds16(x.lo + limb(e0 / 4 + 4)), xh1 = lds16(x.hi + limb(e0 / 4 + 4));
+        const XP x0 = xp_load(x, e0 / 4), x1 = xp_load(x, e0 / 4 + 4);
         const float s = x.scale[c];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float v = dot16(xl0, xh0, b.lo[r].x, b.lo[r].y, b.lo[r].z, b.lo[r].w) +
-                            dot16(xl1, xh1, b.hi[r].x, b.hi[r].y, b.hi[r].z, b.hi[r].w);
-            acc[r] = fmaf(h2f(b.d[r]) * s, v, acc[r]);
+            LimbSum ls = limb_zero();
+            limb_acc(ls, x0, b.lo[r].x, b.lo[r].y, b.lo[r].z, b.lo[r].w);
+            limb_acc(ls, x1, b.hi[r].x, b.hi[r].y, b.hi[r].z, b.hi[r].w);
+            acc[r] = fmaf(h2f(b.d[r]) * s, limb_total(ls), acc[r]);
         }
     }
 };
@@ -456,8 +479,7 @@ struct Q50 {
     }
     static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
         const int e0 = 32 * c;
-        const uint4 xl0 = lds16(x.lo + limb(e0 / 4)), xh0 = lds16(x.hi + limb(e0 / 4));
-        const uint4 xl1 = lds16(x.lo + limb(e0 / 4 + 4)), xh1 = lds16(x.hi + limb(e0 / 4 + 4));
+        const XP x0 = xp_load(x, e0 / 4), x1 = xp_load(x, e0 / 4 + 4);
         const float s = x.scale[c];
         const float t = x.sum16[2 * c] + x.sum16[2 * c + 1];
 #pragma unroll
@@ -476,8 +498,10 @@ struct Q50 {
                 hi[i] = ((qd >> 4) & 0x0f0f0f0fu) | (spread_hi << 4);
             }
             // elements 0..15 are the low nibbles, 16..31 the high nibbles
-            const float v = dot16(xl0, xh0, lo[0], lo[1], lo[2], lo[3]) + dot16(xl1, xh1, hi[0], hi[1], hi[2], hi[3]);
-            acc[r] = fmaf(d, fmaf(s, v, -16.f * t), acc[r]);
+            LimbSum ls = limb_zero();
+            limb_acc(ls, x0, lo[0], lo[1], lo[2], lo[3]);
+            limb_acc(ls, x1, hi[0], hi[1], hi[2], hi[3]);
+            acc[r] = fmaf(d, fmaf(s, limb_total(ls), -16.f * t), acc[r]);
         }
     }
 };
@@ -562,17 +586,16 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // scale / sum16 entries are stored by every lane of their sub-block / quad
 // (the same value to the same address).
 //
-// X = rint(x / s) with s = max|x| / 32512 fits 16 bits.  v_cvt_pknorm_i16_f32
-// converts two values at once (rint(clamp(v, -1, 1) * 32767) into the two
-// halves of a dword), so x is prescaled by 32512 / (32767 max|x|).  With
-// Y = X + 128 (a packed 16-bit add) the signed limbs of X = 256 hi + lo are
-// hi = byte 1 of Y and lo = byte 0 of Y xor 0x80, gathered by byte permutes;
-// the sub-block sums of X come from v_dot2 with (1, 1), exact in int32.
+// X = rint(x / s) with s = max|x| / kXMax fits 24 bits.  With
+// Y = X + 0x8080 the signed limbs of X = 65536 hi + 256 mid + lo are
+// lo = byte 0 of Y xor 0x80, mid = byte 1 of Y xor 0x80 and hi = byte 2 of Y,
+// gathered four elements to a dword by byte permutes; the sub-block sums of
+// X are exact in int32 (16 values below 2^23 each).
 template <int NB>
 __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, int k, uint32_t* smem) {
     // |x| as integers: for non-negative floats the integer order is the
     // float order, and v_max_u32 takes a DPP operand directly; a NaN among
-    // the bit patterns is the largest, so its sub-block is staged as zero
+    // the bit patterns is the largest, so its sub-block's scale becomes NaN
     uint32_t mb[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u)
@@ -585,22 +608,24 @@ __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, in
 #pragma unroll
     for (int u = 0; u < NB; ++u) mb[u] = max(mb[u], (uint32_t)dpp_i<0x141>((int)mb[u]));  // the other quad of the 8
     float sc[NB];
-    short2v x01[NB], x23[NB];
+    int X[NB][4];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-        // sub-blocks below 1e-30 in magnitude are staged as zero
+        // sub-blocks below 1e-30 in magnitude are staged as zero; a NaN
+        // maximum stays the scale (an infinite one gives inf * 0 = NaN)
         const float m = __uint_as_float(mb[u]);
         const bool live = m > 1e-30f;
-        sc[u] = live ? m * (1.0f / 32512.0f) : 0.f;
-        const float is = live ? __builtin_amdgcn_rcpf(m) * (32512.0f / 32767.0f) : 0.f;
-        x01[u] = __builtin_amdgcn_cvt_pknorm_i16(v[u].x * is, v[u].y * is);
-        x23[u] = __builtin_amdgcn_cvt_pknorm_i16(v[u].z * is, v[u].w * is);
+        sc[u] = live ? m * (1.0f / kXMax) : (m == m ? 0.f : m);
+        const float is = live ? __builtin_amdgcn_rcpf(m) * kXMax : 0.f;
+        X[u][0] = __float2int_rn(v[u].x * is);
+        X[u][1] = __float2int_rn(v[u].y * is);
+        X[u][2] = __float2int_rn(v[u].z * is);
+        X[u][3] = __float2int_rn(v[u].w * is);
     }
     // sums of the 16 X of each quad (every lane of the quad holds its sum)
     int t[NB];
 #pragma unroll
-    for (int u = 0; u < NB; ++u)
-        t[u] = __builtin_amdgcn_sdot2(x23[u], (short2v){1, 1}, __builtin_amdgcn_sdot2(x01[u], (short2v){1, 1}, 0, false), false);
+    for (int u = 0; u < NB; ++u) t[u] = (X[u][0] + X[u][1]) + (X[u][2] + X[u][3]);
 #pragma unroll
     for (int u = 0; u < NB; ++u) t[u] += dpp_i<0xb1>(t[u]);
 #pragma unroll
@@ -609,22 +634,28 @@ __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, in
     // and 64 u sums further, so one address per array serves every unit
     const int cap = xq_cap(k), n = limb_dwords(cap);
     uint32_t* lo = smem + limb(e0 >> 2);
-    uint32_t* hi = lo + n;
-    uint32_t* scale = smem + 2 * n + (e0 >> 5);
-    uint32_t* sum16 = smem + 2 * n + cap / 32 + (e0 >> 4);
+    uint32_t* mid = lo + n;
+    uint32_t* hi = lo + 2 * n;
+    uint32_t* scale = smem + 3 * n + (e0 >> 5);
+    uint32_t* sum16 = smem + 3 * n + cap / 32 + (e0 >> 4);
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
         if (u > 0 && 1024 * u >= cap) break;  // (uniform) passes beyond the arrays
-        const uint32_t y01 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x01[u]) + (ushort2v){128, 128});
-        const uint32_t y23 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(ushort2v, x23[u]) + (ushort2v){128, 128});
-        lo[320 * u] = __builtin_amdgcn_perm(y23, y01, 0x06040200u) ^ 0x80808080u;
-        hi[320 * u] = __builtin_amdgcn_perm(y23, y01, 0x07050301u);
+        const uint32_t y0 = (uint32_t)X[u][0] + 0x8080u, y1 = (uint32_t)X[u][1] + 0x8080u;
+        const uint32_t y2 = (uint32_t)X[u][2] + 0x8080u, y3 = (uint32_t)X[u][3] + 0x8080u;
+        const uint32_t a01 = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // y0.b0 y0.b1 y1.b0 y1.b1
+        const uint32_t a23 = __builtin_amdgcn_perm(y3, y2, 0x05040100u);
+        lo[320 * u] = __builtin_amdgcn_perm(a23, a01, 0x06040200u) ^ 0x80808080u;
+        mid[320 * u] = __builtin_amdgcn_perm(a23, a01, 0x07050301u) ^ 0x80808080u;
+        const uint32_t h01 = __builtin_amdgcn_perm(y1, y0, 0x06020602u);  // y0.b2 y1.b2 (twice)
+        const uint32_t h23 = __builtin_amdgcn_perm(y3, y2, 0x06020602u);
+        hi[320 * u] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
         scale[32 * u] = __float_as_uint(sc[u]);
         sum16[64 * u] = __float_as_uint(sc[u] * (float)t[u]);
     }
 }
 
-// Stage x as 16-bit block fixed point (see the file comment).  Thread t
+// Stage x as 24-bit block fixed point (see the file comment).  Thread t
 // handles elements 4t + 1024u (u < NB, NB * 1024 >= k); all of its x (and
 // norm weight) loads are issued before any arithmetic, so staging costs one
 // memory latency.  With a norm weight x is first replaced by the reference

@@ -89,12 +89,12 @@ int add_int_launch(int* p, int v, hipStream_t st);
 // (part_floats floats, may be null) lets narrow shapes split K
 int gemm_bf16_run(int type, const uint16_t* a, const uint16_t* a_lo, int lda, const void* w, float* out, int ldo,
                   const float* res, int m, int n, int k, int form, float* part, size_t part_floats, hipStream_t st);
-// Q4_K prefill GEMM with exact weights on the fp16 matrix cores
+// Prefill GEMM with exact Q4_K / Q5_K / Q8_0 / Q5_0 weights on the fp16 matrix cores
 // (mxh_prefill_q4k.hip): a as fp16 hi / lo of a * 2^e per row, s the split
 // sums of every 32-element sub-block of those values (row stride lds),
 // rscale = 2^-e per row; inputs from rows_to_f16 / silu_mul_f16
-bool gemm_q4k_f16_supported(int type, int k);
-int gemm_q4k_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+bool gemm_q_f16_supported(int type, int k);
+int gemm_q_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
                      const uint16_t* s_lo, int lds, const float* rscale, const void* w, float* out, int ldo,
                      const float* res, int m, int n, int k, int form, float* part, size_t part_floats, hipStream_t st);
 int rows_to_f16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a_hi, uint16_t* a_lo,

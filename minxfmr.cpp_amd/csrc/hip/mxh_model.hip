@@ -590,15 +590,16 @@ int ensure_prefill_buffers(mxh_model* m) {
 }
 
 // Which input form a prefill GEMM reads: the exact-weight fp16 kernel for
-// Q4_K rows (pf_h16 / pf_l16 / pf_sh / pf_sl / pf_rscale), the split-bf16
-// kernel otherwise (pf_a, pf_a_lo).
+// Q4_K, Q5_K, Q8_0 and Q5_0 rows (pf_h16 / pf_l16 / pf_sh / pf_sl /
+// pf_rscale), the split-bf16 kernel otherwise (F32 rows, rows whose length
+// is not a multiple of 256, or MXH_MODEL_BF16_PREFILL; pf_a, pf_a_lo).
 bool f16_gemm(const mxh_model* m, const DevW& w) {
-    return w.p && !m->bf16_prefill && gemm_q4k_f16_supported(w.type, (int)w.cols);
+    return w.p && !m->bf16_prefill && gemm_q_f16_supported(w.type, (int)w.cols);
 }
 
 int gemm(mxh_model* m, const DevW& w, int lda, float* out, int ldo, const float* res, int rows, hipStream_t st) {
     if (f16_gemm(m, w))
-        return gemm_q4k_f16_run(w.type, m->pf_h16, m->pf_l16, lda, m->pf_sh, m->pf_sl, lda / 32, m->pf_rscale, w.p,
+        return gemm_q_f16_run(w.type, m->pf_h16, m->pf_l16, lda, m->pf_sh, m->pf_sl, lda / 32, m->pf_rscale, w.p,
                                 out, ldo, res, rows, (int)w.rows, (int)w.cols, m->form, m->pf_part,
                                 m->pf_part_floats, st);
     return gemm_bf16_run(w.type, m->pf_a, m->pf_a_lo, lda, w.p, out, ldo, res, rows, (int)w.rows, (int)w.cols,

@@ -1,21 +1,24 @@
-// mxh_prefill_q4k.hip — the prefill GEMM for Q4_K weights on the fp16 matrix
-// cores, with every weight exact.
+// mxh_prefill_q4k.hip — the prefill GEMM for quantized weights on the fp16
+// matrix cores, with every weight exact.
 //
-// out[m][n] = sum_k a[m][k] w[n][k] over Q4_K rows w = d sc_j q - dmin m_j
-// (tensor.cpp:405-432; sub-block j of 32 elements inside a 256-element
-// super-block with one d, dmin) regrouped as
+// out[m][n] = sum_k a[m][k] w[n][k].  K-quant rows (Q4_K, Q5_K:
+// w = d sc_j q - dmin m_j, tensor.cpp:405-432; sub-block j of 32 elements
+// inside a 256-element super-block with one d, dmin) are regrouped as
 //
 //   sum_b d_b[n] . sum_{k in b} a[m][k] (sc_j q_k)          main MFMAs
 //   - sum_j dmin[n] m_j . S_j[m],   S_j = sum_{k in j} a[m][k]   correction MFMAs
 //
-// sc_j q_k is an integer below 1024, exact in fp16, so no weight is rounded:
+// sc_j q_k is an integer below 2048, exact in fp16, so no weight is rounded:
 // the tile holds those integers, d is applied once per super-block to a
 // per-block accumulator, and the min terms are a small second contraction
-// over sub-blocks (16 at a time).  Activations come as a' = a 2^e (e per
-// row, so max |a'| lies in [128, 256)) split into fp16 hi + lo (about 22
-// significant bits), with the sub-block sums S of the same values split the
-// same way (rows_to_f16 / silu_mul_f16 below); the output is scaled back by
-// 2^-e.  Reference op: backend_matmul_rhs_transposed with m > 1
+// over sub-blocks (16 at a time).  Rows of 32-element blocks (Q8_0: w = d q,
+// Q5_0: w = d (q - 16); tensor.cpp:434-457) hold the integers q (q - 16) in
+// the tile and apply d once per block; they need no correction.
+// Activations come as a' = a 2^e (e per row, so max |a'| lies in
+// [128, 256)) split into fp16 hi + lo (about 22 significant bits), with the
+// sub-block sums S of the same values split the same way (rows_to_f16 /
+// silu_mul_f16 below); the output is scaled back by 2^-e.  Reference op:
+// backend_matmul_rhs_transposed with m > 1
 // (src/backend/backend_runtime.cpp:302-319).
 //
 // Tiles: 128 x TN outputs per workgroup of 2 TN / 64 waves (TN = 128 or
@@ -43,7 +46,7 @@ constexpr int kRing = 16;       // sub-blocks per correction round
 constexpr int kRLd = kRing + 8; // ring row stride in fp16 (48 bytes)
 template <int TN>
 constexpr size_t q4_lds_bytes() {
-    return (size_t)((2 * kQM + TN) * kQLd + 2 * (kQM + TN) * kRLd) * 2 + TN * sizeof(float);
+    return (size_t)((2 * kQM + TN) * kQLd + 2 * (kQM + TN) * kRLd) * 2 + 2 * TN * sizeof(float);
 }
 
 __device__ __forceinline__ uint16_t f16_bits(float v) { return __half_as_ushort(__float2half_rn(v)); }
@@ -54,37 +57,192 @@ __device__ __forceinline__ uint32_t split_f16(float v) {
     return (uint32_t)__half_as_ushort(h) | ((uint32_t)f16_bits(v - __half2float(h)) << 16);
 }
 
-// the three 16-byte pieces of 64-element chunk k0 / 64 of a Q4_K row
-template <bool TILED>
-struct Q4Chunk {
-    uint4 hd, qa, qb;
-    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0) {
-        const uint8_t* rp = w + (size_t)row * rb;
-        if constexpr (TILED) {
-            const Q4KTileOffs o = q4k_tile_offsets(k0 >> 6, (int64_t)(rb / 144));
-            hd = *reinterpret_cast<const uint4*>(rp + o.hd);
-            qa = *reinterpret_cast<const uint4*>(rp + o.qa);
-            qb = *reinterpret_cast<const uint4*>(rp + o.qb);
-        } else {
-            const uint8_t* blk = rp + (size_t)(k0 >> 8) * 144;
-            const int g = (k0 & 255) >> 6;
-            hd = *reinterpret_cast<const uint4*>(blk);
-            qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g);
-            qb = *reinterpret_cast<const uint4*>(blk + 32 + 32 * g);
-        }
-    }
-};
-
 __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     // both are integers below 2048: round-toward-zero packing is exact
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
 }
 
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+// Weight formats.  Thread (row r, half h) of a K step at k0 fetches the
+// bytes of elements k0 + 32 h .. +31 of its row (fetch, a step ahead) and
+// decodes them (decode) into 16 dwords of fp16 integers, with
+//   K-quants:   o = sc_j q, d = the super-block's d, mt = -dmin m_j;
+//   32-blocks:  o = q (Q5_0: q - 16), d = the block's d.
+enum WFmt { WF_Q4K, WF_Q4KT, WF_Q5K, WF_Q5KT, WF_Q80, WF_Q80T, WF_Q50 };
+
+template <int F>
+struct WFormat;
+
+// Q4_K: the header and the 32 qs bytes of 64-group g = (k0 % 256) / 64
+template <bool TILED>
+struct WQ4K {
+    static constexpr bool kKQuant = true;
+    uint4 hd, qa, qb;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int) {
+        const uint8_t* rp = w + (size_t)row * rb;
+        if constexpr (TILED) {
+            const Q4KTileOffs o = q4k_tile_offsets(k0 >> 6, (int64_t)(rb / 144));
+            hd = ld16(rp + o.hd);
+            qa = ld16(rp + o.qa);
+            qb = ld16(rp + o.qb);
+        } else {
+            const uint8_t* blk = rp + (size_t)(k0 >> 8) * 144;
+            const int g = (k0 & 255) >> 6;
+            hd = ld16(blk);
+            qa = ld16(blk + 16 + 32 * g);
+            qb = ld16(blk + 32 + 32 * g);
+        }
+    }
+    // sub-block j = 2 g + h (tensor.cpp:395-432 with the scale form `form`);
+    // byte i of the group's 32 qs holds element i (low nibble) and 32 + i
+    // (high nibble)
+    __device__ __forceinline__ void decode(int k0, int h, int form, uint32_t (&o)[16], float& d, float& mt) const {
+        const int j = 2 * ((k0 & 255) >> 6) + h;
+        uint32_t sc, mn;
+        k4_scale_min(hd.y, hd.z, hd.w, j, form, sc, mn);
+        const float scf = (float)sc;
+        const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t nb = (qv[i] >> (4 * h)) & 0x0f0f0f0fu;
+            o[2 * i] = pk_f16((float)(nb & 0xffu) * scf, (float)((nb >> 8) & 0xffu) * scf);
+            o[2 * i + 1] = pk_f16((float)((nb >> 16) & 0xffu) * scf, (float)(nb >> 24) * scf);
+        }
+        d = half_bits_to_float(hd.x & 0xffffu);
+        mt = -(half_bits_to_float(hd.x >> 16) * (float)mn);
+    }
+};
+template <> struct WFormat<WF_Q4K> : WQ4K<false> {};
+template <> struct WFormat<WF_Q4KT> : WQ4K<true> {};
+
+// Q5_K (published ggml layout): the header, the 32 qh bytes (the fifth bit
+// of element 64 g + 32 h + i is bit 2 g + h of qh[i]) and the group's 32 qs
+template <bool TILED>
+struct WQ5K {
+    static constexpr bool kKQuant = true;
+    uint4 hd, h0, h1, qa, qb;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int) {
+        const uint8_t* rp = w + (size_t)row * rb;
+        const int g = (k0 & 255) >> 6;
+        if constexpr (TILED) {
+            // chunks 2 g and 2 g + 1 of the block: adjacent 16-byte qs pieces
+            const Q5KTileOffs o = q5k_tile_offsets(8 * (int64_t)(k0 >> 8) + 2 * g, (int64_t)(rb / 176));
+            hd = ld16(rp + o.hd);
+            h0 = ld16(rp + o.qh);
+            h1 = ld16(rp + o.qh + 16);
+            qa = ld16(rp + o.qs);
+            qb = ld16(rp + o.qs + 16);
+        } else {
+            const uint8_t* blk = rp + (size_t)(k0 >> 8) * 176;
+            hd = ld16(blk);
+            h0 = ld16(blk + 16);
+            h1 = ld16(blk + 32);
+            qa = ld16(blk + 48 + 32 * g);
+            qb = ld16(blk + 64 + 32 * g);
+        }
+    }
+    __device__ __forceinline__ void decode(int k0, int h, int form, uint32_t (&o)[16], float& d, float& mt) const {
+        const int j = 2 * ((k0 & 255) >> 6) + h;
+        uint32_t sc, mn;
+        k4_scale_min(hd.y, hd.z, hd.w, j, form, sc, mn);
+        const float scf = (float)sc;
+        const uint32_t qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const uint32_t hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t nb = ((qv[i] >> (4 * h)) & 0x0f0f0f0fu) | (((hv[i] >> j) & 0x01010101u) << 4);
+            o[2 * i] = pk_f16((float)(nb & 0xffu) * scf, (float)((nb >> 8) & 0xffu) * scf);
+            o[2 * i + 1] = pk_f16((float)((nb >> 16) & 0xffu) * scf, (float)(nb >> 24) * scf);
+        }
+        d = half_bits_to_float(hd.x & 0xffffu);
+        mt = -(half_bits_to_float(hd.x >> 16) * (float)mn);
+    }
+};
+template <> struct WFormat<WF_Q5K> : WQ5K<false> {};
+template <> struct WFormat<WF_Q5KT> : WQ5K<true> {};
+
+// four signed bytes as two dwords of fp16 integers
+__device__ __forceinline__ void sbytes_f16(uint32_t v, uint32_t& lo, uint32_t& hi) {
+    lo = pk_f16((float)(int)(int8_t)(v & 0xffu), (float)(int)(int8_t)((v >> 8) & 0xffu));
+    hi = pk_f16((float)(int)(int8_t)((v >> 16) & 0xffu), (float)(int)(int8_t)(v >> 24));
+}
+
+// Q8_0: block (k0 / 32 + h) of the row; the tiled layout keeps its 32 quant
+// bytes as two aligned 16-byte pieces, the GGUF one as 2-aligned blocks of 34
+template <bool TILED>
+struct WQ80 {
+    static constexpr bool kKQuant = false;
+    uint32_t q[8];
+    uint32_t dh;
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int h) {
+        const uint8_t* rp = w + (size_t)row * rb;
+        const int64_t c = (k0 >> 5) + h;
+        if constexpr (TILED) {
+            const Q80TileOffs o = q80_tile_offsets(c, (int64_t)(rb / 34));
+            const uint4 lo = ld16(rp + o.lo), hi = ld16(rp + o.hi);
+            q[0] = lo.x; q[1] = lo.y; q[2] = lo.z; q[3] = lo.w;
+            q[4] = hi.x; q[5] = hi.y; q[6] = hi.z; q[7] = hi.w;
+            dh = ld_u16(rp + o.d);
+        } else {
+            const uint8_t* blk = rp + (size_t)c * 34;
+            dh = ld_u16(blk);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = ld_u16(blk + 2 + 4 * i) | (ld_u16(blk + 4 + 4 * i) << 16);
+        }
+    }
+    __device__ __forceinline__ void decode(int, int, int, uint32_t (&o)[16], float& d, float& mt) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sbytes_f16(q[i], o[2 * i], o[2 * i + 1]);
+        d = half_bits_to_float(dh);
+        mt = 0.f;
+    }
+};
+template <> struct WFormat<WF_Q80> : WQ80<false> {};
+template <> struct WFormat<WF_Q80T> : WQ80<true> {};
+
+// Q5_0 (tensor.cpp:434-449): d, a 32-bit high-bit mask, 16 qs bytes; element
+// i < 16 is the low nibble of qs[i] with bit i, element 16 + i the high
+// nibble with bit 16 + i, value d (q - 16)
+template <>
+struct WFormat<WF_Q50> {
+    static constexpr bool kKQuant = false;
+    uint32_t dh, qh, qs[4];
+    __device__ __forceinline__ void fetch(const uint8_t* __restrict__ w, size_t rb, int row, int k0, int h) {
+        const uint8_t* blk = w + (size_t)row * rb + (size_t)((k0 >> 5) + h) * 22;
+        dh = ld_u16(blk);
+        qh = ld_u16(blk + 2) | (ld_u16(blk + 4) << 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = ld_u16(blk + 6 + 4 * i) | (ld_u16(blk + 8 + 4 * i) << 16);
+    }
+    __device__ __forceinline__ void decode(int, int, int, uint32_t (&o)[16], float& d, float& mt) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v[8];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int e = 4 * i + b;
+                const uint32_t byte = (qs[i] >> (8 * b)) & 0xffu;
+                v[b] = (float)((int)((byte & 15u) | (((qh >> e) & 1u) << 4)) - 16);
+                v[4 + b] = (float)((int)((byte >> 4) | (((qh >> (e + 16)) & 1u) << 4)) - 16);
+            }
+            // elements 4i..4i+3 (low nibbles) and 16+4i.. (high nibbles)
+            o[2 * i] = pk_f16(v[0], v[1]);
+            o[2 * i + 1] = pk_f16(v[2], v[3]);
+            o[8 + 2 * i] = pk_f16(v[4], v[5]);
+            o[8 + 2 * i + 1] = pk_f16(v[6], v[7]);
+        }
+        d = half_bits_to_float(dh);
+        mt = 0.f;
+    }
+};
+
 // Split K: split z takes K steps [z * ksteps, (z + 1) * ksteps), a
 // multiple of 4 (whole super-blocks), and with more than one split writes
 // its scaled partial tile to part[z][m][n] for gemm_f16_reduce.
-template <bool TILED, int TN>
-__global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel(const uint16_t* __restrict__ a_hi,
+template <int F, int TN>
+__global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q_f16_kernel(const uint16_t* __restrict__ a_hi,
                                                            const uint16_t* __restrict__ a_lo, int lda,
                                                            const uint16_t* __restrict__ s_hi,
                                                            const uint16_t* __restrict__ s_lo, int lds,
@@ -104,7 +262,11 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
     uint16_t* Sl = Sh + kQM * kRLd;
     uint16_t* Bh = Sl + kQM * kRLd;   // [TN][kRLd] -dmin m_j per weight row, hi
     uint16_t* Bl = Bh + TN * kRLd;
-    float* dcol = reinterpret_cast<float*>(Bl + TN * kRLd);  // [TN] d of the current super-block
+    // [TN] d of the current super-block (K-quants), [2][TN] d of the step's
+    // two blocks (32-element blocks)
+    float* dcol = reinterpret_cast<float*>(Bl + TN * kRLd);
+    using WF = WFormat<F>;
+    constexpr bool KQ = WF::kKQuant;
 
     // Work item w = (split z, row tile y, column tile x), x fastest, and
     // workgroup ids dealt so that XCD q (ids q, q + 8, ...) takes the
@@ -119,7 +281,11 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
     const int wr = wave / WC, wc = wave % WC;
     const int m0 = ty * kQM, n0 = tx * TN;
     const int kb = tz * ksteps * kQK, ke = min(k, kb + ksteps * kQK);
-    const size_t rb = (size_t)(k / 256) * 144;
+    const size_t rb = row_bytes(F == WF_Q4K || F == WF_Q4KT   ? MXH_Q4_K
+                                : F == WF_Q5K || F == WF_Q5KT ? MXH_Q5_K
+                                : F == WF_Q50                 ? MXH_Q5_0
+                                                              : MXH_Q8_0,
+                                k);
     // staging roles: thread t owns weight row t / 2 of the tile and sub-block
     // half t % 2 of the step, and activation row ra = t / APT, elements
     // EPT aq .. of the step (aq = t % APT), with the sum of sub-block sa
@@ -146,8 +312,8 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
     const uint16_t* ps_l = s_lo + (size_t)arow_c * lds + sa;
     constexpr int AV = EPT / 8;  // 16-byte pieces per thread and limb
     uint4 ahv[AV], alv[AV];
-    uint32_t sh_g, sl_g;
-    Q4Chunk<TILED> wq;
+    uint32_t sh_g = 0, sl_g = 0;
+    WF wq;
 #define MXH_Q4F16_FETCH(K0)                                                   \
     do {                                                                     \
         const uint4* qh_ = reinterpret_cast<const uint4*>(pa_h + (K0));      \
@@ -156,9 +322,11 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
             ahv[v_] = qh_[v_];                                               \
             alv[v_] = ql_[v_];                                               \
         }                                                                    \
-        sh_g = ps_h[(K0) >> 5];                                              \
-        sl_g = ps_l[(K0) >> 5];                                              \
-        wq.fetch(w, rb, wrow, (K0));                                         \
+        if constexpr (KQ) {                                                  \
+            sh_g = ps_h[(K0) >> 5];                                          \
+            sl_g = ps_l[(K0) >> 5];                                          \
+        }                                                                    \
+        wq.fetch(w, rb, wrow, (K0), h);                                      \
     } while (0)
     MXH_Q4F16_FETCH(kb);
 
@@ -175,32 +343,25 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
                 dh[v] = msk(ahv[v]);
                 dl[v] = msk(alv[v]);
             }
-            if (s_owner) {
+            if (KQ && s_owner) {
                 Sh[ra * kRLd + 2 * (step & 7) + sa] = (uint16_t)(sh_g & am);
                 Sl[ra * kRLd + 2 * (step & 7) + sa] = (uint16_t)(sl_g & am);
             }
-            // weights of sub-block j = 2 g + h as the integers sc_j q (tensor.cpp:395-432
-            // with the scale form `form`); bytes i of the chunk's 32 qs hold element i
-            // (low nibble) and element 32 + i (high nibble)
-            const int j = 2 * ((k0 & 255) >> 6) + h;
-            uint32_t sc, mn;
-            k4_scale_min(wq.hd.y, wq.hd.z, wq.hd.w, j, form, sc, mn);
-            const float scf = (float)sc;
-            const uint32_t qv[8] = {wq.qa.x, wq.qa.y, wq.qa.z, wq.qa.w, wq.qb.x, wq.qb.y, wq.qb.z, wq.qb.w};
+            // this thread's 32 weights as fp16 integers, and their scales
             uint32_t o[16];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t nb = (qv[i] >> (4 * h)) & 0x0f0f0f0fu;
-                o[2 * i] = pk_f16((float)(nb & 0xffu) * scf, (float)((nb >> 8) & 0xffu) * scf);
-                o[2 * i + 1] = pk_f16((float)((nb >> 16) & 0xffu) * scf, (float)(nb >> 24) * scf);
-            }
+            float dq, mt;
+            wq.decode(k0, h, form, o, dq, mt);
             uint4* dw = reinterpret_cast<uint4*>(Ws + r * kQLd + 32 * h);
 #pragma unroll
             for (int q = 0; q < 4; ++q) dw[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
-            const uint32_t bsplit = split_f16(-(half_bits_to_float(wq.hd.x >> 16) * (float)mn));
-            Bh[r * kRLd + slot] = (uint16_t)bsplit;
-            Bl[r * kRLd + slot] = (uint16_t)(bsplit >> 16);
-            if (h == 0) dcol[r] = half_bits_to_float(wq.hd.x & 0xffffu);
+            if constexpr (KQ) {
+                const uint32_t bsplit = split_f16(mt);
+                Bh[r * kRLd + slot] = (uint16_t)bsplit;
+                Bl[r * kRLd + slot] = (uint16_t)(bsplit >> 16);
+                if (h == 0) dcol[r] = dq;
+            } else {
+                dcol[h * TN + r] = dq;
+            }
         }
         __syncthreads();
         if (k0 + kQK < ke) MXH_Q4F16_FETCH(k0 + kQK);
@@ -223,9 +384,23 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
                     P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], P[i][j], 0, 0, 0);
                     P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], P[i][j], 0, 0, 0);
                 }
+            if (!KQ && (ks & 31) == 16) {
+                // end of a 32-element block: acc += d[n] . P
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float dc = dcol[(ks >> 5) * TN + wc * 64 + j * 32 + lr];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            acc[i][j][e] = fmaf(dc, P[i][j][e], acc[i][j][e]);
+                            P[i][j][e] = 0.f;
+                        }
+                }
+            }
         }
         const bool last = k0 + kQK >= ke;
-        if (((k0 + kQK) & 255) == 0 || last) {
+        if (KQ && (((k0 + kQK) & 255) == 0 || last)) {
             // end of a super-block: acc += d[n] . P (each lane's accumulators share one column)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -239,7 +414,7 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q4k_f16_kernel
                     }
             }
         }
-        if ((step & 7) == 7 || last) {
+        if (KQ && ((step & 7) == 7 || last)) {
             // correction round over the sub-blocks staged since the last one;
             // ring slots past `used` hold older values and are zeroed here
             const int used = 2 * ((step & 7) + 1);
@@ -346,7 +521,7 @@ __device__ __forceinline__ void emit_subblock(const float* v, float scale, uint1
 
 // Rows of x (optionally the reference rmsnorm x / sqrt(mean(x^2) + eps) * w,
 // rmsnorm.cpp:5-26, sum of squares in double, the same float products as
-// rows_to_bf16) as GEMM input of gemm_q4k_f16.  One workgroup per row; k a
+// rows_to_bf16) as GEMM input of gemm_q_f16.  One workgroup per row; k a
 // multiple of 32 and at most 2 * 256 * 32.
 constexpr int kRowSub = 2;  // sub-blocks per thread
 __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float* __restrict__ x, int ldx,
@@ -409,7 +584,7 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float* __restric
     }
 }
 
-// h = silu(gate) * up (transformer.cpp:183-185) as gemm_q4k_f16 input; gu
+// h = silu(gate) * up (transformer.cpp:183-185) as gemm_q_f16 input; gu
 // rows are [gate | up], f a multiple of 32 and at most 2 * 256 * 32.
 __global__ __launch_bounds__(256) void silu_mul_f16_kernel(const float* __restrict__ gu, int f,
                                                            uint16_t* __restrict__ h_hi, uint16_t* __restrict__ h_lo,
@@ -455,15 +630,15 @@ __global__ __launch_bounds__(256) void silu_mul_f16_kernel(const float* __restri
 // TN = 128: 4 waves, two workgroups per CU; TN = 256: 8 waves, one per CU,
 // each activation tile staged once for twice the weight rows (half the
 // activation traffic per MFMA)
-template <bool TILED, int TN>
-int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+template <int F, int TN>
+int gemm_q_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
                         const uint16_t* s_lo, int lds, const float* rscale, const uint8_t* w, float* out, int ldo,
                         const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
                         hipStream_t st) {
     constexpr size_t lds_bytes = q4_lds_bytes<TN>();
     static bool attr_set = false;  // above 64 KiB of LDS needs the opt-in, once per kernel
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)gemm_q4k_f16_kernel<TILED, TN>,
+        if (hipFuncSetAttribute((const void*)gemm_q_f16_kernel<F, TN>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes) != hipSuccess)
             return MXH_ERR_HIP;
         attr_set = true;
@@ -478,7 +653,7 @@ int gemm_q4k_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, con
     // one dimension of workgroup ids, a multiple of 8 (the kernel's XCD mapping)
     const int items = tn * tm * splits;
     const dim3 grid((unsigned)((items + 7) / 8 * 8));
-    hipLaunchKernelGGL((gemm_q4k_f16_kernel<TILED, TN>), grid, dim3(2 * TN), lds_bytes, st, a_hi, a_lo, lda, s_hi,
+    hipLaunchKernelGGL((gemm_q_f16_kernel<F, TN>), grid, dim3(2 * TN), lds_bytes, st, a_hi, a_lo, lda, s_hi,
                        s_lo, lds, rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
     if (splits > 1)
         hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
@@ -497,28 +672,57 @@ static bool q4_wide_tiles(int m, int n) {
     return m > kQM && n >= 2048 && tiles <= 256;
 }
 
-bool gemm_q4k_f16_supported(int type, int k) {
-    return (type == MXH_Q4_K || type == MXH_Q4_K_TILED) && k % 256 == 0 && k <= kRowSub * 256 * 32;
+static int f16_format(int type) {
+    switch (type) {
+    case MXH_Q4_K: return WF_Q4K;
+    case MXH_Q4_K_TILED: return WF_Q4KT;
+    case MXH_Q5_K: return WF_Q5K;
+    case MXH_Q5_K_TILED: return WF_Q5KT;
+    case MXH_Q8_0: return WF_Q80;
+    case MXH_Q8_0_TILED: return WF_Q80T;
+    case MXH_Q5_0: return WF_Q50;
+    }
+    return -1;
 }
 
-int gemm_q4k_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+bool gemm_q_f16_supported(int type, int k) {
+    return f16_format(type) >= 0 && k % 256 == 0 && k <= kRowSub * 256 * 32;
+}
+
+template <int TN>
+static int gemm_q_f16_dispatch(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+                               const uint16_t* s_lo, int lds, const float* rscale, const uint8_t* wb, float* out,
+                               int ldo, const float* res, int m, int n, int k, int form, float* part,
+                               size_t part_floats, hipStream_t st) {
+#define MXH_QF16_CASE(F)                                                                                         \
+    case F:                                                                                                      \
+        return gemm_q_f16_launch<F, TN>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form, \
+                                        part, part_floats, st);
+    switch (f16_format(type)) {
+        MXH_QF16_CASE(WF_Q4K)
+        MXH_QF16_CASE(WF_Q4KT)
+        MXH_QF16_CASE(WF_Q5K)
+        MXH_QF16_CASE(WF_Q5KT)
+        MXH_QF16_CASE(WF_Q80)
+        MXH_QF16_CASE(WF_Q80T)
+        MXH_QF16_CASE(WF_Q50)
+    }
+#undef MXH_QF16_CASE
+    return MXH_ERR_UNSUPPORTED;
+}
+
+int gemm_q_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
                      const uint16_t* s_lo, int lds, const float* rscale, const void* w, float* out, int ldo,
                      const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
                      hipStream_t st) {
-    if (m <= 0 || n <= 0 || !gemm_q4k_f16_supported(type, k) || lda < k || lds < k / 32 || ldo < n) return MXH_ERR_ARG;
+    if (m <= 0 || n <= 0 || !gemm_q_f16_supported(type, k) || lda < k || lds < k / 32 || ldo < n) return MXH_ERR_ARG;
     if (!part) part_floats = 0;
     const uint8_t* wb = (const uint8_t*)w;
     if (q4_wide_tiles(m, n))
-        return type == MXH_Q4_K_TILED
-                   ? gemm_q4k_f16_launch<true, 256>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n,
-                                                    k, form, part, part_floats, st)
-                   : gemm_q4k_f16_launch<false, 256>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m,
-                                                     n, k, form, part, part_floats, st);
-    return type == MXH_Q4_K_TILED
-               ? gemm_q4k_f16_launch<true, 128>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
-                                                form, part, part_floats, st)
-               : gemm_q4k_f16_launch<false, 128>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
-                                                 form, part, part_floats, st);
+        return gemm_q_f16_dispatch<256>(type, a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
+                                        form, part, part_floats, st);
+    return gemm_q_f16_dispatch<128>(type, a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
+                                    part, part_floats, st);
 }
 
 int rows_to_f16_launch(const float* x, int ldx, const float* nw, float eps, int k, uint16_t* a_hi, uint16_t* a_lo,

@@ -73,6 +73,7 @@ def _load() -> C.CDLL:
         "mxh_memset": (ip, [vp, ip, sz]),
         "mxh_copy": (ip, [vp, vp, sz]),
         "mxh_gemm_q_bf16": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
+        "mxh_gemm_q_f16": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
         "mxh_attention_prefill": (ip, [vp, vp, vp, vp, ip, ip, ip, ip, ip]),
         "mxh_tile_rows": (ip, [ip, vp, i64, i64, C.POINTER(C.c_int)]),
         "mxh_timer_begin": (ip, []),
@@ -113,7 +114,7 @@ def _load() -> C.CDLL:
 lib = _load()
 EXPORTED = (
     "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
-    "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_attention_prefill mxh_tile_rows mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
+    "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_gemm_q_f16 mxh_attention_prefill mxh_tile_rows mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matmul_q mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_sample mxh_model_generate mxh_model_close "
@@ -197,6 +198,12 @@ def gemm_bf16(type_: int, a: DeviceBuffer, m: int, w: DeviceBuffer, n: int, k: i
               form: int = FORM_REF) -> None:
     """out[m x n] = bf16(a) . bf16(dequant(w))^T on the matrix cores."""
     check(lib.mxh_gemm_q_bf16(type_, a.ptr, m, w.ptr, n, k, out.ptr, form), "mxh_gemm_q_bf16")
+
+
+def gemm_f16(type_: int, a: DeviceBuffer, m: int, w: DeviceBuffer, n: int, k: int, out: DeviceBuffer,
+             form: int = FORM_REF) -> None:
+    """out[m x n] = a . dequant(w)^T on the fp16 matrix cores with exact weight codes."""
+    check(lib.mxh_gemm_q_f16(type_, a.ptr, m, w.ptr, n, k, out.ptr, form), "mxh_gemm_q_f16")
 
 
 def tile_rows(type_: int, w: DeviceBuffer, rows: int, cols: int) -> int:

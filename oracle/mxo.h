@@ -12,17 +12,24 @@
  * reference has no counterpart (Q5_K, Qwen3 QK-norm, seeded sampling) the
  * comment says so and names the published algorithm followed instead.
  *
- * Pins (tests/test_oracle_pins.py, tests/test_oracle_layer.py): fp16 decode,
- * Q4_K/Q8_0/Q5_0 dequant, matmul_rhs_t, rmsnorm, rope, softmax and the layer
- * stack are checked against the reference's own KATs, vectors from the
- * reference source compiled under oracle/_ref, closed forms and brute force.
- * Not pinned against the reference:
- *   - mxo_dequant_q5k_block: parity unpinned (no reference Q5_K); checked by
- *     its exact reduction to Q4_K with a zero high-bit plane and round trips;
- *   - QK-norm placement in the model step: parity unpinned (Qwen3 order:
- *     after the q/k projections, before RoPE; the norm itself is pinned);
- *   - mxo_sample's random draw: parity unpinned (the reference draws from an
- *     unseeded mt19937); the greedy limit and determinism are checked.
+ * Pins (tests/test_oracle_pins.py, tests/test_oracle_layer.py,
+ * tests/test_oracle_qknorm.py): fp16 decode, Q4_K/Q8_0/Q5_0 dequant,
+ * matmul_rhs_t, rmsnorm, rope, softmax and the layer stack are checked
+ * against the reference's own KATs, vectors from the reference source
+ * compiled under oracle/_ref, closed forms and brute force.  Where the
+ * reference has no code:
+ *   - mxo_dequant_q5k_block (no reference Q5_K): pinned to the published
+ *     ggml layout by its exact reduction to Q4_K with a zero high-bit plane,
+ *     the position of each high bit, and quantizer round trips;
+ *   - QK-norm placement in the model step (Qwen3 order: after the q/k
+ *     projections, before RoPE): pinned by a float64 numpy forward of a tiny
+ *     Qwen3 model written from that definition (1e-5), which the other
+ *     placements miss by 1e-2;
+ *   - mxo_sample's top-k / temperature / top-p / min-p cuts: pinned by
+ *     closed-form cases whose kept set and probabilities are known (draws
+ *     stay in the set, 20k-draw frequencies match).  The random draw itself
+ *     replaces the reference's unseeded mt19937, so which id a given seed
+ *     picks has no reference counterpart (parity unpinned for the draw).
  */
 #ifndef MXO_H
 #define MXO_H

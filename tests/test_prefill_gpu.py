@@ -4,9 +4,15 @@ The single-product GEMM entry (mxh_gemm_q_bf16) takes bf16 inputs: A rounded to 
 exactly (the bit-exact decoder) and then rounded to bf16, products summed in
 fp32.  Its reference here is the float64 product of exactly those bf16
 values, so the only admitted difference is fp32 summation:
-|err| <= 1e-5 * sum_k |a_k w_k| per output.  The model's prefill uses the
-split form (each operand as bf16 hi + lo, three products), checked through
-the model against the token-by-token oracle.
+|err| <= 1e-5 * sum_k |a_k w_k| per output.
+
+The exact-weight entry (mxh_gemm_q_f16, the model's prefill GEMM for
+quantized rows) multiplies the weights' integer codes exactly and carries A
+as fp16 hi + lo of a 2^e (about 22 significant bits); its reference is the
+float64 product of the unrounded a with the exactly dequantized weights,
+within 2^-19 * sum_k |a_k w_k| (22-bit inputs and fp32 sums), far below a
+bf16-rounded weight's 2^-9.  The model's prefill is also checked end to end
+against the token-by-token oracle.
 """
 from __future__ import annotations
 
@@ -58,6 +64,47 @@ def test_gemm_bf16_vs_rounded_reference(mxh, name, m, n, k):
         b.close()
 
 
+F16_CASES = [
+    ("Q4_K", 1, 256, 256), ("Q4_K", 128, 128, 256), ("Q4_K", 300, 520, 512), ("Q4_K", 512, 1024, 4096),
+    ("Q5_K", 77, 384, 512), ("Q5_K", 200, 640, 1024), ("Q8_0", 130, 200, 256), ("Q8_0", 257, 300, 1024),
+    ("Q5_0", 64, 96, 256), ("Q5_0", 9, 130, 512),
+]
+
+
+@pytest.mark.parametrize("name,m,n,k", F16_CASES, ids=[f"{a}-{b}x{c}x{d}" for a, b, c, d in F16_CASES])
+@pytest.mark.parametrize("tiled", [False, True], ids=["gguf", "tiled"])
+def test_gemm_f16_exact_weights(mxh, name, m, n, k, tiled):
+    t = TYPES[name]
+    rng = np.random.default_rng(m * 5 + n * 11 + k)
+    w = mxo.quantize(t, rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02))
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    a[:, 5] *= 1e-3  # small and large elements in one row
+    forms = (mxo.FORM_REF, mxo.FORM_GGML) if t in (mxo.Q4_K, mxo.Q5_K) else (mxo.FORM_REF,)
+    dw = mxhip.DeviceBuffer.from_array(w)
+    tt = mxhip.tile_rows(t, dw, n, k) if tiled else t
+    da = mxhip.DeviceBuffer.from_array(a)
+    out = mxhip.DeviceBuffer(4 * m * n)
+    for form in forms:
+        wd = mxo.dequant(t, w, n, k, form).astype(np.float64)
+        want = a.astype(np.float64) @ wd.T
+        bound = 2.0 ** -19 * (np.abs(a).astype(np.float64) @ np.abs(wd).T) + 1e-30
+        mxhip.gemm_f16(tt, da, m, dw, n, k, out, form)
+        got = out.download(np.float32, m * n).reshape(m, n).astype(np.float64)
+        err = np.abs(got - want)
+        assert np.all(err <= bound), f"form {form}: worst {float((err / bound).max()):.3g} x bound"
+    for b in (dw, da, out):
+        b.close()
+
+
+def test_gemm_f16_rejects_bad_shapes(mxh):
+    dw = mxhip.DeviceBuffer(1 << 16)
+    da = mxhip.DeviceBuffer(1 << 16)
+    with pytest.raises(mxhip.MxhError, match="bad shape"):
+        mxhip.gemm_f16(mxo.Q8_0, da, 1, dw, 1, 96, da)  # k not a multiple of 256
+    with pytest.raises(mxhip.MxhError, match="bad shape"):
+        mxhip.gemm_f16(mxo.F32, da, 1, dw, 1, 256, da)  # no integer codes
+
+
 def test_gemm_bf16_rejects_bad_shapes(mxh):
     dw = mxhip.DeviceBuffer(4096)
     da = mxhip.DeviceBuffer(4096)
@@ -79,8 +126,8 @@ def test_batched_prefill_then_step(mxh, tmp_path, name, n_ctx, n_prompt, flags):
     """Prompt fed through the matrix-core prefill (one chunk of 70, or 512 +
     18), then one decode step: its per-layer hidden states and logits are
     within the parity bar of the oracle run token by token (fp16 cache).
-    Default: Q4_K projections on the exact-weight fp16 GEMM, the rest split
-    bf16; MODEL_BF16_PREFILL: every projection split bf16."""
+    Default: quantized projections on the exact-weight fp16 GEMM, F32 ones
+    split bf16; MODEL_BF16_PREFILL: every projection split bf16."""
     prefill_vs_oracle(tmp_path, name, n_ctx, n_prompt, flags)
 
 
