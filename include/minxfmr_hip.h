@@ -139,6 +139,19 @@ int mxh_gemm_q_bf16(int type, const float *a, int64_t m, const void *w, int64_t 
  * (src/backend/backend_runtime.cpp:302-319). */
 int mxh_gemm_q_f16(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out, int form);
 
+/* mxh_gemm_q_f16 without any allocation: the staged activations live in a
+ * device scratch array of 12 MiB that every GPU the library runs on holds
+ * from load until the process ends, so 4 m k + m k / 8 + 4 m bytes (about
+ * 4.1 bytes per element of a) must fit in it; larger requests are rejected
+ * with MXH_ERR_ARG and a message.  Calls no hipMalloc / hipFree; results are
+ * identical to mxh_gemm_q_f16's.  Every call on a GPU reuses that GPU's
+ * scratch, so calls that overlap on one GPU (from several host threads, or
+ * with work the caller enqueues on other streams) race.  No counterpart in
+ * the reference: for callers that cannot allocate (code under HIP graph
+ * capture, serving loops that forbid allocation). */
+int mxh_gemm_q_f16_noalloc(int type, const float *a, int64_t m, const void *w, int64_t n, int64_t k, float *out,
+                           int form);
+
 /* Causal attention of m consecutive prompt tokens at positions p0 .. p0+m-1
  * (transformer.cpp:529-629, per token: softmax of q.k / sqrt(hd) over cache
  * positions 0 .. pos, then the weighted sum of V rows), on the fp16 matrix

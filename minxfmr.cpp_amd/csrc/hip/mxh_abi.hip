@@ -34,9 +34,62 @@ struct Context {
 Context g_ctx;
 thread_local std::string g_err;
 
+// Device scratch of mxh_gemm_q_f16_noalloc: the staged activations (fp16 hi
+// and lo of a 2^e, the split sub-block sums, 2^-e per row).  Each GPU holds
+// its own copy from module load until the process ends; in host code the
+// array's name is only a stand-in, so kernels get the device address that
+// hipGetSymbolAddress returned for the current device (g_scratch_ptr).
+constexpr size_t kNoallocScratchBytes = 12u << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// staging bytes of an m x k activation block in the layout of f16_rows_layout
+size_t f16_rows_bytes(size_t m, size_t k) { return 4 * m * k + 4 * (m * k / 32) + 4 * m; }
+
+struct F16Rows {
+    uint16_t *a_hi, *a_lo, *s_hi, *s_lo;
+    float* rscale;
+};
+F16Rows f16_rows_layout(void* buf, size_t m, size_t k) {
+    const size_t mk = m * k, nsb = mk / 32;
+    F16Rows r;
+    r.a_hi = static_cast<uint16_t*>(buf);
+    r.a_lo = r.a_hi + mk;
+    r.s_hi = r.a_lo + mk;
+    r.s_lo = r.s_hi + nsb;
+    r.rscale = reinterpret_cast<float*>(r.s_lo + nsb);
+    return r;
+}
+
 int ensure_ready() {
     if (g_ctx.ready) return MXH_OK;
     return mxh_init(0);
+}
+
+// validation and the two launches of mxh_gemm_q_f16 over staging at `buf`
+int gemm_q_f16_body(const char* who, int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k,
+                    float* out, int form, void* buf) {
+    const F16Rows r = f16_rows_layout(buf, (size_t)m, (size_t)k);
+    if (int rc = rows_to_f16_launch(a, (int)k, nullptr, 0.f, (int)k, r.a_hi, r.a_lo, (int)k, r.s_hi, r.s_lo,
+                                    (int)k / 32, r.rscale, (int)m, g_ctx.stream))
+        return set_error(rc, "%s: conversion launch", who);
+    if (int rc = gemm_q_f16_run(type, r.a_hi, r.a_lo, (int)k, r.s_hi, r.s_lo, (int)k / 32, r.rscale, w, out, (int)n,
+                                nullptr, (int)m, (int)n, (int)k, form, nullptr, 0, g_ctx.stream))
+        return set_error(rc, "%s: launch", who);
+    return check_hip(hipGetLastError(), who);
+}
+
+int gemm_q_f16_check(const char* who, int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k,
+                     float* out) {
+    if (!a || !w || !out) return set_error(MXH_ERR_ARG, "%s: null pointer", who);
+    if (m <= 0 || n <= 0 || k <= 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX ||
+        !gemm_q_f16_supported(type, (int)k))
+        return set_error(MXH_ERR_ARG, "%s: bad shape %lldx%lldx%lld for type %d", who, (long long)m, (long long)n,
+                         (long long)k, type);
+    if (((uintptr_t)w & 15) || ((uintptr_t)a & 15))
+        return set_error(MXH_ERR_ARG, "%s: a and w must be 16-byte aligned", who);
+    return MXH_OK;
 }
 
 int stage(int slot, size_t bytes, void** out) {
@@ -125,7 +178,12 @@ int mxh_init(int device) {
     if (int rc = check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties")) return rc;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return set_error(MXH_ERR_NODEV, "device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+    if (device >= kMaxDevices) return set_error(MXH_ERR_ARG, "device %d beyond the %d the library tracks", device, kMaxDevices);
     if (int rc = check_hip(hipSetDevice(device), "hipSetDevice")) return rc;
+    // the no-allocation entry's scratch on this device (now current)
+    void* sp = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)")) return rc;
+    g_scratch_ptr[device] = sp;
     if (int rc = check_hip(hipStreamCreateWithFlags(&g_ctx.stream, hipStreamNonBlocking), "hipStreamCreate")) return rc;
     if (int rc = check_hip(hipEventCreate(&g_ctx.ev0), "hipEventCreate")) return rc;
     if (int rc = check_hip(hipEventCreate(&g_ctx.ev1), "hipEventCreate")) return rc;
@@ -260,30 +318,26 @@ int mxh_gemm_q_bf16(int type, const float* a, int64_t m, const void* w, int64_t 
     return check_hip(hipGetLastError(), "gemm launch");
 }
 
+
 int mxh_gemm_q_f16(int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k, float* out, int form) {
     if (int rc = ensure_ready()) return rc;
-    if (!a || !w || !out) return set_error(MXH_ERR_ARG, "gemm_f16: null pointer");
-    if (m <= 0 || n <= 0 || k <= 0 || m > INT32_MAX || n > INT32_MAX || !gemm_q_f16_supported(type, (int)k))
-        return set_error(MXH_ERR_ARG, "gemm_f16: bad shape %lldx%lldx%lld for type %d", (long long)m, (long long)n,
-                         (long long)k, type);
-    if (((uintptr_t)w & 15) || ((uintptr_t)a & 15))
-        return set_error(MXH_ERR_ARG, "gemm_f16: a and w must be 16-byte aligned");
-    // staging: a as fp16 hi / lo of a 2^e, the split sub-block sums, 2^-e per row
-    const size_t mk = (size_t)m * (size_t)k, nsb = mk / 32;
+    if (int rc = gemm_q_f16_check("gemm_f16", type, a, m, w, n, k, out)) return rc;
     void* buf = nullptr;
-    if (int rc = stage(2, 4 * mk + 4 * nsb + 4 * (size_t)m, &buf)) return rc;
-    uint16_t* a_hi = static_cast<uint16_t*>(buf);
-    uint16_t* a_lo = a_hi + mk;
-    uint16_t* s_hi = a_lo + mk;
-    uint16_t* s_lo = s_hi + nsb;
-    float* rscale = reinterpret_cast<float*>(s_lo + nsb);
-    if (int rc = rows_to_f16_launch(a, (int)k, nullptr, 0.f, (int)k, a_hi, a_lo, (int)k, s_hi, s_lo, (int)k / 32, rscale,
-                                    (int)m, g_ctx.stream))
-        return set_error(rc, "gemm_f16: conversion launch");
-    if (int rc = gemm_q_f16_run(type, a_hi, a_lo, (int)k, s_hi, s_lo, (int)k / 32, rscale, w, out, (int)n, nullptr,
-                                (int)m, (int)n, (int)k, form, nullptr, 0, g_ctx.stream))
-        return set_error(rc, "gemm_f16: launch");
-    return check_hip(hipGetLastError(), "gemm_f16 launch");
+    if (int rc = stage(2, f16_rows_bytes((size_t)m, (size_t)k), &buf)) return rc;
+    return gemm_q_f16_body("gemm_f16", type, a, m, w, n, k, out, form, buf);
+}
+
+int mxh_gemm_q_f16_noalloc(int type, const float* a, int64_t m, const void* w, int64_t n, int64_t k, float* out,
+                           int form) {
+    if (int rc = ensure_ready()) return rc;
+    if (int rc = gemm_q_f16_check("gemm_f16_noalloc", type, a, m, w, n, k, out)) return rc;
+    if (f16_rows_bytes((size_t)m, (size_t)k) > kNoallocScratchBytes)
+        return set_error(MXH_ERR_ARG, "gemm_f16_noalloc: %lld x %lld activations need %zu bytes of staging, above the "
+                         "%zu-byte device scratch", (long long)m, (long long)k, f16_rows_bytes((size_t)m, (size_t)k),
+                         kNoallocScratchBytes);
+    void* buf = g_scratch_ptr[g_ctx.device];
+    if (!buf) return set_error(MXH_ERR_HIP, "gemm_f16_noalloc: no scratch address for device %d", g_ctx.device);
+    return gemm_q_f16_body("gemm_f16_noalloc", type, a, m, w, n, k, out, form, buf);
 }
 
 int mxh_attention_prefill(const float* q, const void* kc, const void* vc, float* att, int p0, int m, int nh, int nkv,

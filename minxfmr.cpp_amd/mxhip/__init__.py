@@ -74,6 +74,7 @@ def _load() -> C.CDLL:
         "mxh_copy": (ip, [vp, vp, sz]),
         "mxh_gemm_q_bf16": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
         "mxh_gemm_q_f16": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
+        "mxh_gemm_q_f16_noalloc": (ip, [ip, vp, i64, vp, i64, i64, vp, ip]),
         "mxh_attention_prefill": (ip, [vp, vp, vp, vp, ip, ip, ip, ip, ip]),
         "mxh_tile_rows": (ip, [ip, vp, i64, i64, C.POINTER(C.c_int)]),
         "mxh_timer_begin": (ip, []),
@@ -114,7 +115,7 @@ def _load() -> C.CDLL:
 lib = _load()
 EXPORTED = (
     "mxh_init mxh_is_available mxh_last_error mxh_synchronize mxh_stream mxh_alloc mxh_free mxh_upload "
-    "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_gemm_q_f16 mxh_attention_prefill mxh_tile_rows mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
+    "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_gemm_q_f16 mxh_gemm_q_f16_noalloc mxh_attention_prefill mxh_tile_rows mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matmul_q mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_sample mxh_model_generate mxh_model_close "
