@@ -1,0 +1,135 @@
+"""BASELINE configs 3, 4 and 5 at their full model sizes (GPU).
+
+Config 3: Qwen3-8B architecture, Q4_K weights, Q8_0 lm-head.  A 64-token
+prompt and 16 greedy steps against the CPU oracle (fp16 cache): logits within
+the north-star bar (max-abs 2e-2 / relative 1e-2) and identical ids.  On the
+benchmark's own workload (512-token prompt, 256 greedy steps): graph replay
+= eager launches, tiled = GGUF-order weights, and the batched prefill's
+logits within the bar of the prompt fed token by token.
+
+Config 4: Llama-3-8B architecture with Q5_K attn_v / ffn_down, seeded top-k 8
+/ T 0.8 sampling: 16 prompt tokens and 16 sampled ids equal to the oracle's
+(the same seeded draw).
+
+Config 5: an 8192-token prompt in 512-token chunks: the logits after it
+within the bar of the token-by-token prefill, then 128 decode steps at an
+8K cache with graph = eager.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import mxhip
+import mxo
+
+pytestmark = pytest.mark.gpu
+
+QWEN3_8B = dict(n_layer=36, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=12288, n_vocab=151936,
+                ctx=40960, rope_theta=1e6, eps=1e-6, qk_norm=True, tied=False)
+LLAMA3_8B = dict(n_layer=32, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=14336, n_vocab=128256,
+                 ctx=8192, rope_theta=5e5, eps=1e-5, qk_norm=False, tied=False)
+
+
+def close_enough(got, want, atol=2e-2, rtol=1e-2):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    return bool(np.all(err <= atol + rtol * np.abs(want))), float(err.max())
+
+
+@pytest.fixture(scope="module")
+def qwen3_8b(tmp_path_factory):
+    p = tmp_path_factory.mktemp("c3") / "qwen3-8b-q4k.gguf"
+    mxhip.write_synthetic_gguf(p, "qwen3", wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K, seed=3,
+                               threads=16, **QWEN3_8B)
+    return p
+
+
+def test_config3_qwen3_8b_vs_oracle(mxh, qwen3_8b):
+    prompt = np.random.default_rng(33).integers(0, 151936, 64).astype(np.int32)
+    om = mxo.Model(qwen3_8b, 128, mxo.OPEN_KV_FP16, threads=16)
+    for t in prompt[:-1]:
+        om.step(int(t), want_logits=False)
+    olg, _ = om.step(int(prompt[-1]))
+    gm = mxhip.Model(qwen3_8b, 128)
+    gm.prefill(prompt[:-1])
+    lg, _ = gm.step(int(prompt[-1]))
+    worst = 0.0
+    for i in range(16):
+        ok, e = close_enough(lg, olg)
+        assert ok, f"step {i}: logits error {e}"
+        worst = max(worst, e)
+        want, got = int(np.argmax(olg)), int(np.argmax(lg))
+        top = np.sort(olg)[-2:]
+        assert got == want, f"step {i}: id {got} != oracle {want} (oracle top-2 margin {top[1] - top[0]:.3g})"
+        olg, _ = om.step(want)
+        lg, _ = gm.step(got)
+    om.close()
+    gm.close()
+    assert worst < 1e-2, worst
+
+
+def test_config3_bench_workload_properties(mxh, qwen3_8b):
+    prompt = np.random.default_rng(8).integers(0, 151936, 512).astype(np.int32)
+    n_ctx = 512 + 256 + 8
+    runs = {}
+    for name, flags in (("graph", 0), ("eager", mxhip.MODEL_NO_GRAPH), ("gguf", mxhip.MODEL_GGUF_LAYOUT)):
+        m = mxhip.Model(qwen3_8b, n_ctx, flags)
+        ids, _, _ = m.generate(prompt, 256)
+        runs[name] = ids
+        m.close()
+    assert np.array_equal(runs["graph"], runs["eager"])
+    assert np.array_equal(runs["graph"], runs["gguf"])
+    # batched prefill vs the prompt token by token through the decode step
+    logits = {}
+    for name, flags in (("batched", 0), ("token", mxhip.MODEL_TOKEN_PREFILL)):
+        m = mxhip.Model(qwen3_8b, n_ctx, flags)
+        m.prefill(prompt[:-1])
+        logits[name], _ = m.step(int(prompt[-1]))
+        m.close()
+    ok, e = close_enough(logits["batched"], logits["token"])
+    assert ok and e < 1e-2, e
+    assert int(np.argmax(logits["batched"])) == runs["graph"][0]
+
+
+def test_config4_llama3_8b_mixed_sampling_vs_oracle(mxh, tmp_path):
+    p = tmp_path / "llama3-8b-mixed.gguf"
+    mxhip.write_synthetic_gguf(p, "llama", wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K,
+                               attn_v_type=mxhip.Q5_K, ffn_down_type=mxhip.Q5_K, seed=4, threads=16, **LLAMA3_8B)
+    prompt = np.random.default_rng(44).integers(0, 128256, 16).astype(np.int32)
+    seed, top_k, temp = 0xC0F3, 8, 0.8
+    gm = mxhip.Model(p, 64)
+    gm.set_sampling(top_k, temp, seed=seed)
+    ids, _, _ = gm.generate(prompt, 16)
+    gm.close()
+    om = mxo.Model(p, 64, mxo.OPEN_KV_FP16, threads=16)
+    lg = None
+    for t in prompt:
+        lg, _ = om.step(int(t))
+    want, st = [], seed
+    for _ in range(16):
+        tok, st = mxo.sample(lg, top_k, temp, 1.0, 0.0, st)
+        want.append(tok)
+        lg, _ = om.step(tok)
+    om.close()
+    assert ids.tolist() == want
+
+
+def test_config5_long_context(mxh, qwen3_8b):
+    n_prompt = 8192
+    prompt = np.random.default_rng(55).integers(0, 151936, n_prompt).astype(np.int32)
+    n_ctx = n_prompt + 128 + 8
+    logits = {}
+    for name, flags in (("batched", 0), ("token", mxhip.MODEL_TOKEN_PREFILL)):
+        m = mxhip.Model(qwen3_8b, n_ctx, flags)
+        m.prefill(prompt[:-1])
+        logits[name], _ = m.step(int(prompt[-1]))
+        m.close()
+    ok, e = close_enough(logits["batched"], logits["token"])
+    assert ok and e < 1e-2, e
+    ids = {}
+    for name, flags in (("graph", 0), ("eager", mxhip.MODEL_NO_GRAPH)):
+        m = mxhip.Model(qwen3_8b, n_ctx, flags)
+        out, _, _ = m.generate(prompt, 128)
+        ids[name] = out
+        m.close()
+    assert np.array_equal(ids["graph"], ids["eager"])
