@@ -228,14 +228,14 @@ enum {
     MXH_MODEL_GGML_FORM = 4,    /* ggml Q4_K/Q5_K scale unpacking instead of the reference CPU form */
     MXH_MODEL_NO_QK_NORM = 8,   /* ignore attn_{q,k}_norm (reference layer semantics) */
     MXH_MODEL_NO_GRAPH = 16,    /* enqueue kernels directly instead of replaying HIP graphs */
-    MXH_MODEL_TOKEN_PREFILL = 32, /* prompt token by token through the decode step (fp32 GEMVs) instead of
-                                     batched on the matrix cores (bf16 GEMM inputs) */
+    MXH_MODEL_TOKEN_PREFILL = 32, /* prompt token by token through the decode step (GEMVs with 24-bit x)
+                                     instead of batched on the matrix cores */
     MXH_MODEL_GGUF_LAYOUT = 64,   /* keep the projection weights in their GGUF block order in HBM instead of
                                      the tiled order (same bytes regrouped per row) the kernels read fastest;
                                      results are identical either way */
     MXH_MODEL_BF16_PREFILL = 128  /* batched prefill GEMMs in the split-bf16 form for every weight type; by
-                                     default Q4_K projections use the exact-weight fp16 form (weights as
-                                     integers sc*q, activations as fp16 hi + lo) */
+                                     default quantized projections use the exact-weight fp16 form (weights as
+                                     integer codes, activations as fp16 hi + lo) */
 };
 
 /* Load a GGUF file into HBM with room for n_ctx positions.

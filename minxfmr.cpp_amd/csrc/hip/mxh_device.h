@@ -175,9 +175,25 @@ __device__ __forceinline__ double wave_sum_d_all(double v) {
 // Stores and loads that are coherent across the per-XCD L2 caches by
 // themselves (agent-scope relaxed atomics, issued with sc1): data one
 // workgroup hands to another within a launch goes through these, so no
-// device-wide fence (an L2 writeback and invalidate) is needed.  Ordering
-// comes from waiting for the stores (s_waitcnt) before the atomic counter
-// that publishes them.
+// device-wide fence (an L2 writeback and invalidate) is needed.
+//
+// The hand-off protocol and the invariant it relies on.  A producer writes
+// its data with st_agent (sc1: written through its XCD's L2 to the device
+// coherence point), then waits for its own stores with s_waitcnt vmcnt(0)
+// (wait_mem: on this target a store leaves the count only when the write is
+// acknowledged), then publishes with a relaxed agent-scope atomic add on a
+// counter.  The consumer that sees the final count (the add's return value
+// in the attention merge) then reads the data with ld_agent / ld_agent4
+// (sc1 loads, which do not return a line its own XCD's L2 may hold stale).
+// The C++ memory model would want release / acquire orderings here; they
+// are not used because at agent scope they lower to an L2 writeback before
+// the atomic and an L2 invalidate after it, which cost microseconds with
+// hundreds of workgroups.  What makes the relaxed form correct is the
+// hardware order above: every data store is complete at the coherence
+// point before the counter update is issued, and the consumer's data loads
+// are issued after its atomic returned and bypass stale cached copies.
+// Code that hands data over must keep that shape: sc1 stores, a full vmcnt
+// wait, the atomic; the atomic's result, then sc1 loads.
 __device__ __forceinline__ void st_agent(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

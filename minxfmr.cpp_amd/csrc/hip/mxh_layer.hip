@@ -366,7 +366,9 @@ __global__ __launch_bounds__(256) void attention_kernel(const int* ppos, __half*
     }
 
     // the last workgroup of kv head g to finish merges the partials; they
-    // were stored device-coherently and are complete before the count
+    // were stored device-coherently and are complete before the count (the
+    // hand-off protocol written out at st_agent in mxh_device.h: sc1 stores,
+    // a full vmcnt wait, the relaxed add; the add's return value, sc1 loads)
     wait_mem();
     __syncthreads();
     if (tid == 0) last = add_agent(a.counter + g, 1) == nparts - 1;
