@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--prompt P] [--no-cpu-baseline]
 
-Workload (BASELINE.json configs[2]): a seeded synthetic GGUF with the
+Workload (BASELINE config 3, BASELINE.json configs[2]): a seeded synthetic GGUF with the
 Qwen3-8B architecture (36 layers, hidden 4096, 32/8 heads of 128, FFN 12288,
 vocab 151936, QK-norm), every 2D weight Q4_K, the lm-head Q8_0.  A P-token
 seeded prompt (default 512) is prefilled, W decode steps warm up, then
@@ -11,12 +11,14 @@ through the whole device-resident stack plus the lm-head and argmax.
 
 One JSON line is printed.  `value` is decode tokens/s; `roofline` is for the
 dominant kernel, the Q4_K dequant-GEMV, timed with HIP events over every
-Q4_K GEMV of the model on its own HBM-resident weights (`traffic` is the
-HBM bytes per launch that rocprofv3 counters measured for the same shapes,
-profiles/gemv_q4k_traffic.json); `cpu_baseline` is the CPU oracle decoding a
-bounded sample of the same model on the host cores.  Also reported:
-`gemv_microbench` (the isolated Q4_K GEMV shapes),
-`long_context`, and with --all-configs configs[0] and [3].
+Q4_K GEMV of the model on its own HBM-resident weights, launched as the
+decode step launches them (`traffic` is the HBM bytes per launch that
+rocprofv3 counters measured for the same launches, read from the committed
+profiles/gemv_q4k_traffic.json, not measured in this run); `cpu_baseline` is
+the CPU oracle decoding a bounded sample of the same model on the host
+cores.  Also reported: `gemv_microbench` (the isolated
+Q4_K GEMV shapes), `long_context` (config 5), and with --all-configs
+configs 1 (Qwen3-0.6B) and 4 (Llama-3-8B mixed).
 """
 from __future__ import annotations
 
@@ -87,7 +89,7 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
 def cpu_reference_gemv(budget_s: float, seed: int) -> dict | None:
     """The reference's own CPU GEMV (backend_matmul_rhs_transposed from its
     sources, built into oracle/_ref/libmxref.so with OpenMP) on the four
-    Q4_K shapes of BASELINE config 1, random blocks with small finite d, dmin,
+    Q4_K shapes of BASELINE config 2, random blocks with small finite d, dmin,
     x ~ N(0, 1); each shape repeated within an equal share of the time budget.
     None when the library was not built."""
     import numpy as np
@@ -123,7 +125,7 @@ def cpu_reference_gemv(budget_s: float, seed: int) -> dict | None:
     return {"value": round(tot_bytes / tot_s / 1e9, 2),
             "unit": "GB/s", "cores": threads, "kind": "reference",
             "sample": "the reference's backend_matmul_rhs_transposed (its CPU sources, OpenMP) on the four Q4_K shapes "
-                      "of BASELINE config 1, each repeated for about a quarter of the budget; value = algorithmic bytes "
+                      "of BASELINE config 2, each repeated for about a quarter of the budget; value = algorithmic bytes "
                       "of one call per shape over the summed per-call times",
             "shapes": shapes}
 
@@ -154,7 +156,7 @@ def extra_model(mxhip, name: str, seed: int) -> Path:
 
 
 def run_long_context(mxhip, path: Path, seed: int) -> dict:
-    """BASELINE config 4: 8192-token prompt prefilled in 512-token chunks on
+    """BASELINE config 5: 8192-token prompt prefilled in 512-token chunks on
     the matrix cores, then 128 greedy decode tokens against the 8192+ cache."""
     import numpy as np
 
@@ -177,7 +179,7 @@ def run_long_context(mxhip, path: Path, seed: int) -> dict:
 
 
 def run_gemv_microbench(mxhip, seed: int) -> dict:
-    """BASELINE config 1: the isolated Q4_K dequant-GEMV at batch 1 over the
+    """BASELINE config 2: the isolated Q4_K dequant-GEMV at batch 1 over the
     four listed shapes, with the weights regrouped into the tiled layout
     (mxh_tile_rows) as the model holds them.  Each shape rotates over at least
     512 MB of distinct weight copies (more than the 256 MB Infinity Cache), so
@@ -222,7 +224,7 @@ def run_gemv_microbench(mxhip, seed: int) -> dict:
 
 
 def run_extra_configs(mxhip, seed: int) -> dict:
-    """BASELINE configs 0 and 3: Qwen3-0.6B Q8_0 greedy (32-token prompt, 128
+    """BASELINE configs 1 and 4: Qwen3-0.6B Q8_0 greedy (32-token prompt, 128
     tokens) and Llama-3-8B mixed Q4_K/Q5_K with seeded top-k 8, T 0.8 sampling
     (128-token prompt, 512 tokens)."""
     import numpy as np
@@ -274,7 +276,7 @@ def main() -> int:
     ap.add_argument("--no-long-context", action="store_true", help="skip the 8192-token context measurement")
     ap.add_argument("--no-microbench", action="store_true", help="skip the isolated Q4_K GEMV shapes")
     ap.add_argument("--all-configs", action="store_true",
-                    help="also run BASELINE configs 0 (Qwen3-0.6B Q8_0) and 3 (Llama-3-8B mixed, sampled)")
+                    help="also run BASELINE configs 1 (Qwen3-0.6B Q8_0) and 4 (Llama-3-8B mixed, sampled)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build targets a single MI355X); --gpus {args.gpus} is not "
@@ -337,7 +339,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        # the GEMV arithmetic: Q4_K codes times x as 24-bit block fixed point
+        # (int8 limb dot products, exact in int32), fp32 scaling and sums
+        "dtype": "q4_k x int24 (int32 dot, fp32 accumulate)",
         "data": "synthetic",
         "config": {"workload": f"qwen3-8b-shape, Q4_K weights + Q8_0 lm-head, bs=1: {args.prompt}-token seeded "
                                f"prompt prefill, then {args.steps} timed greedy decode steps",
@@ -353,7 +357,12 @@ def main() -> int:
                                        "split hi+lo activations)"},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(g_bytes_launch),
-                     "kernel": "Q4_K dequant-GEMV, tiled weight layout (gemv_kernel<Q4KT>)",
+                     "traffic_source": "profiles/gemv_q4k_traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE of the "
+                                       "same launches, calibrated by a copy of known size (committed, not measured "
+                                       "in this run)",
+                     "kernel": "Q4_K dequant-GEMV, tiled weight layout (gemv_kernel<Q4KT>), every Q4_K GEMV of "
+                               "the decode step as the step launches it (norm-fused q|k|v and gate|up, SwiGLU "
+                               "gate|up, residual o and down)",
                      "per_launch_bytes": int(g_bytes_launch), "avg_launch_us": round(g_avg_us, 3)},
     }
     if not args.no_microbench:

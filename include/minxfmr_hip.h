@@ -281,9 +281,11 @@ int mxh_model_generate(mxh_model *m, const int *prompt, int n_prompt, int n_gen,
 int mxh_model_decode(mxh_model *m, int n_gen, int *out, float *decode_ms);
 /* Enqueue every GEMV of the model whose weights have `type` (in layer order,
  * then the lm-head) `reps` times on the library stream, on the model's own
- * HBM-resident weights; reports device time, launch count and algorithmic
- * bytes (weights + fp32 x and y).  Benchmark support, no reference
- * counterpart. */
+ * HBM-resident weights and in the form the decode step launches it (norm
+ * fused into the q|k|v and gate|up staging, SwiGLU epilogue for gate|up,
+ * residual for o and down; the lm-head plain), writing scratch vectors only;
+ * reports device time, launch count and algorithmic bytes (weights + fp32 x
+ * and y).  Benchmark support, no reference counterpart. */
 int mxh_model_bench_gemv(mxh_model *m, int type, int reps, float *ms, int64_t *launches, int64_t *bytes);
 void mxh_model_close(mxh_model *m);
 

@@ -14,6 +14,8 @@
 
 #include <cmath>
 #include <cstring>
+#include <exception>
+#include <new>
 #include <initializer_list>
 #include <string>
 #include <vector>
@@ -232,13 +234,14 @@ bool gemv_type_ok(int t) { return t == MXH_Q4_K || t == MXH_Q5_K || t == MXH_Q8_
 
 extern "C" {
 
-int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out) {
+static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_model** out) {
     if (!gguf_path || !out || n_ctx <= 0) return set_error(MXH_ERR_ARG, "model_open: bad arguments");
     *out = nullptr;
-    if (int rc = mxh_init(0)) return rc;
+    // the file is checked before any device work
     GgufFile f;
     std::string err;
     if (!f.open(gguf_path, &err)) return set_error(MXH_ERR_ARG, "model_open: %s", err.c_str());
+    if (int rc = mxh_init(0)) return rc;
 
     mxh_model* m = new mxh_model();
     mxh_model_config& c = m->cfg;
@@ -800,30 +803,50 @@ int mxh_model_decode(mxh_model* m, int n_gen, int* out, float* decode_ms) {
 int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* launches, int64_t* bytes) {
     if (!m || reps <= 0 || !ms) return set_error(MXH_ERR_ARG, "bench_gemv: bad arguments");
     hipStream_t st = lib_stream();
-    std::vector<const DevW*> ws;
-    for (const Layer& L : m->layers)
-        for (const DevW* w : {&L.qkv, &L.q, &L.k, &L.v, &L.o, &L.gu, &L.g, &L.u, &L.down})
-            if (w->p && storage_type(w->type) == type) ws.push_back(w);
-    if (storage_type(m->out.type) == type) ws.push_back(&m->out);
-    if (ws.empty()) return set_error(MXH_ERR_ARG, "bench_gemv: model has no matrices of type %d", type);
+    const mxh_model_config& c = m->cfg;
+    const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+    // every GEMV of `type` in the form the decode step launches it (fused
+    // norms, SwiGLU and residual epilogues), outputs into scratch vectors so
+    // the model's state is left as it was; the lm-head in plain mode
+    struct Job {
+        const DevW* w;
+        const float *x, *res, *nw;
+        float* y;
+        int mode;
+    };
+    std::vector<Job> jobs;
+    auto add = [&](const DevW& w, const float* x, float* y, const float* res, const float* nw, int mode) {
+        if (w.p && storage_type(w.type) == type) jobs.push_back(Job{&w, x, res, nw, y, mode});
+    };
+    for (const Layer& L : m->layers) {
+        add(L.qkv, m->x, m->qkv, nullptr, L.attn_norm, GEMV_PLAIN);
+        add(L.q, m->x, m->qkv, nullptr, L.attn_norm, GEMV_PLAIN);
+        add(L.k, m->x, m->qkv + qd, nullptr, L.attn_norm, GEMV_PLAIN);
+        add(L.v, m->x, m->qkv + qd + kvd, nullptr, L.attn_norm, GEMV_PLAIN);
+        add(L.o, m->att, m->xn, m->x, nullptr, GEMV_PLAIN);
+        add(L.gu, m->x, m->h, nullptr, L.ffn_norm, GEMV_SILU);
+        add(L.g, m->x, m->gu, nullptr, L.ffn_norm, GEMV_PLAIN);
+        add(L.u, m->x, m->gu + c.n_ff, nullptr, L.ffn_norm, GEMV_PLAIN);
+        add(L.down, m->h, m->xn, m->x, nullptr, GEMV_PLAIN);
+    }
+    add(m->out, m->x, m->logits, nullptr, m->out_norm, GEMV_PLAIN);
+    if (jobs.empty()) return set_error(MXH_ERR_ARG, "bench_gemv: model has no matrices of type %d", type);
     int64_t b = 0;
-    for (const DevW* w : ws) b += (int64_t)row_bytes(w->type, w->cols) * w->rows + 4 * (w->rows + w->cols);
+    for (const Job& j : jobs) b += (int64_t)row_bytes(j.w->type, j.w->cols) * j.w->rows + 4 * (j.w->rows + j.w->cols);
     hipEvent_t e0, e1;
     if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
     (void)hipEventCreate(&e1);
     int rc = check_hip(hipEventRecord(e0, st), "event");
     for (int r = 0; r < reps && !rc; ++r)
-        for (const DevW* w : ws) {
-            // x: a K-long activation buffer (xn holds max(n_embd, n_ff)); y: scratch wide enough for any row count
-            float* y = w->rows <= 2 * (int64_t)m->cfg.n_ff ? m->gu : m->logits;
-            rc = gemv(*w, m->xn, y, nullptr, m->form, st);
+        for (const Job& j : jobs) {
+            rc = gemv(*j.w, j.x, j.y, j.res, m->form, st, j.nw, c.eps, j.mode);
             if (rc) break;
         }
     if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
     if (!rc) rc = check_hip(hipEventSynchronize(e1), "bench_gemv");
     if (!rc) {
         (void)hipEventElapsedTime(ms, e0, e1);
-        if (launches) *launches = (int64_t)ws.size() * reps;
+        if (launches) *launches = (int64_t)jobs.size() * reps;
         if (bytes) *bytes = b * reps;
     }
     (void)hipEventDestroy(e0);
@@ -833,7 +856,35 @@ int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* l
 
 void mxh_model_close(mxh_model* m) { free_model(m); }
 
+// No C++ exception crosses the C ABI: allocation failures and anything else
+// a malformed file may raise come back as status codes.
+int mxh_model_open(const char* gguf_path, int n_ctx, int flags, mxh_model** out) {
+    try {
+        return model_open_impl(gguf_path, n_ctx, flags, out);
+    } catch (const std::bad_alloc&) {
+        return set_error(MXH_ERR_OOM, "model_open: host allocation failed");
+    } catch (const std::exception& e) {
+        return set_error(MXH_ERR_ARG, "model_open: %s", e.what());
+    } catch (...) {
+        return set_error(MXH_ERR_ARG, "model_open: unexpected failure");
+    }
+}
+
+static int write_synthetic_impl(const char* path, const mxh_synth_arch* a, uint64_t seed, int threads);
+
 int mxh_write_synthetic_gguf(const char* path, const mxh_synth_arch* a, uint64_t seed, int threads) {
+    try {
+        return write_synthetic_impl(path, a, seed, threads);
+    } catch (const std::bad_alloc&) {
+        return set_error(MXH_ERR_OOM, "write_synthetic_gguf: host allocation failed");
+    } catch (const std::exception& e) {
+        return set_error(MXH_ERR_ARG, "write_synthetic_gguf: %s", e.what());
+    } catch (...) {
+        return set_error(MXH_ERR_ARG, "write_synthetic_gguf: unexpected failure");
+    }
+}
+
+static int write_synthetic_impl(const char* path, const mxh_synth_arch* a, uint64_t seed, int threads) {
     if (!path || !a || !a->arch) return set_error(MXH_ERR_ARG, "write_synthetic_gguf: null argument");
     SynthArch s;
     s.arch = a->arch;

@@ -203,8 +203,12 @@ uint64_t mix(uint64_t a, uint64_t b) {
 
 size_t tensor_bytes(int type, int64_t rows, int64_t cols) {
     const BlockInfo b = block_info(type);
-    if (!b.elems || cols % b.elems) return 0;
-    return (size_t)rows * (size_t)(cols / b.elems) * (size_t)b.bytes;
+    if (!b.elems || rows < 0 || cols < 0 || cols % b.elems) return 0;
+    size_t row = 0, total = 0;
+    if (__builtin_mul_overflow((size_t)(cols / b.elems), (size_t)b.bytes, &row) ||
+        __builtin_mul_overflow((size_t)rows, row, &total))
+        return 0;
+    return total;
 }
 
 void quantize_row(int type, const float* x, int64_t n, uint8_t* out) {
@@ -300,6 +304,7 @@ bool GgufFile::open(const std::string& path, std::string* err) {
     for (uint64_t i = 0; i < n_kv && c.ok(); ++i) {
         const std::string key = c.str();
         const uint32_t t = (uint32_t)c.u(4);
+        if (!c.ok()) break;  // reported as a truncated header below
         if (t == 8) {
             strs_[key] = c.str();
         } else if (t == 9) {
@@ -320,13 +325,27 @@ bool GgufFile::open(const std::string& path, std::string* err) {
     }
     auto it = strs_.find("general.architecture");
     arch_ = it != strs_.end() ? it->second : "";
+    if (!c.ok()) {
+        *err = "truncated GGUF header";
+        return false;
+    }
+    // a directory entry takes at least 32 bytes (name length, rank, one
+    // dimension, type, offset): a count beyond what the file can hold is corrupt
+    if (n_tensors > (size_ - c.pos()) / 32) {
+        *err = "tensor count exceeds the file";
+        return false;
+    }
     tensors_.resize((size_t)n_tensors);
     for (uint64_t i = 0; i < n_tensors && c.ok(); ++i) {
         GgufTensor& t = tensors_[(size_t)i];
         t.name = c.str();
         t.n_dims = (int)c.u(4);
         if (t.n_dims < 1 || t.n_dims > 4) { *err = "bad tensor rank for " + t.name; return false; }
-        for (int d = 0; d < t.n_dims; ++d) t.ne[d] = (int64_t)c.u(8);
+        for (int d = 0; d < t.n_dims; ++d) {
+            const uint64_t ne = c.u(8);
+            if (ne > (uint64_t)INT64_MAX) { *err = "bad dimension for " + t.name; return false; }
+            t.ne[d] = (int64_t)ne;
+        }
         t.type = (int)c.u(4);
         t.offset = c.u(8);
     }
@@ -334,15 +353,26 @@ bool GgufFile::open(const std::string& path, std::string* err) {
         *err = "truncated GGUF header";
         return false;
     }
-    if (alignment == 0 || (alignment & (alignment - 1))) { *err = "bad alignment"; return false; }
+    if (alignment == 0 || (alignment & (alignment - 1)) || alignment > (1u << 20)) { *err = "bad alignment"; return false; }
     const size_t data0 = (c.pos() + alignment - 1) / alignment * alignment;
+    if (data0 > size_) { *err = "tensor data starts past end of file"; return false; }
     for (size_t i = 0; i < tensors_.size(); ++i) {
         GgufTensor& t = tensors_[i];
         int64_t rows = 1;
-        for (int d = 1; d < t.n_dims; ++d) rows *= t.ne[d];
+        bool overflow = false;
+        for (int d = 1; d < t.n_dims; ++d) overflow |= __builtin_mul_overflow(rows, t.ne[d], &rows);
+        if (overflow) { *err = "tensor " + t.name + " has too many elements"; return false; }
         t.nbytes = tensor_bytes(t.type, rows, t.ne[0]);
-        if (t.nbytes == 0 && block_info(t.type).elems == 0) continue;  // unknown type: not addressable
-        if (data0 + t.offset + t.nbytes > size_) { *err = "tensor " + t.name + " extends past end of file"; return false; }
+        if (block_info(t.type).elems == 0) continue;  // unknown type: not addressable
+        if (t.nbytes == 0 && rows > 0 && t.ne[0] > 0) {
+            *err = "tensor " + t.name + " is not a whole number of blocks";
+            return false;
+        }
+        // offset, then size, against the bytes left (no sum that can wrap)
+        if (t.offset > size_ - data0 || t.nbytes > size_ - data0 - t.offset) {
+            *err = "tensor " + t.name + " extends past end of file";
+            return false;
+        }
         t.data = base + data0 + t.offset;
         index_[t.name] = i;
     }

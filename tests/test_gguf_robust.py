@@ -1,0 +1,58 @@
+"""The GGUF reader behind mxh_model_open rejects malformed files with a
+status and a message instead of reading out of bounds or throwing through
+the C ABI (CPU only: the file is checked before any device work)."""
+from __future__ import annotations
+
+import ctypes as C
+import struct
+
+import pytest
+
+import mxhip
+
+
+def _s(x: str) -> bytes:
+    return struct.pack("<Q", len(x)) + x.encode()
+
+
+def gguf(path, n_tensors=None, ne=(32, 4), offset=0, ttype=0, truncate=None):
+    """One F32 tensor token_embd.weight with dims `ne` at `offset`."""
+    kv = _s("general.architecture") + struct.pack("<I", 8) + _s("qwen3")
+    ent = _s("token_embd.weight") + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", n) for n in ne)
+    ent += struct.pack("<IQ", ttype, offset)
+    head = struct.pack("<IIQQ", 0x46554747, 3, 1 if n_tensors is None else n_tensors, 1) + kv + ent
+    head += b"\0" * ((-len(head)) % 32)
+    data = head + b"\0" * (4 * 32 * 4)
+    if truncate is not None:
+        data = data[:truncate]
+    path.write_bytes(data)
+    return path
+
+
+def open_err(path):
+    h = C.c_void_p()
+    rc = mxhip.lib.mxh_model_open(str(path).encode(), 16, 0, C.byref(h))
+    return rc, mxhip.lib.mxh_last_error().decode()
+
+
+@pytest.mark.parametrize("case,kw,msg", [
+    ("tensor count beyond the file", dict(n_tensors=1 << 40), "tensor count"),
+    ("offset that wraps", dict(offset=(1 << 64) - 16), "past end"),
+    ("offset past the end", dict(offset=1 << 20), "past end"),
+    ("dimension above int64", dict(ne=(32, (1 << 63) + 5)), "bad dimension"),
+    ("element count overflow", dict(ne=(32, 1 << 40, 1 << 40)), "too many elements"),
+    ("rows not whole blocks", dict(ne=(48, 4), ttype=8), "whole number of blocks"),
+    ("truncated directory", dict(truncate=40), "truncated"),
+])
+def test_malformed_gguf_is_rejected(tmp_path, case, kw, msg):
+    rc, err = open_err(gguf(tmp_path / "bad.gguf", **kw))
+    assert rc != 0
+    assert msg in err, (case, err)
+
+
+def test_wellformed_gguf_gets_past_the_reader(tmp_path):
+    rc, err = open_err(gguf(tmp_path / "ok.gguf"))
+    # without a GPU the next step (device init) fails; with one, the model
+    # lacks layers; either way the reader accepted the file
+    assert rc != 0
+    assert "past end" not in err and "tensor count" not in err and "truncated" not in err
