@@ -258,6 +258,21 @@ int mxh_model_position(const mxh_model *m);
  * same. */
 int mxh_model_set_sampling(mxh_model *m, int top_k, double temperature, double top_p, double min_p, uint64_t seed);
 
+/* Logit edits applied before every following choice (greedy or sampled),
+ * on the device, as src/api/minxfmr.cpp:2047-2089 applies them: the ids in
+ * suppress[0 .. n_suppress) get -inf (the caller passes the reference's
+ * special-token ids minus its EOS tokens), then over the last repeat_last_n
+ * ids of the history (prompt and generated ids up to the current position;
+ * repeat_last_n < 0: all of it) each distinct id with count c has its logit
+ * l replaced by (l <= 0 ? l * repeat_penalty : l / repeat_penalty)
+ * - c * frequency_penalty - presence_penalty, computed in double (the
+ * repeat factor only when repeat_penalty != 1; no penalty pass when the
+ * window is empty or all three are neutral).  No ids and neutral penalties
+ * restore the fused greedy head.  The reference keeps logits in double; here
+ * they are fp32, so the edited value is rounded once to float. */
+int mxh_model_set_logit_edits(mxh_model *m, const int *suppress, int n_suppress, int repeat_last_n,
+                              double repeat_penalty, double frequency_penalty, double presence_penalty);
+
 /* One sampling decision over n device-resident logits with the rules of
  * mxh_model_set_sampling, using draw number `draw` of the stream; the token
  * id is written to *token (host).  For tests and per-op callers. */

@@ -115,6 +115,18 @@ struct SampleParams {
     uint64_t draws;
 };
 size_t sample_scratch_keys(int n, int top_k);
+// Logit edits before the choice (minxfmr.cpp:2047-2089), parameters in
+// device memory: suppressed ids to -inf, then over the last last_n ids of
+// tokens[0 .. *pos] (all when last_n < 0) each distinct id with count c:
+// l = (l <= 0 ? l * repeat : l / repeat) - c * frequency - presence.  cnt is
+// an n_vocab int scratch that is zero before and after.
+struct EditParams {
+    int last_n;
+    int n_suppress;
+    double repeat_penalty, frequency_penalty, presence_penalty;
+};
+int logit_edits_launch(float* logits, int n_vocab, const int* tokens, const int* pos, const EditParams* prm,
+                       const int* suppress, int* cnt, hipStream_t st);
 int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint64_t* cand, int* out, int* tokens,
                   int* pos, hipStream_t st);
 int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,

@@ -74,6 +74,11 @@ struct mxh_model {
     int top_k = 1;
     SampleParams* sprm = nullptr;  // device copy, draw counter included
     uint64_t* scand = nullptr;     // pass-1 candidates
+    // logit edits before the choice (mxh_model_set_logit_edits)
+    bool edits = false;
+    EditParams* eprm = nullptr;  // device copy
+    int* esup = nullptr;         // suppressed ids [n_vocab]
+    int* ecnt = nullptr;         // per-id counts [n_vocab], zero between steps
     // batched prefill (allocated on first use): rows of up to pf_rows tokens
     int pf_rows = 0;
     float *pf_x = nullptr, *pf_qkv = nullptr, *pf_q = nullptr, *pf_att = nullptr, *pf_gu = nullptr;
@@ -165,10 +170,19 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
     }
     if (with_head) {
         if (m->trace_on) rc |= rmsnorm_launch(m->x, m->out_norm, m->trace + (size_t)c.n_layer * d, d, c.eps, st);
-        if (m->sampling) {
-            // logits, then top-k / temperature sampling writes tokens[pos+1]
+        if (m->sampling || m->edits) {
+            // logits, the reference's edits (suppressed ids, penalties over
+            // the history), then top-k / temperature sampling or the argmax
+            // writes tokens[pos+1]
             rc |= gemv(m->out, m->x, m->logits, nullptr, m->form, st, m->out_norm, c.eps);
-            rc |= sample_launch(m->logits, c.n_vocab, m->sprm, m->top_k, m->scand, nullptr, m->tokens, m->pos, st);
+            if (m->edits)
+                rc |= logit_edits_launch(m->logits, c.n_vocab, m->tokens, m->pos, m->eprm, m->esup, m->ecnt, st);
+            if (m->sampling) {
+                rc |= sample_launch(m->logits, c.n_vocab, m->sprm, m->top_k, m->scand, nullptr, m->tokens, m->pos, st);
+            } else {
+                rc |= argmax_launch(m->logits, c.n_vocab, m->tokens, m->pos, st);
+                rc |= add_int_launch(m->pos, 1, st);
+            }
         } else {
             rc |= gemv(m->out, m->x, m->logits, nullptr, m->form, st, m->out_norm, c.eps, GEMV_ARGMAX, m);
         }
@@ -211,7 +225,8 @@ int free_model(mxh_model* m) {
     void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
                     m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
                     m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part,
-                    m->pf_h16, m->pf_l16, m->pf_sh, m->pf_sl, m->pf_rscale, m->sprm, m->scand};
+                    m->pf_h16, m->pf_l16, m->pf_sh, m->pf_sl, m->pf_rscale, m->sprm, m->scand, m->eprm, m->esup,
+                    m->ecnt};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     delete m;
@@ -490,6 +505,11 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     if (!rc) rc = dalloc(&m->sprm, 1);
     if (!rc) rc = dalloc(&m->scand, std::max(sample_scratch_keys(c.n_vocab, 64), (size_t)4096));
     if (!rc) rc = check_hip(hipMemset(m->sprm, 0, sizeof(SampleParams)), "sampler init");
+    if (!rc) rc = dalloc(&m->eprm, 1);
+    if (!rc) rc = dalloc(&m->esup, (size_t)c.n_vocab);
+    if (!rc) rc = dalloc(&m->ecnt, (size_t)c.n_vocab);
+    if (!rc) rc = check_hip(hipMemset(m->eprm, 0, sizeof(EditParams)), "edit params init");
+    if (!rc) rc = check_hip(hipMemset(m->ecnt, 0, sizeof(int) * (size_t)c.n_vocab), "edit counts init");
     if (!rc) rc = dalloc(&m->counters, (size_t)c.n_head_kv + 1);
     if (!rc) rc = check_hip(hipMemset(m->counters, 0, sizeof(int) * ((size_t)c.n_head_kv + 1)), "counter init");
     if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * ((size_t)n_ctx + 1)), "token init");
@@ -717,6 +737,53 @@ int mxh_model_set_sampling(mxh_model* m, int top_k, double temperature, double t
         }
     }
     return MXH_OK;
+}
+
+int mxh_model_set_logit_edits(mxh_model* m, const int* suppress, int n_suppress, int repeat_last_n,
+                              double repeat_penalty, double frequency_penalty, double presence_penalty) {
+    if (!m || n_suppress < 0 || (n_suppress > 0 && !suppress))
+        return set_error(MXH_ERR_ARG, "set_logit_edits: bad arguments");
+    if (n_suppress > m->cfg.n_vocab) return set_error(MXH_ERR_ARG, "set_logit_edits: %d ids exceed the vocabulary", n_suppress);
+    if (!(repeat_penalty > 0.0) || !std::isfinite(repeat_penalty) || !std::isfinite(frequency_penalty) ||
+        !std::isfinite(presence_penalty))
+        return set_error(MXH_ERR_ARG, "set_logit_edits: penalties must be finite, repeat_penalty > 0");
+    hipStream_t st = lib_stream();
+    if (int rc = check_hip(hipStreamSynchronize(st), "set_logit_edits")) return rc;
+    EditParams h{};
+    h.last_n = repeat_last_n;
+    h.n_suppress = n_suppress;
+    h.repeat_penalty = repeat_penalty;
+    h.frequency_penalty = frequency_penalty;
+    h.presence_penalty = presence_penalty;
+    if (int rc = check_hip(hipMemcpy(m->eprm, &h, sizeof(h), hipMemcpyHostToDevice), "edit params")) return rc;
+    if (n_suppress > 0)
+        if (int rc = check_hip(hipMemcpy(m->esup, suppress, sizeof(int) * (size_t)n_suppress, hipMemcpyHostToDevice),
+                               "suppressed ids"))
+            return rc;
+    // the reference skips its penalty pass when the window is empty or every
+    // penalty is neutral (minxfmr.cpp:2065)
+    const bool pen = repeat_last_n != 0 && (repeat_penalty != 1.0 || frequency_penalty != 0.0 || presence_penalty != 0.0);
+    const bool want = n_suppress > 0 || pen;
+    if (want == m->edits) return MXH_OK;
+    m->edits = want;
+    // the decode graphs hold the head's form: capture them again (each in
+    // its own mode: capture() records the current `sampling` choice)
+    const bool sampling = m->sampling;
+    int rc = MXH_OK;
+    if (m->g_decode) {
+        (void)hipGraphExecDestroy(m->g_decode);
+        m->g_decode = nullptr;
+        m->sampling = false;
+        rc = capture(m, true, &m->g_decode);
+    }
+    if (!rc && m->g_sample) {
+        (void)hipGraphExecDestroy(m->g_sample);
+        m->g_sample = nullptr;
+        m->sampling = true;
+        rc = capture(m, true, &m->g_sample);
+    }
+    m->sampling = sampling;
+    return rc;
 }
 
 int mxh_model_prefill(mxh_model* m, const int* tokens, int n) {

@@ -194,4 +194,73 @@ int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint
     return MXH_OK;
 }
 
+// ---- logit edits before the choice (minxfmr.cpp:2047-2089) ---------------
+
+namespace {
+
+__device__ __forceinline__ bool edits_active(const EditParams* prm) {
+    return prm->repeat_penalty != 1.0 || prm->frequency_penalty != 0.0 || prm->presence_penalty != 0.0;
+}
+
+// the penalty window: the last last_n ids of tokens[0 .. pos] (all when
+// last_n < 0), as [*h0, *h1)
+__device__ __forceinline__ void edit_window(const EditParams* prm, int pos, int* h0, int* h1) {
+    const int len = pos + 1;
+    int n = prm->last_n < 0 ? len : prm->last_n;
+    if (n > len) n = len;
+    *h0 = len - n;
+    *h1 = len;
+}
+
+// suppressed ids to -inf; occurrences of each id in the window counted
+__global__ void logit_count_kernel(float* __restrict__ logits, int n_vocab, const int* __restrict__ tokens,
+                                   const int* __restrict__ pos_p, const EditParams* __restrict__ prm,
+                                   const int* __restrict__ suppress, int* __restrict__ cnt) {
+    const int tid = blockIdx.x * blockDim.x + threadIdx.x, nthr = gridDim.x * blockDim.x;
+    for (int j = tid; j < prm->n_suppress; j += nthr) {
+        const int id = suppress[j];
+        if (id >= 0 && id < n_vocab) logits[id] = -INFINITY;
+    }
+    if (!edits_active(prm)) return;
+    int h0, h1;
+    edit_window(prm, *pos_p, &h0, &h1);
+    for (int i = h0 + tid; i < h1; i += nthr) {
+        const int t = tokens[i];
+        if (t >= 0 && t < n_vocab) atomicAdd(cnt + t, 1);
+    }
+}
+
+// each distinct id of the window (the one occurrence whose exchange returns
+// its count) gets the reference's penalty, computed in double; the counts go
+// back to zero for the next step
+__global__ void logit_penalty_kernel(float* __restrict__ logits, int n_vocab, const int* __restrict__ tokens,
+                                     const int* __restrict__ pos_p, const EditParams* __restrict__ prm,
+                                     int* __restrict__ cnt) {
+    if (!edits_active(prm)) return;
+    const int tid = blockIdx.x * blockDim.x + threadIdx.x, nthr = gridDim.x * blockDim.x;
+    int h0, h1;
+    edit_window(prm, *pos_p, &h0, &h1);
+    for (int i = h0 + tid; i < h1; i += nthr) {
+        const int t = tokens[i];
+        if (t < 0 || t >= n_vocab) continue;
+        const int c = atomicExch(cnt + t, 0);
+        if (c <= 0) continue;
+        double l = (double)logits[t];
+        if (prm->repeat_penalty != 1.0) l = l <= 0.0 ? l * prm->repeat_penalty : l / prm->repeat_penalty;
+        l -= (double)c * prm->frequency_penalty + prm->presence_penalty;
+        logits[t] = (float)l;
+    }
+}
+
+}  // namespace
+
+int logit_edits_launch(float* logits, int n_vocab, const int* tokens, const int* pos, const EditParams* prm,
+                       const int* suppress, int* cnt, hipStream_t st) {
+    if (n_vocab <= 0) return MXH_ERR_ARG;
+    hipLaunchKernelGGL(logit_count_kernel, dim3(64), dim3(256), 0, st, logits, n_vocab, tokens, pos, prm, suppress,
+                       cnt);
+    hipLaunchKernelGGL(logit_penalty_kernel, dim3(64), dim3(256), 0, st, logits, n_vocab, tokens, pos, prm, cnt);
+    return MXH_OK;
+}
+
 }  // namespace mxh

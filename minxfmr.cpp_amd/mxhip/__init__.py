@@ -98,6 +98,7 @@ def _load() -> C.CDLL:
         "mxh_model_step": (ip, [vp, ip, vp, vp]),
         "mxh_model_prefill": (ip, [vp, vp, ip]),
         "mxh_model_set_sampling": (ip, [vp, ip, C.c_double, C.c_double, C.c_double, C.c_uint64]),
+        "mxh_model_set_logit_edits": (ip, [vp, vp, ip, ip, C.c_double, C.c_double, C.c_double]),
         "mxh_sample": (ip, [vp, ip, ip, C.c_double, C.c_double, C.c_double, C.c_uint64, C.c_uint64, C.POINTER(C.c_int)]),
         "mxh_model_generate": (ip, [vp, vp, ip, ip, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mxh_model_close": (None, [vp]),
@@ -118,7 +119,7 @@ EXPORTED = (
     "mxh_download mxh_memset mxh_copy mxh_gemm_q_bf16 mxh_gemm_q_f16 mxh_gemm_q_f16_noalloc mxh_attention_prefill mxh_tile_rows mxh_timer_begin mxh_timer_end mxh_gemv mxh_matmul_rhs_t mxh_dequant mxh_preload "
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matmul_q mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
-    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_sample mxh_model_generate mxh_model_close "
+    "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_model_set_logit_edits mxh_sample mxh_model_generate mxh_model_close "
     "mxh_write_synthetic_gguf mxh_model_decode mxh_model_bench_gemv"
 ).split()
 
@@ -298,6 +299,13 @@ class Model:
     def set_sampling(self, top_k: int, temperature: float, top_p: float = 1.0, min_p: float = 0.0, seed: int = 0):
         """Top-k / temperature sampling on the device (temperature <= 0: greedy)."""
         check(lib.mxh_model_set_sampling(self.h, top_k, temperature, top_p, min_p, seed), "set_sampling")
+
+    def set_logit_edits(self, suppress=(), repeat_last_n: int = 64, repeat_penalty: float = 1.0,
+                        frequency_penalty: float = 0.0, presence_penalty: float = 0.0):
+        """Suppressed ids and repetition / frequency / presence penalties applied before each choice."""
+        ids = np.ascontiguousarray(suppress, np.int32)
+        check(lib.mxh_model_set_logit_edits(self.h, ptr(ids) if ids.size else None, ids.size, repeat_last_n,
+                                            repeat_penalty, frequency_penalty, presence_penalty), "set_logit_edits")
 
     def prefill(self, tokens) -> None:
         """Feed prompt ids at the current position (no logits)."""

@@ -585,6 +585,38 @@ int mxo_sample(const float *logits, size_t n, int top_k, double temperature, dou
     return pick;
 }
 
+/* minxfmr.cpp:2047-2089: suppressed ids to -inf, then the llama.cpp-style
+ * penalties over the last repeat_last_n history ids (all when < 0), each
+ * distinct id once with its count, in double.  The reference's logits are
+ * doubles; here the edited value is rounded back to the float logits. */
+void mxo_logit_edits(float *logits, size_t n, const int *history, size_t n_hist, const int *suppress,
+                     size_t n_suppress, int repeat_last_n, double repeat_penalty, double frequency_penalty,
+                     double presence_penalty)
+{
+    for (size_t j = 0; j < n_suppress; ++j)
+        if (suppress[j] >= 0 && (size_t)suppress[j] < n) logits[suppress[j]] = -INFINITY;
+    size_t pn = repeat_last_n < 0 ? n_hist : (size_t)repeat_last_n;
+    if (pn > n_hist) pn = n_hist;
+    if (pn == 0 || (repeat_penalty == 1.0 && frequency_penalty == 0.0 && presence_penalty == 0.0)) return;
+    const int *win = history + (n_hist - pn);
+    for (size_t i = 0; i < pn; ++i) {
+        const int t = win[i];
+        if (t < 0 || (size_t)t >= n) continue;
+        int first = 1, count = 0;
+        for (size_t j = 0; j < pn; ++j) {
+            if (win[j] == t) {
+                if (j < i) first = 0;
+                ++count;
+            }
+        }
+        if (!first) continue;
+        double l = (double)logits[t];
+        if (repeat_penalty != 1.0) l = l <= 0.0 ? l * repeat_penalty : l / repeat_penalty;
+        l -= (double)count * frequency_penalty + (count > 0 ? presence_penalty : 0.0);
+        logits[t] = (float)l;
+    }
+}
+
 /* ------------------------------------------------------------------ */
 /* GGUF reader (gguf_reader.cpp:224-676 semantics, exact names)        */
 /* ------------------------------------------------------------------ */

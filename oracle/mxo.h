@@ -130,6 +130,13 @@ int mxo_sample(const float *logits, size_t n, int top_k, double temperature, dou
                double min_p, uint64_t *rng_state);
 double mxo_rng_uniform(uint64_t *state);
 
+/* Logit edits before the choice (minxfmr.cpp:2047-2089): suppressed ids to
+ * -inf, then repetition / frequency / presence penalties over the last
+ * repeat_last_n ids of history (all when < 0). */
+void mxo_logit_edits(float *logits, size_t n, const int *history, size_t n_hist, const int *suppress,
+                     size_t n_suppress, int repeat_last_n, double repeat_penalty, double frequency_penalty,
+                     double presence_penalty);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,7 @@ def _load():
         "mxo_model_pos": (ip, [vp]),
         "mxo_argmax": (ip, [vp, sz]),
         "mxo_sample": (ip, [vp, sz, ip, C.c_double, C.c_double, C.c_double, C.POINTER(C.c_uint64)]),
+        "mxo_logit_edits": (None, [vp, sz, vp, sz, vp, sz, ip, C.c_double, C.c_double, C.c_double]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -139,6 +140,17 @@ def sample(logits: np.ndarray, top_k: int, temperature: float, top_p: float, min
     logits = np.ascontiguousarray(logits, np.float32)
     tok = lib.mxo_sample(_p(logits), logits.size, top_k, temperature, top_p, min_p, C.byref(st))
     return tok, st.value
+
+
+def logit_edits(logits: np.ndarray, history, suppress=(), repeat_last_n: int = 64, repeat_penalty: float = 1.0,
+                frequency_penalty: float = 0.0, presence_penalty: float = 0.0) -> np.ndarray:
+    """The reference's logit edits (minxfmr.cpp:2047-2089) on a copy of logits."""
+    out = np.array(logits, np.float32, copy=True)
+    h = np.ascontiguousarray(history, np.int32)
+    s = np.ascontiguousarray(suppress, np.int32)
+    lib.mxo_logit_edits(_p(out), out.size, _p(h) if h.size else None, h.size, _p(s) if s.size else None, s.size,
+                        repeat_last_n, repeat_penalty, frequency_penalty, presence_penalty)
+    return out
 
 
 class Model:

@@ -1,6 +1,7 @@
-"""Independent pins of the oracle's two functions the reference does not have
-the code to check: Qwen3 QK-norm placement in the model step, and the top-p /
-min-p cuts of the sampler (CPU only).
+"""Independent pins of oracle functions that neither the reference's tests
+nor its compiled code check: Qwen3 QK-norm placement in the model step, the
+top-p / min-p cuts of the sampler, and the logit edits before the choice
+(CPU only).
 
 QK-norm.  The reference layer goes projection -> bias -> RoPE
 (src/transformer/transformer.cpp:406-514) and never loads attn_{q,k}_norm.
@@ -19,6 +20,12 @@ then the top-p prefix (first i with cumulative p >= top_p) renormalised,
 then the min-p prefix (p >= min_p * p_max) renormalised, then a draw.  With
 logits log(p) for chosen p the kept set and its probabilities are known in
 closed form; no draw may leave the set and 20k-draw frequencies must match.
+
+Logit edits.  minxfmr.cpp:2047-2089: suppressed ids to -inf, then per
+distinct id of the last N history ids (count c):
+l <- (l <= 0 ? l * rp : l / rp) - c * fp - presence.  Checked on values
+worked by hand, including the window, the zero-logit branch and the
+neutral / empty-window cases.
 """
 from __future__ import annotations
 
@@ -182,3 +189,30 @@ def test_sampler_top_p_min_p_closed_form(params, probs):
     assert set(got.tolist()) <= set(kept.tolist()), set(got.tolist()) - set(kept.tolist())
     freq = np.array([(got == i).mean() for i in kept])
     np.testing.assert_allclose(freq, probs, atol=0.015)
+
+
+# ---- logit edits before the choice (minxfmr.cpp:2047-2089) -------------------
+
+def test_logit_edits_closed_form():
+    """Values worked by hand from the reference's formula:
+    l <- (l <= 0 ? l * rp : l / rp) - count * fp - presence, once per distinct
+    id of the last N history ids; suppressed ids to -inf."""
+    lg = np.array([2.0, -1.0, 0.5, 3.0, 1.0], np.float32)
+    hist = [0, 0, 1, 3]
+    got = mxo.logit_edits(lg, hist, (), -1, 2.0, 0.5, 1.0)
+    # id 0 twice: 2/2 - 1 - 1; id 1 once: -1*2 - 0.5 - 1; id 3 once: 3/2 - 0.5 - 1
+    np.testing.assert_array_equal(got, np.array([-1.0, -3.5, 0.5, 0.0, 1.0], np.float32))
+    # window of the last two ids: 1 and 3 only
+    got = mxo.logit_edits(lg, hist, (), 2, 2.0, 0.5, 1.0)
+    np.testing.assert_array_equal(got, np.array([2.0, -3.5, 0.5, 0.0, 1.0], np.float32))
+    # suppression, and a zero logit takes the multiplying branch
+    z = np.array([0.0, 1.0, 1.0], np.float32)
+    got = mxo.logit_edits(z, [0, 0], [2], -1, 3.0, 0.25, 0.0)
+    np.testing.assert_array_equal(got, np.array([-0.5, 1.0, -np.inf], np.float32))
+    # neutral penalties change nothing, repeat alone divides / multiplies
+    np.testing.assert_array_equal(mxo.logit_edits(lg, hist, (), -1, 1.0, 0.0, 0.0), lg)
+    got = mxo.logit_edits(lg, hist, (), -1, 1.5, 0.0, 0.0)
+    np.testing.assert_allclose(got, [2.0 / 1.5, -1.5, 0.5, 2.0, 1.0], rtol=1e-7)
+    # an empty window (N = 0) skips the penalty pass but not suppression
+    got = mxo.logit_edits(lg, hist, [1], 0, 2.0, 0.5, 1.0)
+    np.testing.assert_array_equal(got, np.array([2.0, -np.inf, 0.5, 3.0, 1.0], np.float32))

@@ -82,3 +82,52 @@ def test_model_sampling_matches_oracle(mxh, tmp_path, name):
     assert np.array_equal(g1, g2)
     for m in (gm, em):
         m.close()
+
+
+@pytest.mark.parametrize("sampled", [False, True], ids=["greedy", "topk8"])
+def test_model_logit_edits_match_oracle(mxh, tmp_path, sampled):
+    """The reference's logit edits before each choice (minxfmr.cpp:2047-2089):
+    three suppressed ids and repetition 1.3 / frequency 0.3 / presence 0.2
+    penalties over the last 16 ids of the history (prompt included).  Greedy
+    and seeded top-k 8 ids equal the oracle's with the same edits; graph
+    replay equals eager launches; neutral settings restore the plain ids."""
+    p = build(tmp_path, "q4k-qknorm")
+    prompt = np.random.default_rng(21).integers(0, TINY["n_vocab"], 16).astype(np.int32)
+    n_gen, seed = 40, 777
+    plain = mxhip.Model(p, 128)
+    base, _, _ = plain.generate(prompt, n_gen)
+    sup = [int(base[1]), int(base[3]), 5]
+    edits = dict(suppress=sup, repeat_last_n=16, repeat_penalty=1.3, frequency_penalty=0.3, presence_penalty=0.2)
+    runs = []
+    for flags in (0, mxhip.MODEL_NO_GRAPH):
+        gm = mxhip.Model(p, 128, flags)
+        if sampled:
+            gm.set_sampling(8, 0.8, seed=seed)
+        gm.set_logit_edits(**edits)
+        ids, _, _ = gm.generate(prompt, n_gen)
+        runs.append(ids)
+        gm.close()
+    assert np.array_equal(runs[0], runs[1])
+    om = mxo.Model(p, 128)
+    hist = prompt.tolist()
+    lg = None
+    for t in prompt:
+        lg, _ = om.step(int(t))
+    want, state = [], seed
+    for _ in range(n_gen):
+        e = mxo.logit_edits(lg, hist, sup, edits["repeat_last_n"], edits["repeat_penalty"],
+                            edits["frequency_penalty"], edits["presence_penalty"])
+        if sampled:
+            nxt, state = mxo.sample(e, 8, 0.8, 1.0, 0.0, state)
+        else:
+            nxt = int(np.argmax(e))
+        want.append(nxt)
+        hist.append(nxt)
+        lg, _ = om.step(nxt)
+    assert runs[0].tolist() == want
+    assert not set(sup) & set(runs[0].tolist())
+    # neutral settings give back the fused greedy head
+    plain.set_logit_edits()
+    again, _, _ = plain.generate(prompt, n_gen)
+    assert np.array_equal(again, base)
+    plain.close()
