@@ -35,6 +35,7 @@
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "mxh_device.h"
 #include "mxh_internal.h"
@@ -772,6 +773,14 @@ __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ 
 //               (transformer.cpp:183-185, 696-704) for i < F
 //  GEMV_ARGMAX: y = logits; each workgroup also leaves its (largest logit,
 //               lowest index) in red_val/red_idx[blockIdx] for argmax_finish
+// f(integral_constant<int, K>) for K = 0 .. N-1, expanded at compile time
+// (a plain unrolled loop over a register array may be left rolled, which
+// sends the array to scratch memory)
+template <class F, int... K>
+__device__ __forceinline__ void for_each_k(F&& f, std::integer_sequence<int, K...>) {
+    (f(std::integral_constant<int, K>{}), ...);
+}
+
 // Consume steps K .. NS-1 of the short form: step K waits until only the
 // (NS - 1 - K) later steps' loads may be outstanding.
 template <int K, int NS, int KL, class F>
@@ -849,7 +858,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     // bounds), so the explicit waits below can count them
     // A step past the wave's last one repeats the last step's addresses (its
     // loads hit lines already in flight and its data is never consumed).
-    auto issue = [&](Cursor& cu, Step& st) {
+    // both lambdas are inlined at every use: a call would put the state they
+    // capture by reference (kernel arguments, cursors, buffers) in scratch
+    auto issue = [&](Cursor& cu, Step& st) __attribute__((always_inline)) {
         const bool past = cu.g >= my_groups;
         const int gi = past ? my_groups - 1 : cu.g, ji = past ? cpl - 1 : cu.j;
         const int grp = wave_id + gi * n_waves;
@@ -870,7 +881,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             ++cu.g;
         }
     };
-    auto consume = [&](Cursor& cu, const Step& st) {
+    auto consume = [&](Cursor& cu, const Step& st) __attribute__((always_inline)) {
         const int c = lane + 64 * cu.j;
         if (c < nchunks) Ty::compute(st.b, c, xview, a.form, acc);
         if (cu.j == cpl - 1) {
@@ -921,8 +932,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             // so x is not queued behind weights in the CU's memory pipeline
             // (a bare s_barrier: no wait for the loads themselves)
             __builtin_amdgcn_s_barrier();
-#pragma unroll
-            for (int k = 0; k < NS; ++k) issue(ci, sb[k]);
+            for_each_k([&](auto kc) { issue(ci, sb[decltype(kc)::value]); }, std::make_integer_sequence<int, NS>{});
             wait_vmcnt<NS * kL>();
         };
         if constexpr (Ty::kIntX) {

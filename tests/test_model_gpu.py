@@ -133,9 +133,9 @@ def test_step_errors_are_reported(mxh, tmp_path):
         mxhip.Model(tmp_path / "missing.gguf", 16)
 
 
-# BASELINE config 1 seeds: (model weights, prompt).  The first is the seed
-# the round-one test used; with it the oracle's smallest top-2 margin over the
-# 64 steps is 8.5e-5 (step 40).
+# BASELINE config 1 seeds: (model weights, prompt).  With the first, the
+# oracle's smallest top-2 margin over the 64 steps is 8.5e-5 (step 40): a
+# near-tie that an error of 1e-4 in the logits would flip.
 CONFIG1_SEEDS = [(0x0C0F1, 0xC0F1), (0x1001, 0x2001), (0x1002, 0x2002), (0x1003, 0x2003), (0x1004, 0x2004)]
 
 
