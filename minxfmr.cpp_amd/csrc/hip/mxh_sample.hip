@@ -5,7 +5,8 @@
 // 64-bit keys: order-preserving bits of the logit above the complemented id,
 // so ties go to the lower id, as the reference's partial_sort with `>` and an
 // increasing initial order) and keeps its best kk = pow2(top_k) candidates.
-// Pass 2: one workgroup sorts the W * kk candidates the same way, then thread
+// Pass 2: one workgroup sorts the lists of the top_k groups with the largest
+// maxima (they hold every candidate that can rank in the top k), then thread
 // 0 forms the probabilities in double exactly as the reference does (exp of
 // (l - max) / T, normalise, top-p cut and renormalise, min-p cut and
 // renormalise) and draws.  The uniform of draw d is splitmix64 at state
@@ -22,6 +23,7 @@ namespace {
 
 constexpr int kSortMax = 4096;  // keys one workgroup sorts in LDS
 constexpr int kTopKMax = 64;
+constexpr int kMaxGroups = 2048;  // pass-1 lists one pass-2 workgroup ranks
 
 __device__ __forceinline__ uint64_t sort_key(float v, int idx) {
     uint32_t u = __float_as_uint(v);
@@ -82,30 +84,49 @@ __device__ __forceinline__ double draw_uniform(uint64_t seed, uint64_t d) {
 // Candidates -> token.  The token goes to out[0] or, with tokens/pos, to
 // tokens[*pos + 1] with the position advanced (the decode loop on device);
 // the draw counter advances either way.
+//
+// Each group's list is sorted, so its first key is the group's maximum.  The
+// k-th largest group maximum T bounds the k-th largest key from below (k
+// group maxima reach it), and only the k groups whose maximum reaches T can
+// hold keys >= T: their lists are the only ones sorted.  Keys are distinct
+// (they carry the id), so the order is the full sort's.
 __global__ __launch_bounds__(1024) void topk_pass2_kernel(const float* __restrict__ logits, const uint64_t* cand,
-                                                          int ncand, SampleParams* prm, int* out, int* tokens,
-                                                          int* pos) {
+                                                          int groups, int kk, SampleParams* prm, int* out,
+                                                          int* tokens, int* pos) {
     __shared__ uint64_t s[kSortMax];
-    const int p = pow2_at_least(ncand);
-    for (int i = threadIdx.x; i < p; i += blockDim.x) s[i] = i < ncand ? cand[i] : 0ull;
+    __shared__ uint64_t gmax[kMaxGroups];
+    __shared__ double pr[kTopKMax];
+    const int k = prm->top_k;
+    for (int j = threadIdx.x; j < groups; j += blockDim.x) gmax[j] = cand[(size_t)j * kk];
+    __syncthreads();
+    const int sel = groups < k ? groups : k;  // groups taken
+    for (int j = threadIdx.x; j < groups; j += blockDim.x) {
+        const uint64_t v = gmax[j];
+        int rank = 0;
+        for (int i = 0; i < groups; ++i) rank += gmax[i] > v;
+        if (rank < sel)
+            for (int i = 0; i < kk; ++i) s[rank * kk + i] = cand[(size_t)j * kk + i];
+    }
+    const int p = pow2_at_least(sel * kk);
+    for (int i = sel * kk + threadIdx.x; i < p; i += blockDim.x) s[i] = 0ull;
     __syncthreads();
     bitonic_desc(s, p);
-    if (threadIdx.x != 0) return;
-    const int k = prm->top_k;
     const double temperature = prm->temperature;
+    if (temperature > 0.0 && threadIdx.x < k) {
+        // the k unnormalised probabilities, each exp as the reference forms it
+        const double mx = logits[key_id(s[0])];
+        pr[threadIdx.x] = exp(((double)logits[key_id(s[threadIdx.x])] - mx) / temperature);
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
     double top_p = prm->top_p, min_p = prm->min_p;
     int pick = key_id(s[0]);
     if (temperature > 0.0) {
         if (top_p <= 0.0 || top_p > 1.0) top_p = 1.0;
         if (min_p < 0.0) min_p = 0.0;
         if (min_p > 1.0) min_p = 1.0;
-        double pr[kTopKMax];
-        const double mx = logits[key_id(s[0])];
         double sum = 0.0;
-        for (int i = 0; i < k; ++i) {
-            pr[i] = exp(((double)logits[key_id(s[i])] - mx) / temperature);
-            sum += pr[i];
-        }
+        for (int i = 0; i < k; ++i) sum += pr[i];
         if (sum > 0.0) {
             for (int i = 0; i < k; ++i) pr[i] /= sum;
             int m = k;
@@ -188,9 +209,9 @@ int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint
     if (n <= 0 || top_k < 1 || top_k > kTopKMax || top_k > n) return MXH_ERR_ARG;
     int g, sl, kk;
     sample_shape(n, top_k, &g, &sl, &kk);
-    if ((size_t)g * kk > (size_t)kSortMax) return MXH_ERR_UNSUPPORTED;
+    if ((size_t)g * kk > (size_t)kSortMax || g > kMaxGroups) return MXH_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(topk_pass1_kernel, dim3(g), dim3(1024), 0, st, logits, n, sl, kk, cand);
-    hipLaunchKernelGGL(topk_pass2_kernel, dim3(1), dim3(1024), 0, st, logits, cand, g * kk, prm, out, tokens, pos);
+    hipLaunchKernelGGL(topk_pass2_kernel, dim3(1), dim3(1024), 0, st, logits, cand, g, kk, prm, out, tokens, pos);
     return MXH_OK;
 }
 

@@ -37,6 +37,26 @@ def test_sample_matches_oracle_on_fixed_logits(mxh, n, k, t, p, mp):
     buf.close()
 
 
+@pytest.mark.parametrize("k,t,p,mp", [(8, 0.8, 1.0, 0.0), (64, 1.0, 1.0, 0.1), (40, 0.7, 0.95, 0.05)])
+def test_sample_top_values_in_one_slice(mxh, k, t, p, mp):
+    """The largest logits sit at consecutive ids, inside one first-pass
+    slice (and straddling the next): the second pass must still see all of
+    them, whichever lists it keeps."""
+    n = 151936
+    rng = np.random.default_rng(k)
+    logits = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    logits[1000:1000 + 2 * k] = np.linspace(6.0, 5.0, 2 * k, dtype=np.float32)
+    logits[1000 + 3] = logits[1000 + 5]  # a tie inside the cluster: the lower id first
+    buf = mxhip.DeviceBuffer.from_array(logits)
+    seed = 0xC1A5 + k
+    state = seed
+    for d in range(40):
+        want, state = mxo.sample(logits, k, t, p, mp, state)
+        got = mxhip.sample(buf, n, k, t, p, mp, seed, d)
+        assert got == want, f"draw {d}: device {got}, oracle {want}"
+    buf.close()
+
+
 def test_sample_rejects_bad_top_k(mxh):
     buf = mxhip.DeviceBuffer.from_array(np.zeros(10, np.float32))
     for k in (0, 65, 11):
