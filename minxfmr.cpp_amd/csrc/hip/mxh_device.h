@@ -54,6 +54,21 @@ __device__ __forceinline__ void k4_scale_min(uint32_t s0, uint32_t s1, uint32_t 
     }
 }
 
+// 6-bit (scale, min) of sub-blocks 2g and 2g+1 as byte pairs, without
+// branches (tensor.cpp:395-403 reference form; ggml form for form != 0)
+__device__ __forceinline__ void k4_pair(uint32_t s0, uint32_t s1, uint32_t s2, int g, int form, uint32_t& sc,
+                                        uint32_t& mn) {
+    const int sh = (g & 1) * 16;
+    const uint32_t A = s0 >> sh, B = s1 >> sh, C = s2 >> sh;
+    if (g >= 2) {
+        sc = (C & 0x0f0fu) | (((form ? A : B) >> 2) & 0x3030u);
+        mn = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
+    } else {
+        sc = A & 0x3f3fu;
+        mn = B & 0x3f3fu;
+    }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

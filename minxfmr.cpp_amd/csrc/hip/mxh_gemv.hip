@@ -218,21 +218,6 @@ __device__ __forceinline__ float dot16(const XP& x, uint32_t q0, uint32_t q1, ui
     return limb_total(a);
 }
 
-// 6-bit (scale, min) of sub-blocks 2g and 2g+1 as byte pairs, without
-// branches (tensor.cpp:395-403 reference form; ggml form for form != 0)
-__device__ __forceinline__ void k4_pair(uint32_t s0, uint32_t s1, uint32_t s2, int g, int form, uint32_t& sc,
-                                        uint32_t& mn) {
-    const int sh = (g & 1) * 16;
-    const uint32_t A = s0 >> sh, B = s1 >> sh, C = s2 >> sh;
-    if (g >= 2) {
-        sc = (C & 0x0f0fu) | (((form ? A : B) >> 2) & 0x3030u);
-        mn = ((C >> 4) & 0x0f0fu) | ((B >> 2) & 0x3030u);
-    } else {
-        sc = A & 0x3f3fu;
-        mn = B & 0x3f3fu;
-    }
-}
-
 __device__ __forceinline__ float2 h2f2(uint32_t v) {
     __half2 h;
     __builtin_memcpy(&h, &v, 4);

@@ -465,6 +465,293 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q_f16_kernel(c
 
 #undef MXH_Q4F16_FETCH
 
+// ---- Q4_K on a direct-to-LDS pipeline ------------------------------------
+//
+// The same product as gemm_q_f16_kernel for Q4_K rows (GGUF or tiled order),
+// organised around the matrix cores: global memory goes straight into LDS
+// (global_load_lds_dwordx4, no registers, no conversion), three K steps in
+// flight, one barrier per step, and each wave decodes the weight rows it
+// multiplies from their raw bytes in LDS into MFMA operands itself.
+//
+// Tile 128 activation rows x 128 weight rows per workgroup of 8 waves (2 x 4,
+// 64 x 32 each, two per SIMD), one workgroup per CU.  Per stage (one 64-element K step):
+//   activations hi and lo, [row][8 x 16 bytes], 16-byte chunk c of row r at
+//   c ^ swz(r) (conflict-free MFMA operand reads),
+//   raw weight bytes, [row][header, first 16 qs bytes, last 16 qs bytes].
+// K order inside a step: the MFMA's 16-element slices are taken so that the
+// lane holding weight row n, half h, reads one 16-byte qs piece: slice jj of
+// half h covers elements 8 ((jj & 1) + 2 h + 4 (jj >> 1)) .. + 7 of the step
+// (low nibbles of bytes 8 (jj & 1) .. of piece h for jj < 2, high nibbles for
+// jj >= 2), and the activation operand reads the same elements.
+// Sub-block sums S (for the min terms) come in a ring of 16 sub-blocks per
+// round of 8 steps, double-buffered; the -dmin m_j values of a round are
+// written to a second ring by the decoding waves; the correction MFMAs of a
+// round run at the top of the step after it.
+namespace q4p {
+constexpr int BM = 128, BN = 128, BK = 64, NST = 3;
+constexpr int kStageA = 2 * BM * 128;             // hi + lo
+constexpr int kStageW = 512 * 16;                 // 384 chunks used, 128 padding
+constexpr int kStage = kStageA + kStageW;
+constexpr int kRingB4 = 2 * BM * 16 * 2;            // [limb][row][16 slots] fp16
+constexpr size_t kLds = (size_t)NST * kStage + 4 * (size_t)kRingB4;
+constexpr int kLoadsStep = 4 + 1;                 // per wave: activation + weight chunks
+}  // namespace q4p
+
+__device__ __forceinline__ int q4p_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+// 16 bytes per lane from global memory straight into LDS: lane i writes
+// lds_wave_base + 16 i.  Issued as inline assembly so that the compiler does
+// not wait for every such load before the next LDS read (it cannot tell the
+// stages apart); the pipeline waits for them itself (wait_vm).
+__device__ __forceinline__ void g2l16(const void* g, uint8_t* lds_wave_base) {
+    const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds_wave_base;
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(l) : "memory");
+}
+
+// Workgroup barrier for the pipeline: LDS writes of this wave complete, then
+// s_barrier, with no wait for outstanding global loads (__syncthreads' fence
+// would drain the loads of the steps in flight).  The direct-to-LDS loads of
+// a stage are waited for with wait_vm before it.
+__device__ __forceinline__ void q4p_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    // vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+// fp16 pairs of (4 nibble bytes in n, selected by the perm) x sc, exact:
+// bytes q0, q1 become fp16 1024 + q (high byte 0x64), then
+// (1024 + q) sc - 1024 sc in one fused fp16 operation
+__device__ __forceinline__ uint32_t q4p_pair(uint32_t n, uint32_t sel, h2v scv, h2v offv) {
+    const uint32_t b = __builtin_amdgcn_perm(0x64u, n, sel);
+    const h2v r = __builtin_elementwise_fma(__builtin_bit_cast(h2v, b), scv, offv);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// eight weights (bytes 0-3 and 4-7 of (lo, hi), nibble at `shift`) as fp16
+// integers times sc
+__device__ __forceinline__ f16x8 q4p_slice(uint32_t w0, uint32_t w1, int shift, h2v scv, h2v offv) {
+    const uint32_t n0 = (w0 >> shift) & 0x0f0f0f0fu, n1 = (w1 >> shift) & 0x0f0f0f0fu;
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const u4v r = {q4p_pair(n0, 0x04010400u, scv, offv), q4p_pair(n0, 0x04030402u, scv, offv),
+                   q4p_pair(n1, 0x04010400u, scv, offv), q4p_pair(n1, 0x04030402u, scv, offv)};
+    return __builtin_bit_cast(f16x8, r);
+}
+
+template <bool TILED>
+__global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* __restrict__ a_hi,
+                                                               const uint16_t* __restrict__ a_lo, int lda,
+                                                               const uint16_t* __restrict__ s_hi,
+                                                               const uint16_t* __restrict__ s_lo, int lds,
+                                                               const float* __restrict__ rscale,
+                                                               const uint8_t* __restrict__ w, float* out, int ldo,
+                                                               const float* res, int m, int n, int k, int form,
+                                                               int ksteps, float* __restrict__ part) {
+    using namespace q4p;
+    extern __shared__ __align__(16) uint8_t smem8[];
+    uint8_t* ringS = smem8 + (size_t)NST * kStage;  // [2][kRingB4]
+    uint8_t* ringB = ringS + 2 * kRingB4;            // [2][kRingB4]
+
+    // work item as in gemm_q_f16_kernel (XCD-contiguous ranges)
+    const int tn = (n + BN - 1) / BN, tm = (m + BM - 1) / BM, splits = (k / BK + ksteps - 1) / ksteps;
+    const int total = tn * tm * splits, per = (int)gridDim.x / 8;
+    const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (wi >= total) return;
+    const int tx = wi % tn, ty = (wi / tn) % tm, tz = wi / (tn * tm);
+    // 8 waves: 2 along the activation rows (64 each) x 4 along the weight rows (32 each)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wr = wave >> 2, wc = wave & 3;
+    const int m0 = ty * BM, n0 = tx * BN;
+    const int kb = tz * ksteps * BK, ke = min(k, kb + ksteps * BK);
+    const int nsteps = (ke - kb) / BK;
+    const size_t rb = (size_t)(k / 256) * 144;
+    const int64_t nblk = k / 256;
+    const int lr = lane & 31, hh = lane >> 5;
+
+    // ---- global -> LDS load roles (fixed per lane; the step adds k0) ----
+    // activations: load u of this wave fills LDS chunks (4 wave + u) * 64 + lane
+    const uint16_t* aptr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int slot = (wave * 4 + u) * 64 + lane, limb = slot >> 10, P = slot & 1023;
+        const int row = P >> 3, c = (P & 7) ^ q4p_swz(row);
+        const int grow = min(m0 + row, m - 1);
+        aptr[u] = (limb ? a_lo : a_hi) + (size_t)grow * lda + 8 * c;
+    }
+    // weights: this wave's load fills raw chunk wave * 64 + lane (row Q / 3, part Q % 3)
+    int Qw = wave * 64 + lane;
+    if (Qw >= 384) Qw -= 384;  // padding lanes repeat a real chunk
+    const int wpart = Qw % 3;
+    const uint8_t* wrow = w + (size_t)min(n0 + Qw / 3, n - 1) * rb;
+    auto w_addr = [&](int step) -> const uint8_t* {
+        const int64_t c = (int64_t)(kb / BK + step);  // 64-element chunk of the row
+        if constexpr (TILED) {
+            const Q4KTileOffs o = q4k_tile_offsets(c, nblk);
+            return wrow + (wpart == 0 ? o.hd : wpart == 1 ? o.qa : o.qb);
+        } else {
+            const size_t blk = (size_t)(c >> 2) * 144;
+            return wrow + blk + (wpart == 0 ? 0 : 16 + 32 * (int)(c & 3) + 16 * (wpart - 1));
+        }
+    };
+    // sub-block sums: this wave's load fills ring chunk wave * 64 + lane
+    const int s_slot = wave * 64 + lane, s_half = s_slot & 1;
+    const uint16_t* sptr = ((s_slot >> 8) ? s_lo : s_hi) + (size_t)min(m0 + ((s_slot >> 1) & 127), m - 1) * lds +
+                           8 * s_half;
+    const int nsb = k / 32;
+    auto issue_stage = [&](int step) {
+        const int st = min(step, nsteps - 1);  // past the end: the last step again (never read)
+        uint8_t* base = smem8 + (size_t)(step % NST) * kStage;
+        const int k0 = kb + st * BK;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) g2l16(aptr[u] + k0, base + (wave * 4 + u) * 1024);
+        g2l16(w_addr(st), base + kStageA + wave * 1024);
+    };
+    auto issue_sums = [&](int round) {
+        int j0 = kb / 32 + 16 * round;
+        // chunks past the row (rounds beyond this work item) read sub-block 0
+        if (j0 + 8 * s_half >= nsb) j0 = -8 * s_half;
+        g2l16(sptr + j0, ringS + (size_t)(round & 1) * kRingB4 + wave * 1024);
+    };
+
+    f32x16 acc[2], P[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][e] = P[i][e] = 0.f;
+
+    // correction of round r over its first `used` sub-block slots:
+    // acc += S . (-dmin m) with S and -dmin m split hi / lo
+    const int col = wc * 32 + lr;  // this lane's weight row in the tile
+    auto correction = [&](int r, int used) {
+        const uint8_t* sb = ringS + (size_t)(r & 1) * kRingB4;
+        const uint8_t* bb = ringB + (size_t)(r & 1) * kRingB4;
+        f16x8 sh[2], sl[2];
+        f16x8 bh = *reinterpret_cast<const f16x8*>(bb + col * 32 + hh * 16);
+        f16x8 bl = *reinterpret_cast<const f16x8*>(bb + 4096 + col * 32 + hh * 16);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = wr * 64 + i * 32 + lr;
+            sh[i] = *reinterpret_cast<const f16x8*>(sb + row * 32 + hh * 16);
+            sl[i] = *reinterpret_cast<const f16x8*>(sb + 4096 + row * 32 + hh * 16);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (8 * hh + e >= used) {
+                bh[e] = bl[e] = (_Float16)0.f;
+                sh[0][e] = sl[0][e] = sh[1][e] = sl[1][e] = (_Float16)0.f;
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl[i], bh, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bl, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bh, acc[i], 0, 0, 0);
+        }
+    };
+
+    // prologue: round 0's sums, steps 0 and 1
+    issue_sums(0);
+    issue_stage(0);
+    issue_stage(1);
+
+    for (int t = 0; t < nsteps; ++t) {
+        // stage t complete: only the loads issued after it may be outstanding
+        if (t == 0 || ((t - 1) & 7) != 1) wait_vm<kLoadsStep>();
+        else wait_vm<kLoadsStep + 1>();
+        q4p_barrier();
+        if (t > 0 && (t & 7) == 0) correction((t >> 3) - 1, 16);
+        issue_stage(t + 2);
+        if ((t & 7) == 1) issue_sums((t >> 3) + 1);
+
+        const uint8_t* stg = smem8 + (size_t)(t % NST) * kStage;
+        const int k0 = kb + t * BK, g = (k0 >> 6) & 3;
+        // this lane's weight row: header and its 16-byte qs piece
+        f16x8 bw[4];
+        float dcol;
+        {
+            const uint4 hd = *reinterpret_cast<const uint4*>(stg + kStageA + col * 48);
+            const uint4 q = *reinterpret_cast<const uint4*>(stg + kStageA + col * 48 + 16 + 16 * hh);
+            uint32_t scp, mnp;
+            k4_pair(hd.y, hd.z, hd.w, g, form, scp, mnp);
+            // hardware conversion: d and dmin only scale sums (a NaN payload need not survive)
+            dcol = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xffffu)));
+            const float dmin = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16)));
+            const _Float16 sc0 = (_Float16)(float)(scp & 0xffu), sc1 = (_Float16)(float)(scp >> 8);
+            const h2v sv0 = {sc0, sc0}, sv1 = {sc1, sc1};
+            const h2v ov0 = {(_Float16)(-1024.f) * sc0, (_Float16)(-1024.f) * sc0};
+            const h2v ov1 = {(_Float16)(-1024.f) * sc1, (_Float16)(-1024.f) * sc1};
+            bw[0] = q4p_slice(q.x, q.y, 0, sv0, ov0);
+            bw[1] = q4p_slice(q.z, q.w, 0, sv0, ov0);
+            bw[2] = q4p_slice(q.x, q.y, 4, sv1, ov1);
+            bw[3] = q4p_slice(q.z, q.w, 4, sv1, ov1);
+            if (wr == 0) {
+                // -dmin m of sub-block 2g (lanes of half 0) or 2g + 1 (half 1)
+                const float mt = -(dmin * (float)(hh ? (mnp >> 8) : (mnp & 0xffu)));
+                const uint32_t sp = split_f16(mt);
+                uint16_t* bb = reinterpret_cast<uint16_t*>(ringB + (size_t)((t >> 3) & 1) * kRingB4);
+                const int slot = 2 * (t & 7) + hh;
+                bb[col * 16 + slot] = (uint16_t)sp;
+                bb[2048 + col * 16 + slot] = (uint16_t)(sp >> 16);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int c = (jj & 1) + 2 * hh + 4 * (jj >> 1);
+            f16x8 ah[2], al[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = wr * 64 + i * 32 + lr;
+                const int off = row * 128 + 16 * (c ^ q4p_swz(row));
+                ah[i] = *reinterpret_cast<const f16x8*>(stg + off);
+                al[i] = *reinterpret_cast<const f16x8*>(stg + BM * 128 + off);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                P[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[jj], P[i], 0, 0, 0);
+                P[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[jj], P[i], 0, 0, 0);
+            }
+        }
+        if (((k0 + BK) & 255) == 0 || t == nsteps - 1) {
+            // end of a super-block: acc += d[n] . P
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    acc[i][e] = fmaf(dcol, P[i][e], acc[i][e]);
+                    P[i][e] = 0.f;
+                }
+        }
+    }
+    wait_vm<0>();
+    q4p_barrier();
+    {
+        const int r = (nsteps - 1) >> 3;
+        correction(r, 2 * (nsteps - 8 * r));
+    }
+
+    const bool partial = splits > 1;
+    float* dst = partial ? part + (size_t)tz * m * n : out;
+    const int ld = partial ? n : ldo;
+    const int ocol = n0 + col;
+    if (ocol < n) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
+                if (row < m) {
+                    const size_t o = (size_t)row * ld + ocol;
+                    const float v = acc[i][e] * rscale[row];
+                    if (partial) dst[o] = v;
+                    else dst[o] = res ? v + res[o] : v;
+                }
+            }
+    }
+}
+
 __global__ void gemm_f16_reduce_kernel(const float* __restrict__ part, int splits, float* out, int ldo,
                                        const float* res, int m, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -661,6 +948,63 @@ int gemm_q_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const
     return MXH_OK;
 }
 
+// Split K for the pipelined kernel (one workgroup per CU): the fewest splits
+// (1, 2, 4 or 8, whole super-blocks, within the partial buffer) that minimise
+// rounds x steps per work item.
+int q4p_splits(int tiles, int steps, int n_cu, size_t mn, size_t part_floats) {
+    int best = 1;
+    long best_cost = -1;
+    for (int s = 1; s <= 8; s *= 2) {
+        if (steps % (4 * s)) break;
+        if (s > 1 && (size_t)s * mn > part_floats) break;
+        const long rounds = ((long)tiles * s + n_cu - 1) / n_cu;
+        const long cost = rounds * (steps / s);
+        if (best_cost < 0 || cost < best_cost) {
+            best = s;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+template <bool TILED>
+int gemm_q4k_pipe_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
+                         const uint16_t* s_lo, int lds, const float* rscale, const uint8_t* w, float* out, int ldo,
+                         const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
+                         hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*)gemm_q4k_pipe_kernel<TILED>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)q4p::kLds) != hipSuccess)
+            return MXH_ERR_HIP;
+        attr_set = true;
+    }
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n_cu = 256;
+    }
+    const int tn = (n + q4p::BN - 1) / q4p::BN, tm = (m + q4p::BM - 1) / q4p::BM, steps = k / q4p::BK;
+    const int splits = q4p_splits(tn * tm, steps, n_cu, (size_t)m * n, part ? part_floats : 0);
+    const int items = tn * tm * splits;
+    const dim3 grid((unsigned)((items + 7) / 8 * 8));
+    hipLaunchKernelGGL((gemm_q4k_pipe_kernel<TILED>), grid, dim3(512), q4p::kLds, st, a_hi, a_lo, lda, s_hi, s_lo,
+                       lds, rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
+    if (splits > 1)
+        hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
+                           res, m, n);
+    return MXH_OK;
+}
+
+// the pipelined kernel's 16-byte direct loads need 16-byte aligned rows
+bool q4p_aligned(const void* a_hi, const void* a_lo, int lda, const void* s_hi, const void* s_lo, int lds,
+                 const void* w) {
+    auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    return al(a_hi) && al(a_lo) && al(s_hi) && al(s_lo) && al(w) && lda % 8 == 0 && lds % 8 == 0;
+}
+
 }  // namespace
 
 // Wide (256-row) weight tiles stage each activation tile once for twice the
@@ -718,6 +1062,13 @@ int gemm_q_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda
     if (m <= 0 || n <= 0 || !gemm_q_f16_supported(type, k) || lda < k || lds < k / 32 || ldo < n) return MXH_ERR_ARG;
     if (!part) part_floats = 0;
     const uint8_t* wb = (const uint8_t*)w;
+    if ((type == MXH_Q4_K || type == MXH_Q4_K_TILED) && q4p_aligned(a_hi, a_lo, lda, s_hi, s_lo, lds, w)) {
+        if (type == MXH_Q4_K_TILED)
+            return gemm_q4k_pipe_launch<true>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
+                                              form, part, part_floats, st);
+        return gemm_q4k_pipe_launch<false>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
+                                           part, part_floats, st);
+    }
     if (q4_wide_tiles(m, n))
         return gemm_q_f16_dispatch<256>(type, a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
                                         form, part, part_floats, st);
