@@ -649,13 +649,73 @@ __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, in
 // transformer.cpp:189-214; float products where the reference rounds a
 // double product to float, within 1 ulp); the sum of squares is reduced in
 // double in a fixed order, so every workgroup stages identical values.
-template <int NB, bool NORM, class F>
-__device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
+// x as stored in memory
+struct PlainIn {
+    const float* x;
+    typedef float4 Raw;
+    __device__ __forceinline__ Raw issue(int e) const { return *reinterpret_cast<const float4*>(x + e); }
+    __device__ __forceinline__ float4 finish(const Raw& r) const { return r; }
+};
+
+// x of GEMV_ATTN: the decode attention's output, merged from its split
+// partials (attention_run).  Element e lies in q head h = e / hd; split s
+// left the running max m_s (base-2 units), the sum l_s and the exp-weighted
+// V sums V_s over its positions, and the merged value is
+// sum_s w_s V_s / sum_s w_s l_s with w_s = 2^(m_s - max_s m_s): the softmax
+// of softmax.cpp:4-18 over the union of the splits' positions.  A split
+// that held no position this step has m_s = -inf and weight 0 (its V sums
+// are stale and are not used).
+struct AttnIn {
+    const float* part;
+    int S, hd, nh;
+    struct Raw {
+        float4 v[kAttnMaxSplits];
+        float2 ml[kAttnMaxSplits];
+    };
+    __device__ __forceinline__ Raw issue(int e) const {
+        Raw r;
+        const int h = e / hd, d = e - h * hd;
+        const float* pv = part + (size_t)h * S * hd + d;
+        const float* ml = part + (size_t)nh * S * hd + (size_t)h * S * 2;
+#pragma unroll
+        for (int s = 0; s < kAttnMaxSplits; ++s)
+            if (s < S) {
+                r.v[s] = *reinterpret_cast<const float4*>(pv + (size_t)s * hd);
+                r.ml[s] = *reinterpret_cast<const float2*>(ml + 2 * s);
+            }
+        return r;
+    }
+    __device__ __forceinline__ float4 finish(const Raw& r) const {
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kAttnMaxSplits; ++s)
+            if (s < S) M = fmaxf(M, r.ml[s].x);
+        float den = 0.f;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int s = 0; s < kAttnMaxSplits; ++s) {
+            if (s >= S) break;
+            const float m = r.ml[s].x;
+            if (m == -INFINITY) continue;
+            const float w = __builtin_amdgcn_exp2f(m - M);
+            den = fmaf(w, r.ml[s].y, den);
+            a.x = fmaf(w, r.v[s].x, a.x);
+            a.y = fmaf(w, r.v[s].y, a.y);
+            a.z = fmaf(w, r.v[s].z, a.z);
+            a.w = fmaf(w, r.v[s].w, a.w);
+        }
+        return make_float4(a.x / den, a.y / den, a.z / den, a.w / den);
+    }
+};
+
+template <int NB, bool NORM, class XS, class F>
+__device__ __forceinline__ void stage_xq_nb(float* smem, const XS& xs, const float* __restrict__ nw,
                                             int k, float eps, double* red, F&& after_loads) {
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
     constexpr int kStep = kThreads * 4;
     const int base = threadIdx.x * 4;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    typename XS::Raw raw[NB];
     float4 v[NB], g[NORM ? NB : 1];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
@@ -664,14 +724,13 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const float* __restrict
         // static for the explicit wait in after_loads; out-of-range values
         // are replaced by zero only after that wait
         const int ec = e < k ? e : k - 4;
-        v[u] = *reinterpret_cast<const float4*>(x + ec);
+        raw[u] = xs.issue(ec);
         if (NORM) g[u] = *reinterpret_cast<const float4*>(nw + ec);
     }
     // issues the first weight steps (younger than x) and waits for x only
     after_loads();
 #pragma unroll
-    for (int u = 0; u < NB; ++u)
-        if (base + u * kStep >= k) v[u] = z;
+    for (int u = 0; u < NB; ++u) v[u] = base + u * kStep >= k ? z : xs.finish(raw[u]);
     if (NORM) {
         // per-thread float partials (at most 64 squares), summed in double
         float sf = 0.f;
@@ -741,12 +800,13 @@ __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ 
     const int nb = (k + kThreads * 4 - 1) / (kThreads * 4);
     // register budget: the two weight buffers issued during staging stay
     // live, so at most 48 staged registers (x, and the norm weight)
+    const PlainIn xs{x};
     if (nw) {
-        if (nb <= 4) return stage_xq_nb<4, true>(smem, x, nw, k, eps, red, issue_first);
+        if (nb <= 4) return stage_xq_nb<4, true>(smem, xs, nw, k, eps, red, issue_first);
     } else {
-        if (nb <= 4) return stage_xq_nb<4, false>(smem, x, nw, k, eps, red, issue_first);
-        if (nb <= 8) return stage_xq_nb<8, false>(smem, x, nw, k, eps, red, issue_first);
-        if (nb <= 12) return stage_xq_nb<12, false>(smem, x, nw, k, eps, red, issue_first);
+        if (nb <= 4) return stage_xq_nb<4, false>(smem, xs, nw, k, eps, red, issue_first);
+        if (nb <= 8) return stage_xq_nb<8, false>(smem, xs, nw, k, eps, red, issue_first);
+        if (nb <= 12) return stage_xq_nb<12, false>(smem, xs, nw, k, eps, red, issue_first);
     }
     issue_first();
     stage_xq_2pass(smem, x, nw, k, eps, red);
@@ -758,6 +818,8 @@ __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ 
 //               (transformer.cpp:183-185, 696-704) for i < F
 //  GEMV_ARGMAX: y = logits; each workgroup also leaves its (largest logit,
 //               lowest index) in red_val/red_idx[blockIdx] for argmax_finish
+//  GEMV_ATTN  : as PLAIN, with x merged from the decode attention's split
+//               partials in the staging (AttnIn; k <= 4096, no norm)
 // f(integral_constant<int, K>) for K = 0 .. N-1, expanded at compile time
 // (a plain unrolled loop over a register array may be left rolled, which
 // sends the array to scratch memory)
@@ -831,7 +893,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
     // PLAIN mode also prefetches the residual of the row group with each step
-    constexpr bool kRes = MODE == GEMV_PLAIN;
+    constexpr bool kRes = MODE == GEMV_PLAIN || MODE == GEMV_ATTN;
     constexpr int kL = Ty::kLoads * R + (kRes ? kOut : 0);  // vector loads per step
     constexpr int kL1 = kL < 63 ? kL : 63, kL2 = 2 * kL < 63 ? 2 * kL : 63;
     const float* res_src = a.res ? a.res : a.y;  // (not used without a residual)
@@ -920,7 +982,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             for_each_k([&](auto kc) { issue(ci, sb[decltype(kc)::value]); }, std::make_integer_sequence<int, NS>{});
             wait_vmcnt<NS * kL>();
         };
-        if constexpr (Ty::kIntX) {
+        if constexpr (MODE == GEMV_ATTN) {
+            stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
+                                  red, issue_all);
+        } else if constexpr (Ty::kIntX) {
             stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
         } else {
             issue_all();
@@ -938,7 +1003,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             issue(ci, s1);
             wait_vmcnt<kL2>();
         };
-        if constexpr (Ty::kIntX) {
+        if constexpr (MODE == GEMV_ATTN) {
+            stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
+                                  red, issue_first);
+        } else if constexpr (Ty::kIntX) {
             stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
         } else {
             issue_first();
@@ -1061,6 +1129,37 @@ int resident_grid(const void* kernel, size_t lds) {
     return grid;
 }
 
+// the kernel instance of an epilogue mode (GEMV_ATTN only for the
+// quantized formats, whose staging merges the attention partials)
+template <template <int> class T, int R, int NS>
+const void* kernel_for(int mode) {
+    if (mode == GEMV_SILU) return (const void*)gemv_kernel<T, R, GEMV_SILU, NS>;
+    if constexpr (NS == 0)
+        if (mode == GEMV_ARGMAX) return (const void*)gemv_kernel<T, R, GEMV_ARGMAX, NS>;
+    if constexpr (T<R>::kIntX)
+        if (mode == GEMV_ATTN) return (const void*)gemv_kernel<T, R, GEMV_ATTN, NS>;
+    return (const void*)gemv_kernel<T, R, GEMV_PLAIN, NS>;
+}
+
+// launch of a PLAIN, SILU or ATTN instance
+template <template <int> class T, int R, int NS>
+void launch_mode(int mode, unsigned grid, size_t lds, const GemvArgs& a, hipStream_t st) {
+    if (mode == GEMV_SILU) {
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, NS>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x,
+                           a.norm_w, a.n, a.k, a);
+        return;
+    }
+    if constexpr (T<R>::kIntX) {
+        if (mode == GEMV_ATTN) {
+            hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ATTN, NS>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x,
+                               a.norm_w, a.n, a.k, a);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, NS>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
+                       a.n, a.k, a);
+}
+
 template <template <int> class T, int R>
 int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const int kout = mode == GEMV_SILU ? R / 2 : R;
@@ -1088,25 +1187,15 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
                     const int64_t min_grid = (n_groups + per_wg - 1) / per_wg;
                     int64_t grid = need < n_cu ? need : n_cu;
                     if (grid < min_grid) grid = min_grid;
-                    const void* ks = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, NSv>
-                                                        : (const void*)gemv_kernel<T, R, GEMV_SILU, NSv>;
-                    if (grid > resident_grid(ks, lds)) return false;
-                    if (mode == GEMV_PLAIN)
-                        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, NSv>), dim3((unsigned)grid), dim3(kThreads),
-                                           lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
-                    else
-                        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, NSv>), dim3((unsigned)grid), dim3(kThreads),
-                                           lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
+                    if (grid > resident_grid(kernel_for<T, R, NSv>(mode), lds)) return false;
+                    launch_mode<T, R, NSv>(mode, (unsigned)grid, lds, a, st);
                     return true;
                 }
             };
             if (try_short(std::integral_constant<int, kShortSteps>{})) return MXH_OK;
         }
     }
-    const void* kern = mode == GEMV_PLAIN ? (const void*)gemv_kernel<T, R, GEMV_PLAIN, 0>
-                       : mode == GEMV_SILU ? (const void*)gemv_kernel<T, R, GEMV_SILU, 0>
-                                           : (const void*)gemv_kernel<T, R, GEMV_ARGMAX, 0>;
-    int cap = grid_cap > 0 ? grid_cap : resident_grid(kern, lds);
+    int cap = grid_cap > 0 ? grid_cap : resident_grid(kernel_for<T, R, 0>(mode), lds);
     // Short runs (a few row groups per wave with one workgroup per CU): one
     // workgroup per CU, so x is staged and quantized once per CU and no CU
     // carries two workgroups' staging while others carry one.  Long runs keep
@@ -1114,18 +1203,14 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     if (grid_cap <= 0 && need > n_cu && (n_groups + (int64_t)n_cu * kWaves - 1) / ((int64_t)n_cu * kWaves) <= 8)
         cap = n_cu;
     const unsigned grid = (unsigned)(need < cap ? need : cap);
-    if (mode == GEMV_PLAIN)
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
-                           a.n, a.k, a);
-    else if (mode == GEMV_SILU)
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
-                           a.n, a.k, a);
-    else {
+    if (mode == GEMV_ARGMAX) {
         if ((int)grid > a.red_cap) return MXH_ERR_ARG;
         hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
                            a.n, a.k, a);
         hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, st, a.red_val, a.red_idx, (int)grid, a.tokens,
                            a.pos);
+    } else {
+        launch_mode<T, R, 0>(mode, grid, lds, a, st);
     }
     return MXH_OK;
 }
@@ -1137,6 +1222,12 @@ constexpr int64_t kGemvMaxK = 15360;
 
 int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     if (a.k % 32 || a.k > kGemvMaxK || a.n <= 0 || (mode == GEMV_SILU && a.n % 2)) return MXH_ERR_ARG;
+    // the attention merge: at most 4096 inputs (one staging pass), quantized
+    // weights, whole q heads of 4 to 128 elements, no norm
+    if (mode == GEMV_ATTN &&
+        (a.k > 4096 || !a.part || a.norm_w || a.part_splits < 1 || a.part_splits > kAttnMaxSplits ||
+         a.part_hd < 4 || a.part_hd > 128 || a.part_hd % 4 || a.k % a.part_hd || storage_type(type) == MXH_F32))
+        return MXH_ERR_ARG;
     if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.tokens || !a.pos)) return MXH_ERR_ARG;
     switch (type) {
     case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);

@@ -20,7 +20,7 @@ int gemv_launch(int type, const void* w, const float* x, float* y, const float* 
                 hipStream_t st);
 
 // Fused GEMV launch (see mxh_gemv.hip for the epilogues).
-enum { GEMV_PLAIN = 0, GEMV_SILU = 1, GEMV_ARGMAX = 2 };
+enum { GEMV_PLAIN = 0, GEMV_SILU = 1, GEMV_ARGMAX = 2, GEMV_ATTN = 3 };
 struct GemvArgs {
     const uint8_t* w;
     const float* x;
@@ -37,6 +37,12 @@ struct GemvArgs {
     int* counter;
     int* tokens;
     int* pos;
+    // ATTN: x is the decode attention's output, merged here from its split
+    // partials (attention_run): V sums [k / part_hd][part_splits][part_hd],
+    // then (max in base-2 units, sum) pairs [k / part_hd][part_splits][2];
+    // y = W.x (+ res) as in PLAIN
+    const float* part;
+    int part_splits, part_hd;
 };
 int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st);
 
@@ -56,8 +62,10 @@ int matmul_f32_launch(const float* a, const float* b, float* out, int64_t m, int
 
 // decoder-step kernels (mxh_layer.hip)
 int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, hipStream_t st);
-// Fused decode attention: QK-norm, RoPE, fp16 KV append, split-K softmax*V
-// and the split merge (mxh_layer.hip).
+// Fused decode attention: QK-norm, RoPE, fp16 KV append and split-K
+// softmax*V (mxh_layer.hip); the splits' partials are merged by the
+// o-projection GEMV (GEMV_ATTN).
+constexpr int kAttnMaxSplits = 8;  // workgroups (partials) per kv head
 struct AttnArgs {
     const float* qkv;     // [q | k | v] raw projections of the current token
     const float* bias;    // [bq | bk | bv] or null
@@ -67,13 +75,14 @@ struct AttnArgs {
     const int* pos;       // current position (device)
     __half* kc;           // this layer's K cache [n_ctx][nkv*hd]
     __half* vc;
-    float* part;          // split partials
-    int* counter;         // per kv head, zero between launches
-    float* att;           // [nh*hd] output
+    float* part;          // split partials (attention_scratch_floats)
     int nh, nkv, hd, neox;
     float eps, scale;
 };
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st);
+// the attention output [nh][hd] merged from `splits` partials (for
+// o-projections that do not merge them in their staging)
+int attention_merge_launch(const float* part, int splits, int nh, int hd, float* att, hipStream_t st);
 int attention_splits(int n_ctx, int nh, int nkv, int hd);
 bool attention_supported(int nh, int nkv, int hd);
 size_t attention_scratch_floats(int nh, int nkv, int hd, int n_ctx);

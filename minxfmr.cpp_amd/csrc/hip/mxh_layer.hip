@@ -50,9 +50,13 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
     }
 }
 
+// timeline hook for out-of-tree probes (empty in the library)
+#ifndef MXH_ATTN_STAMP
+#define MXH_ATTN_STAMP(i)
+#endif
+
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
-constexpr int kAttnChunk = 64;      // positions per pass of a workgroup (one per lane in the softmax)
-constexpr int kAttnMaxSplits = 128;  // partials per kv head (two per lane in the merge)
+constexpr int kAttnSplitPos = 256;  // positions per workgroup (split) before the next split opens
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
 // wave; `src` is the raw projection, the result goes to dst (LDS).
@@ -129,324 +133,231 @@ __device__ __forceinline__ float fold_position_groups(float v) {
     return v + lane_xor<32>(v);
 }
 
-// Decode attention for kv head g over the L = pos+1 positions
-// (transformer.cpp:529-629), head_dim = 8 * LPP.
+template <int LPP>
+__device__ __forceinline__ float fold_position_groups_max(float v) {
+    if constexpr (LPP <= 4) v = fmaxf(v, lane_xor<4>(v));
+    if constexpr (LPP <= 8) v = fmaxf(v, lane_xor<8>(v));
+    if constexpr (LPP <= 16) v = fmaxf(v, lane_xor<16>(v));
+    return fmaxf(v, lane_xor<32>(v));
+}
+
+// Decode attention (transformer.cpp:529-629, softmax.cpp:4-18) for one q
+// head over a split of the L = pos + 1 positions, head_dim = 8 * LPP.
 //
-// Positions are taken in chunks of 64; workgroup s of the S per kv head takes
-// chunks s, s+S, ...  Thread (position group pg, lane sub) holds 8 dims
-// (one 16-byte fp16 load) of NP positions of K and of V, so a chunk's cache
-// rows are read with every load in flight at once.  Scores are reduced over
-// the LPP lanes of a position with DPP; one wave per q head keeps a running
-// softmax (max, sum) across chunks, and the exp-weighted V sums stay in
-// registers, rescaled per chunk.
+// Workgroup (i, s): q head qh of kv head g = i % nkv (qh = g * group +
+// i / nkv, so the q heads that share a kv head have workgroup ids equal
+// modulo 8 and run on one XCD, whose L2 serves their common K/V rows once),
+// split s of S = min(gridDim.y, ceil(L / kAttnSplitPos)) contiguous position
+// ranges.  It leaves the split's running max m (base-2 units), sum l and
+// exp-weighted V sums in `part`; the o-projection's x staging merges the S
+// partials of each q head (GEMV_ATTN), so no workgroup waits for another.
+// Workgroups past S leave an empty partial (m = -inf, l = 0).
 //
-// The current token's k and v are prepared, appended (fp16) to the cache and
-// used from LDS copies for position pos, so no workgroup reads a cache row
-// written in this launch: by the workgroup holding chunk pos/64 when the
-// context is one chunk (it then writes the normalised output directly), else
-// by an extra workgroup per kv head (blockIdx.y == S) whose partial is that
-// one position.  Each partial is (max, sum, V sums) per q head; the last
-// workgroup to finish merges them.  GM (4 or 8) bounds the q heads per kv head held in registers;
-// GM = 4 keeps the kernel near 128 VGPRs, so more workgroups are resident.
-template <int LPP, int GM>
+// Inside a workgroup each of the 8 waves takes chunks w, w + 8, ... of the
+// range (4 positions per lane: 16 positions at head_dim 128), with DB
+// chunks' K and V rows in flight per wave (a lane holds 8 dims, one 16-byte
+// fp16 load, of each of its positions), and keeps its own running softmax in
+// registers; scores are reduced over the LPP lanes of a position with DPP.
+// The eight wave partials are merged through LDS at the end.
+//
+// q is prepared (bias, QK-norm, RoPE) by each workgroup of its head; in the
+// last split, which holds position pos, k and v of the current token too,
+// rounded through fp16 as every cached position and used from LDS; the
+// workgroup of the kv head's first q head appends them to the cache.  No
+// cache row written in this launch is read in it.
+template <int LPP, int DB>
 // pos, the caches and q|k|v, needed first, also come as leading scalars that
 // the command processor preloads into SGPRs (-amdgpu-kernarg-preload-count).
-__global__ __launch_bounds__(256) void attention_kernel(const int* ppos, __half* pkc, __half* pvc, const float* pqkv,
+__global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half* pkc, __half* pvc, const float* pqkv,
                                                         AttnArgs a) {
     a.pos = ppos;
     a.kc = pkc;
     a.vc = pvc;
     a.qkv = pqkv;
-    constexpr int HD = LPP * 8, NPG = 256 / LPP, NP = kAttnChunk / NPG;
-    __shared__ float qs[kAttnMaxGroup][HD];
+    MXH_ATTN_STAMP(0);
+    constexpr int HD = LPP * 8, PR = 64 / LPP, NP = 4, CH = NP * PR, NW = 8;
+    __shared__ float qs[HD];
     __shared__ float kvt[HD];
     __shared__ __align__(16) __half kvh[2][HD];
-    __shared__ float sc[kAttnMaxGroup][kAttnChunk];
-    __shared__ float run_m[kAttnMaxGroup], run_l[kAttnMaxGroup], alpha[kAttnMaxGroup];
-    __shared__ __align__(16) float red[4][kAttnMaxGroup][HD];
-    __shared__ float wgt[kAttnMaxGroup][kAttnMaxSplits];
-    __shared__ int last;
+    __shared__ float wm[NW], wl[NW];
+    __shared__ __align__(16) float wacc[NW][HD];
 
-    // blockIdx.y < S: chunk splits; blockIdx.y == S: the current-token
-    // workgroup (see `sep`)
-    const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y - 1;
     const int group = a.nh / a.nkv, kvd = a.nkv * HD, qd = a.nh * HD;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int sub = tid % LPP, pg = tid / LPP;
+    const int g = (int)blockIdx.x % a.nkv, qh = g * group + (int)blockIdx.x / a.nkv;
+    const int s = blockIdx.y, SM = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sub = lane % LPP, pr = lane / LPP;
     const int pos = *a.pos, L = pos + 1;
-    // With more than one chunk the partials are merged anyway, and the
-    // current token (q, k and v preparation, its k/v append and its own
-    // score) goes to a workgroup of its own instead of the chunk holding pos,
-    // which would otherwise finish a preparation round after the others.
-    // The chunks then cover the cached positions [0, pos) only (every chunk
-    // holds at least one of them).
-    const bool sep = L > kAttnChunk;
-    const int nch = ((sep ? pos : L) + kAttnChunk - 1) / kAttnChunk;
-    const int sact = nch < S ? nch : S;        // chunk workgroups with work
-    const int nparts = sact + (sep ? 1 : 0);  // partials to merge
-    const bool cur = s == S;
-    if (cur ? !sep : s >= sact) return;
-    const int own_chunk = pos / kAttnChunk;
-    const bool owns = cur || (!sep && own_chunk % S == s);
-    const int lim = sep ? pos : L;  // chunk positions below lim
+    const int S = min(SM, (L + kAttnSplitPos - 1) / kAttnSplitPos);
+    MXH_ATTN_STAMP(1);
+    float* part_v = a.part;                              // [nh][SM][HD]
+    float* part_ml = a.part + (size_t)a.nh * SM * HD;    // [nh][SM][2]
+    const size_t slot = (size_t)qh * SM + s;
+    if (s >= S) {
+        if (tid == 0) {
+            part_ml[slot * 2] = -INFINITY;
+            part_ml[slot * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    // this split's positions [p0, p1); the last one ends at pos, which comes
+    // from LDS, so the cache rows read are [p0, min(p1, pos))
+    const int p0 = (int)((int64_t)L * s / S), p1 = (int)((int64_t)L * (s + 1) / S);
+    const bool last = s == S - 1;
+    const int rows_end = last ? pos : p1;
+    const int nch = (p1 - p0 + CH - 1) / CH;
     const size_t col = (size_t)g * HD + sub * 8;
 
-    uint4 kraw[NP], vraw[NP];
-    // cache rows of this thread's positions in chunk c; positions >= pos are
-    // not read (pos itself comes from LDS)
-    auto load = [&](uint4* raw, const __half* cache, int c) {
+    uint4 kraw[DB][NP], vraw[DB][NP];
+    auto load = [&](int b, int c) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const int j = c * kAttnChunk + i * NPG + pg;
-            raw[i] = j < pos ? *reinterpret_cast<const uint4*>(cache + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
+            const int j = p0 + c * CH + i * PR + pr;
+            const bool in = j < rows_end;
+            kraw[b][i] = in ? *reinterpret_cast<const uint4*>(a.kc + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
+            vraw[b][i] = in ? *reinterpret_cast<const uint4*>(a.vc + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
         }
     };
-    if (!cur) {
-        load(kraw, a.kc, s);
-        load(vraw, a.vc, s);
-    }
+    // the first DB chunks of this wave are requested before the q
+    // preparation (they do not depend on it)
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+        if (wave + NW * b < nch) load(b, wave + NW * b);
+    MXH_ATTN_STAMP(2);
 
-    // q heads (and k, v of the current token) of this kv head
+    // wave 0: q; in the last split wave 1: k, wave 2: v of the current token
     const double* cs = a.rope_cs + (size_t)pos * HD;  // (hd/2) pairs of (cos, sin)
-    const int njobs = group + (owns ? 2 : 0);
-    for (int job = wave; job < njobs; job += 4) {
-        if (job < group) {
-            const int qh = g * group + job;
-            head_prep(a.qkv + (size_t)qh * HD, a.bias ? a.bias + (size_t)qh * HD : nullptr, a.q_norm, cs, qs[job], HD,
-                      a.eps, a.neox);
-            continue;
-        }
-        const bool is_k = job == group;
+    if (wave == 0) {
+        head_prep(a.qkv + (size_t)qh * HD, a.bias ? a.bias + (size_t)qh * HD : nullptr, a.q_norm, cs, qs, HD, a.eps,
+                  a.neox);
+    } else if (last && wave <= 2) {
+        const bool is_k = wave == 1;
         const size_t off = (is_k ? qd : qd + kvd) + (size_t)g * HD;
         if (is_k) {
             head_prep(a.qkv + off, a.bias ? a.bias + off : nullptr, a.k_norm, cs, kvt, HD, a.eps, a.neox);
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         }
-        // rounded through fp16 like every cached position, and appended
+        // rounded through fp16 like every cached position; appended once
+        // per kv head
+        const bool append = qh % group == 0;
         __half* cache = (is_k ? a.kc : a.vc) + (size_t)pos * kvd + (size_t)g * HD;
         for (int t = lane; t < HD; t += 64) {
             const float v = is_k ? kvt[t] : a.qkv[off + t] + (a.bias ? a.bias[off + t] : 0.f);
             const __half hv = __float2half_rn(v);
             kvh[is_k ? 0 : 1][t] = hv;
-            cache[t] = hv;
+            if (append) cache[t] = hv;
         }
-    }
-    if (tid < kAttnMaxGroup) {
-        run_m[tid] = -INFINITY;
-        run_l[tid] = 0.f;
     }
     __syncthreads();
+    MXH_ATTN_STAMP(3);
 
-    float qreg[GM][8], acc[GM][8];
+    float qreg[8], acc[8], run_m = -INFINITY, run_l = 0.f;
 #pragma unroll
-    for (int h = 0; h < GM; ++h)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            qreg[h][e] = h < group ? qs[h][sub * 8 + e] : 0.f;
-            acc[h][e] = 0.f;
-        }
-
-    // scores in base-2 units (exp(x - m) == exp2(x log2 e - m log2 e)): the
-    // running max and the split maxima below are in the same units
+    for (int e = 0; e < 8; ++e) {
+        qreg[e] = qs[sub * 8 + e];
+        acc[e] = 0.f;
+    }
+    // scores in base-2 units (exp(x - m) == exp2(x log2 e - m log2 e))
     const float scale2 = a.scale * 1.4426950408889634f;
-    for (int c = cur ? nch : s; c < nch; c += S) {
-        if (!sep && c == own_chunk) {
+    auto chunk = [&](int b, int c) {
+        // the current position (last split) from the LDS copies
+        if (last && c == (pos - p0) / CH) {
 #pragma unroll
             for (int i = 0; i < NP; ++i)
-                if (c * kAttnChunk + i * NPG + pg == pos) {
-                    kraw[i] = *reinterpret_cast<const uint4*>(&kvh[0][sub * 8]);
-                    vraw[i] = *reinterpret_cast<const uint4*>(&kvh[1][sub * 8]);
+                if (p0 + c * CH + i * PR + pr == pos) {
+                    kraw[b][i] = *reinterpret_cast<const uint4*>(&kvh[0][sub * 8]);
+                    vraw[b][i] = *reinterpret_cast<const uint4*>(&kvh[1][sub * 8]);
                 }
         }
-        // scores
+        float sc[NP];
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
-            const int jl = i * NPG + pg, j = c * kAttnChunk + jl;
+            const int j = p0 + c * CH + i * PR + pr;
             float kf[8];
-            half8_to_float(kraw[i], kf);
+            half8_to_float(kraw[b][i], kf);
+            float d = 0.f;
 #pragma unroll
-            for (int h = 0; h < GM; ++h) {
-                if (h >= group) break;
-                float d = 0.f;
+            for (int e = 0; e < 8; ++e) d = fmaf(qreg[e], kf[e], d);
+            d = lane_group_sum<LPP>(d);
+            sc[i] = j < p1 ? d * scale2 : -INFINITY;
+        }
+        // running softmax over this wave's positions (every chunk holds at
+        // least one position, so the new max is finite unless a score is
+        // NaN, which then propagates)
+        float mc = sc[0];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf(qreg[h][e], kf[e], d);
-                d = lane_group_sum<LPP>(d);
-                if (sub == 0) sc[h][jl] = j < lim ? d * scale2 : -INFINITY;
-            }
+        for (int i = 1; i < NP; ++i) mc = fmaxf(mc, sc[i]);
+        mc = fold_position_groups_max<LPP>(mc);
+        const float mn = fmaxf(run_m, mc);
+        const float al = __builtin_amdgcn_exp2f(run_m - mn);
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            sc[i] = __builtin_amdgcn_exp2f(sc[i] - mn);
+            ps += sc[i];
         }
-        if (c + S < nch) load(kraw, a.kc, c + S);
-        __syncthreads();
-        // running softmax per q head (softmax.cpp:4-18, normalised at the end)
-        for (int h = wave; h < group; h += 4) {
-            const float sv = sc[h][lane];
-            const float mo = run_m[h], mn = fmaxf(mo, wave_max_all(sv));
-            const float p = __builtin_amdgcn_exp2f(sv - mn), al = __builtin_amdgcn_exp2f(mo - mn);
-            const float ps = wave_sum_all(p);
-            sc[h][lane] = p;
-            if (lane == 0) {
-                run_m[h] = mn;
-                run_l[h] = run_l[h] * al + ps;
-                alpha[h] = al;
-            }
-        }
-        __syncthreads();
+        run_l = run_l * al + fold_position_groups<LPP>(ps);
+        run_m = mn;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= al;
         // exp-weighted V
-#pragma unroll
-        for (int h = 0; h < GM; ++h) {
-            if (h >= group) break;
-            const float al = alpha[h];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] *= al;
-        }
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             float vf[8];
-            half8_to_float(vraw[i], vf);
+            half8_to_float(vraw[b][i], vf);
 #pragma unroll
-            for (int h = 0; h < GM; ++h) {
-                if (h >= group) break;
-                const float p = sc[h][i * NPG + pg];
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(sc[i], vf[e], acc[e]);
+        }
+    };
+    // chunks wave, wave + 8, ...: the wave's k-th chunk sits in buffer
+    // k % DB, which is refilled with the chunk DB further on once consumed
+    for (int c0 = wave; c0 < nch; c0 += NW * DB) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
+        for (int b = 0; b < DB; ++b) {
+            const int c = c0 + NW * b;
+            if (c < nch) {
+                chunk(b, c);
+                if (c + NW * DB < nch) load(b, c + NW * DB);
             }
         }
-        if (c + S < nch) load(vraw, a.vc, c + S);
-        __syncthreads();  // sc and alpha are rewritten by the next chunk
     }
+    MXH_ATTN_STAMP(4);
 
-    const int SP = S + 1;                                   // partial slots per q head
-    float* part_v = a.part;                                 // [nh][SP][hd]
-    float* part_ml = a.part + (size_t)a.nh * SP * HD;       // [nh][SP][2]
-    if (cur) {
-        // the current token's partial (slot sact): score q_h . k with k and v
-        // rounded through fp16 as every cached position, max = that score,
-        // sum 1, V sums = v
-        for (int h = wave; h < group; h += 4) {
-            float d = 0.f;
-            for (int t = lane; t < HD; t += 64) d = fmaf(qs[h][t], __half2float(kvh[0][t]), d);
-            d = wave_sum_all(d) * scale2;
-            const size_t slot = ((size_t)g * group + h) * SP + sact;
-            for (int t = lane; t < HD; t += 64) st_agent(part_v + slot * HD + t, __half2float(kvh[1][t]));
-            if (lane == 0) {
-                st_agent(part_ml + slot * 2, d);
-                st_agent(part_ml + slot * 2 + 1, 1.0f);
-            }
-        }
-    } else {
-        // sum the V partials of the position groups: lanes of a wave with the
-        // same `sub`, then the four waves through LDS
+    // the wave's partial (V sums folded over its position rows) to LDS
 #pragma unroll
-        for (int h = 0; h < GM; ++h) {
-            if (h >= group) break;
+    for (int e = 0; e < 8; ++e) acc[e] = fold_position_groups<LPP>(acc[e]);
+    if (lane < LPP) {
+        float4* dst = reinterpret_cast<float4*>(&wacc[wave][sub * 8]);
+        dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    }
+    if (lane == 0) {
+        wm[wave] = run_m;
+        wl[wave] = run_l;
+    }
+    __syncthreads();
+    MXH_ATTN_STAMP(5);
+    // merge the waves (a wave without chunks has m = -inf, weight 0) and
+    // store the workgroup's partial
+    if (tid < HD) {
+        float M = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[h][e] = fold_position_groups<LPP>(acc[h][e]);
-            if (lane < LPP) {
-                float4* dst = reinterpret_cast<float4*>(&red[wave][h][sub * 8]);
-                dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-                dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-            }
-        }
-        __syncthreads();
-        for (int i = tid; i < group * HD; i += 256) {
-            const int h = i / HD, t = i % HD;
-            const float v = red[0][h][t] + red[1][h][t] + red[2][h][t] + red[3][h][t];
-            const size_t qh = (size_t)g * group + h;
-            if (nparts == 1) {
-                a.att[qh * HD + t] = v / run_l[h];
-            } else {
-                st_agent(part_v + (qh * SP + s) * HD + t, v);
-                if (t == 0) {
-                    st_agent(part_ml + (qh * SP + s) * 2, run_m[h]);
-                    st_agent(part_ml + (qh * SP + s) * 2 + 1, run_l[h]);
-                }
-            }
-        }
-        if (nparts == 1) return;
-    }
-
-    // the last workgroup of kv head g to finish merges the partials; they
-    // were stored device-coherently and are complete before the count (the
-    // hand-off protocol written out at st_agent in mxh_device.h: sc1 stores,
-    // a full vmcnt wait, the relaxed add; the add's return value, sc1 loads)
-    wait_mem();
-    __syncthreads();
-    if (tid == 0) last = add_agent(a.counter + g, 1) == nparts - 1;
-    __syncthreads();
-    if (!last) return;
-    // (q head, 4 dims) items; the splits of an item are shared by `per`
-    // threads.  The first kPre splits of each thread are requested together
-    // with the (max, sum) pairs, so most merges cost one memory round trip.
-    constexpr int kPre = 16;
-    const int items = group * HD / 4, per = 256 / items;
-    const int item = tid % items, part = tid / items;
-    const int hi = item / (HD / 4), d4 = item % (HD / 4);
-    // byte offsets into the V partials, read as 16-byte agent-coherent loads
-    const __amdgpu_buffer_rsrc_t prs = agent_rsrc(part_v, (int)((size_t)a.nh * SP * HD * sizeof(float)));
-    const int src = (int)((((size_t)g * group + hi) * SP * HD + 4 * d4) * sizeof(float));
-    float4 pre[kPre];
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w]);
+        float l = 0.f, v = 0.f;
 #pragma unroll
-    for (int k = 0; k < kPre; ++k) {
-        const int i = part + per * k;
-        pre[k] = part < per && i < nparts ? ld_agent4(prs, src + i * HD * (int)sizeof(float))
-                                        : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    for (int h = wave; h < group; h += 4) {
-        // splits lane and lane + 64
-        const float* ml = part_ml + ((size_t)g * group + h) * SP * 2;
-        const bool in0 = lane < nparts, in1 = lane + 64 < nparts;
-        const float m0 = in0 ? ld_agent(ml + 2 * lane) : -INFINITY;
-        const float l0 = in0 ? ld_agent(ml + 2 * lane + 1) : 0.f;
-        const float m1 = in1 ? ld_agent(ml + 2 * lane + 128) : -INFINITY;
-        const float l1 = in1 ? ld_agent(ml + 2 * lane + 129) : 0.f;
-        const float M = wave_max_all(fmaxf(m0, m1));
-        const float w0 = in0 ? __builtin_amdgcn_exp2f(m0 - M) : 0.f;
-        const float w1 = in1 ? __builtin_amdgcn_exp2f(m1 - M) : 0.f;
-        const float den = wave_sum_all(w0 * l0 + w1 * l1);
-        wgt[h][lane] = w0 / den;
-        wgt[h][lane + 64] = w1 / den;
-    }
-    __syncthreads();
-    float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (part < per) {
-#pragma unroll
-        for (int k = 0; k < kPre; ++k) {
-            const int i = part + per * k;
-            if (i < nparts) {
-                const float w = wgt[hi][i];
-                s4.x = fmaf(w, pre[k].x, s4.x);
-                s4.y = fmaf(w, pre[k].y, s4.y);
-                s4.z = fmaf(w, pre[k].z, s4.z);
-                s4.w = fmaf(w, pre[k].w, s4.w);
-            }
+        for (int w = 0; w < NW; ++w) {
+            const float mw = wm[w];
+            const float ww = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+            l = fmaf(ww, wl[w], l);
+            v = fmaf(ww, wacc[w][tid], v);
         }
-#pragma unroll 8
-        for (int i = part + per * kPre; i < nparts; i += per) {
-            const float4 v = ld_agent4(prs, src + i * HD * (int)sizeof(float));
-            const float w = wgt[hi][i];
-            s4.x = fmaf(w, v.x, s4.x);
-            s4.y = fmaf(w, v.y, s4.y);
-            s4.z = fmaf(w, v.z, s4.z);
-            s4.w = fmaf(w, v.w, s4.w);
+        part_v[slot * HD + tid] = v;
+        if (tid == 0) {
+            part_ml[slot * 2] = M;
+            part_ml[slot * 2 + 1] = l;
         }
     }
-    float4* r4 = reinterpret_cast<float4*>(&red[0][0][0]);  // 256 float4 fit: 4 * 8 * HD floats >= 1024
-    __syncthreads();
-    r4[tid] = s4;
-    __syncthreads();
-    if (tid < items) {
-        float4 t4 = r4[tid];
-        for (int p = 1; p < per; ++p) {
-            const float4 u = r4[p * items + tid];
-            t4.x += u.x;
-            t4.y += u.y;
-            t4.z += u.z;
-            t4.w += u.w;
-        }
-        const int h = tid / (HD / 4), d4 = tid % (HD / 4);
-        reinterpret_cast<float4*>(a.att + ((size_t)g * group + h) * HD)[d4] = t4;
-    }
-    if (tid == 0) st_agent(a.counter + g, 0);
 }
 
 // ---- batched prefill ---------------------------------------------------------
@@ -573,33 +484,17 @@ int rmsnorm_launch(const float* x, const float* w, float* y, int n, float eps, h
 
 namespace {
 
-const void* attention_kernel_for(int nh, int nkv, int hd) {
-    const bool g4 = nh / nkv <= 4;
-    switch (hd) {
-    case 32: return g4 ? (const void*)attention_kernel<4, 4> : (const void*)attention_kernel<4, 8>;
-    case 64: return g4 ? (const void*)attention_kernel<8, 4> : (const void*)attention_kernel<8, 8>;
-    default: return g4 ? (const void*)attention_kernel<16, 4> : (const void*)attention_kernel<16, 8>;
-    }
-}
-
 }  // namespace
 
-// Workgroups per kv head: one per 64-position chunk of the context up to 64
-// chunks.  Beyond that, enough for at most two chunks each (a workgroup's
-// chunks run one after another), as far as all of them stay resident at
-// once (more would run in a second round), and at most kAttnMaxSplits.
+// Workgroups (splits) per kv head for a context of n_ctx positions: one per
+// kAttnSplitPos positions, at most kAttnMaxSplits (the o-projection merges
+// that many partials per q head in its x staging).
 int attention_splits(int n_ctx, int nh, int nkv, int hd) {
-    const int nch = (n_ctx + kAttnChunk - 1) / kAttnChunk;
-    if (nch <= 64) return nch < 1 ? 1 : nch;
-    int dev = 0, n_cu = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attention_kernel_for(nh, nkv, hd), 256, 0) != hipSuccess)
-        n_cu = per_cu = 0;
-    const int cap = nkv > 0 ? per_cu * n_cu / nkv - 1 : 0;  // (one current-token workgroup per kv head)
-    int S = (nch + 1) / 2;
-    if (S > cap) S = cap;
-    if (S > kAttnMaxSplits - 1) S = kAttnMaxSplits - 1;  // partials: S chunk splits and the current token
-    return S < 64 ? 64 : S;
+    (void)nh;
+    (void)nkv;
+    (void)hd;
+    const int S = (n_ctx + kAttnSplitPos - 1) / kAttnSplitPos;
+    return S < 1 ? 1 : S > kAttnMaxSplits ? kAttnMaxSplits : S;
 }
 
 // head_dim 32, 64 or 128 (8 dims per lane, a power-of-two lane count per
@@ -610,29 +505,44 @@ bool attention_supported(int nh, int nkv, int hd) {
 
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
-    // chunk splits plus the current-token workgroup
-    const dim3 grid(a.nkv, attention_splits(n_ctx, a.nh, a.nkv, a.hd) + 1);
-    const bool g4 = a.nh / a.nkv <= 4;
+    const dim3 grid(a.nh, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
     switch (a.hd) {
-    case 32:
-        if (g4) hipLaunchKernelGGL((attention_kernel<4, 4>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
-        else hipLaunchKernelGGL((attention_kernel<4, 8>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
-        break;
-    case 64:
-        if (g4) hipLaunchKernelGGL((attention_kernel<8, 4>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
-        else hipLaunchKernelGGL((attention_kernel<8, 8>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
-        break;
-    default:
-        if (g4) hipLaunchKernelGGL((attention_kernel<16, 4>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
-        else hipLaunchKernelGGL((attention_kernel<16, 8>), grid, dim3(256), 0, st, a.pos, a.kc, a.vc, a.qkv, a);
-        break;
+    case 32: hipLaunchKernelGGL((attention_kernel<4, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 64: hipLaunchKernelGGL((attention_kernel<8, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    default: hipLaunchKernelGGL((attention_kernel<16, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
     }
     return MXH_OK;
 }
 
-// V partials [nh][S + 1][hd] followed by (max, sum) pairs [nh][S + 1][2]
+// att[h][t] = sum_s w_s V_s[t] / sum_s w_s l_s, w_s = 2^(m_s - max m) over
+// the splits of q head h (a split with m_s = -inf held no position); one
+// thread per output
+__global__ void attention_merge_kernel(const float* __restrict__ part, int S, int nh, int hd, float* __restrict__ att) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nh * hd) return;
+    const int h = i / hd, t = i % hd;
+    const float* ml = part + (size_t)nh * S * hd + (size_t)h * S * 2;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+    float den = 0.f, v = 0.f;
+    for (int s = 0; s < S; ++s) {
+        if (ml[2 * s] == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f(ml[2 * s] - M);
+        den = fmaf(w, ml[2 * s + 1], den);
+        v = fmaf(w, part[((size_t)h * S + s) * hd + t], v);
+    }
+    att[i] = v / den;
+}
+
+int attention_merge_launch(const float* part, int splits, int nh, int hd, float* att, hipStream_t st) {
+    if (splits < 1 || nh < 1 || hd < 1) return MXH_ERR_ARG;
+    hipLaunchKernelGGL(attention_merge_kernel, dim3((nh * hd + 255) / 256), dim3(256), 0, st, part, splits, nh, hd, att);
+    return MXH_OK;
+}
+
+// V partials [nh][S][hd] followed by (max, sum) pairs [nh][S][2]
 size_t attention_scratch_floats(int nh, int nkv, int hd, int n_ctx) {
-    return (size_t)nh * (attention_splits(n_ctx, nh, nkv, hd) + 1) * (hd + 2);
+    return (size_t)nh * attention_splits(n_ctx, nh, nkv, hd) * (hd + 2);
 }
 
 int qkv_prep_rows_launch(const float* qkv, int ldq, const float* bias, const float* q_norm, const float* k_norm,

@@ -62,7 +62,7 @@ struct mxh_model {
           *part = nullptr, *trace = nullptr, *red_val = nullptr;
     int* red_idx = nullptr;
     int red_cap = 0;
-    int* counters = nullptr;  // [0]: lm-head argmax, [1 ..]: attention per kv head
+    int* counters = nullptr;  // [0]: lm-head argmax
     int* tokens = nullptr;  // [n_ctx + 1]: prompt then generated ids
     int* pos = nullptr;     // current position
     int host_pos = 0;
@@ -114,7 +114,28 @@ int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hi
         a.tokens = m->tokens;
         a.pos = m->pos;
     }
+    if (mode == GEMV_ATTN) {
+        a.part = m->part;
+        a.part_splits = attention_splits(m->cfg.n_ctx, m->cfg.n_head, m->cfg.n_head_kv, m->cfg.head_dim);
+        a.part_hd = m->cfg.head_dim;
+    }
     return gemv_run(w.type, a, mode, st);
+}
+
+// Whether the o-projection merges the attention partials in its x staging
+// (GEMV_ATTN: quantized rows of at most 4096 inputs); otherwise a merge
+// kernel writes the attention output first.
+bool o_merges(const mxh_model* m, const DevW& o) {
+    return storage_type(o.type) != MXH_F32 && o.cols <= 4096;
+}
+
+// the o-projection and residual of the decode step, from the attention partials
+int o_proj(mxh_model* m, const Layer& L, hipStream_t st) {
+    if (o_merges(m, L.o)) return gemv(L.o, nullptr, m->x, m->x, m->form, st, nullptr, 0.f, GEMV_ATTN, m);
+    const mxh_model_config& c = m->cfg;
+    int rc = attention_merge_launch(m->part, attention_splits(c.n_ctx, c.n_head, c.n_head_kv, c.head_dim), c.n_head,
+                                    c.head_dim, m->att, st);
+    return rc | gemv(L.o, m->att, m->x, m->x, m->form, st);
 }
 
 // Enqueue one token step at the device position.  with_head: the final
@@ -147,8 +168,6 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
         aa.kc = L.kc;
         aa.vc = L.vc;
         aa.part = m->part;
-        aa.counter = m->counters + 1;
-        aa.att = m->att;
         aa.nh = nh;
         aa.nkv = nkv;
         aa.hd = hd;
@@ -156,7 +175,7 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
         aa.eps = c.eps;
         aa.scale = 1.0f / sqrtf((float)hd);
         rc |= attention_run(aa, c.n_ctx, st);
-        rc |= gemv(L.o, m->att, m->x, m->x, m->form, st);
+        rc |= o_proj(m, L, st);
         if (L.gu_fused) {
             rc |= gemv(L.gu, m->x, m->h, nullptr, m->form, st, L.ffn_norm, c.eps, GEMV_SILU);
         } else {
@@ -494,6 +513,10 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     if (!rc) rc = dalloc(&m->h, (size_t)c.n_ff);
     if (!rc) rc = dalloc(&m->logits, (size_t)c.n_vocab);
     if (!rc) rc = dalloc(&m->part, attention_scratch_floats(c.n_head, c.n_head_kv, c.head_dim, n_ctx));
+    if (!rc)
+        rc = check_hip(hipMemset(m->part, 0, sizeof(float) * attention_scratch_floats(c.n_head, c.n_head_kv,
+                                                                                       c.head_dim, n_ctx)),
+                       "attention partials init");
     if (!rc) rc = dalloc(&m->trace, (size_t)(c.n_layer + 1) * c.n_embd);
     if (!rc) rc = dalloc(&m->tokens, (size_t)n_ctx + 1);
     if (!rc) rc = dalloc(&m->pos, 1);
@@ -890,7 +913,7 @@ int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* l
         add(L.q, m->x, m->qkv, nullptr, L.attn_norm, GEMV_PLAIN);
         add(L.k, m->x, m->qkv + qd, nullptr, L.attn_norm, GEMV_PLAIN);
         add(L.v, m->x, m->qkv + qd + kvd, nullptr, L.attn_norm, GEMV_PLAIN);
-        add(L.o, m->att, m->xn, m->x, nullptr, GEMV_PLAIN);
+        add(L.o, m->att, m->xn, m->x, nullptr, o_merges(m, L.o) ? GEMV_ATTN : GEMV_PLAIN);
         add(L.gu, m->x, m->h, nullptr, L.ffn_norm, GEMV_SILU);
         add(L.g, m->x, m->gu, nullptr, L.ffn_norm, GEMV_PLAIN);
         add(L.u, m->x, m->gu + c.n_ff, nullptr, L.ffn_norm, GEMV_PLAIN);
@@ -906,7 +929,7 @@ int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* l
     int rc = check_hip(hipEventRecord(e0, st), "event");
     for (int r = 0; r < reps && !rc; ++r)
         for (const Job& j : jobs) {
-            rc = gemv(*j.w, j.x, j.y, j.res, m->form, st, j.nw, c.eps, j.mode);
+            rc = gemv(*j.w, j.x, j.y, j.res, m->form, st, j.nw, c.eps, j.mode, m);
             if (rc) break;
         }
     if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
