@@ -487,15 +487,23 @@ __global__ __launch_bounds__(2 * TN, TN == 128 ? 2 : 1) void gemm_q_f16_kernel(c
 // round of 8 steps, double-buffered; the -dmin m_j values of a round are
 // written to a second ring by the decoding waves; the correction MFMAs of a
 // round run at the top of the step after it.
-namespace q4p {
-constexpr int BM = 128, BN = 128, BK = 64, NST = 3;
-constexpr int kStageA = 2 * BM * 128;             // hi + lo
-constexpr int kStageW = 512 * 16;                 // 384 chunks used, 128 padding
-constexpr int kStage = kStageA + kStageW;
-constexpr int kRingB4 = 2 * BM * 16 * 2;            // [limb][row][16 slots] fp16
-constexpr size_t kLds = (size_t)NST * kStage + 4 * (size_t)kRingB4;
-constexpr int kLoadsStep = 4 + 1;                 // per wave: activation + weight chunks
-}  // namespace q4p
+// Geometry for WJ blocks of 32 weight rows per wave: the 4 waves along the
+// weight rows cover BN = 128 WJ of them.  WJ = 2 stages each activation tile
+// once for 256 weight rows, half the activation bytes per MFMA of WJ = 1, in
+// two stages instead of three (the LDS holds no more).
+template <int WJ>
+struct Q4P {
+    static constexpr int BM = 128, BN = 128 * WJ, BK = 64, NST = WJ == 1 ? 3 : 2;
+    static constexpr int kStageA = 2 * BM * 128;              // hi + lo
+    static constexpr int kWChunks = 3 * BN;                   // 16-byte (header, qs, qs) chunks
+    static constexpr int kWLoads = (kWChunks + 511) / 512;    // direct loads per wave and stage
+    static constexpr int kStageW = kWLoads * 512 * 16;        // (padding lanes repeat a real chunk)
+    static constexpr int kStage = kStageA + kStageW;
+    static constexpr int kRingS = 2 * BM * 16 * 2;            // activation sums [limb][row][16 slots] fp16
+    static constexpr int kRingB = 2 * BN * 16 * 2;            // -dmin m [limb][weight row][16 slots] fp16
+    static constexpr size_t kLds = (size_t)NST * kStage + 2 * (size_t)kRingS + 2 * (size_t)kRingB;
+    static constexpr int kLoadsStep = 4 + kWLoads;            // per wave: activation + weight chunks
+};
 
 __device__ __forceinline__ int q4p_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -507,6 +515,11 @@ __device__ __forceinline__ void g2l16(const void* g, uint8_t* lds_wave_base) {
     const uint32_t l = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds_wave_base;
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(l) : "memory");
 }
+
+// timeline hook for out-of-tree probes (empty in the library)
+#ifndef MXH_Q4P_STAMP
+#define MXH_Q4P_STAMP(t, i)
+#endif
 
 // Workgroup barrier for the pipeline: LDS writes of this wave complete, then
 // s_barrier, with no wait for outstanding global loads (__syncthreads' fence
@@ -542,7 +555,7 @@ __device__ __forceinline__ f16x8 q4p_slice(uint32_t w0, uint32_t w1, int shift, 
     return __builtin_bit_cast(f16x8, r);
 }
 
-template <bool TILED>
+template <bool TILED, int WJ>
 __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* __restrict__ a_hi,
                                                                const uint16_t* __restrict__ a_lo, int lda,
                                                                const uint16_t* __restrict__ s_hi,
@@ -551,10 +564,12 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* _
                                                                const uint8_t* __restrict__ w, float* out, int ldo,
                                                                const float* res, int m, int n, int k, int form,
                                                                int ksteps, float* __restrict__ part) {
-    using namespace q4p;
+    using G = Q4P<WJ>;
+    constexpr int BM = G::BM, BN = G::BN, BK = G::BK, NST = G::NST, kStageA = G::kStageA, kStage = G::kStage;
+    constexpr int kRingS = G::kRingS, kRingB = G::kRingB, kLoadsStep = G::kLoadsStep;
     extern __shared__ __align__(16) uint8_t smem8[];
-    uint8_t* ringS = smem8 + (size_t)NST * kStage;  // [2][kRingB4]
-    uint8_t* ringB = ringS + 2 * kRingB4;            // [2][kRingB4]
+    uint8_t* ringS = smem8 + (size_t)NST * kStage;  // [2][kRingS]
+    uint8_t* ringB = ringS + 2 * kRingS;             // [2][kRingB]
 
     // work item as in gemm_q_f16_kernel (XCD-contiguous ranges)
     const int tn = (n + BN - 1) / BN, tm = (m + BM - 1) / BM, splits = (k / BK + ksteps - 1) / ksteps;
@@ -562,7 +577,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* _
     const int wi = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     if (wi >= total) return;
     const int tx = wi % tn, ty = (wi / tn) % tm, tz = wi / (tn * tm);
-    // 8 waves: 2 along the activation rows (64 each) x 4 along the weight rows (32 each)
+    // 8 waves: 2 along the activation rows (64 each) x 4 along the weight rows (32 WJ each)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wr = wave >> 2, wc = wave & 3;
     const int m0 = ty * BM, n0 = tx * BN;
@@ -582,19 +597,25 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* _
         const int grow = min(m0 + row, m - 1);
         aptr[u] = (limb ? a_lo : a_hi) + (size_t)grow * lda + 8 * c;
     }
-    // weights: this wave's load fills raw chunk wave * 64 + lane (row Q / 3, part Q % 3)
-    int Qw = wave * 64 + lane;
-    if (Qw >= 384) Qw -= 384;  // padding lanes repeat a real chunk
-    const int wpart = Qw % 3;
-    const uint8_t* wrow = w + (size_t)min(n0 + Qw / 3, n - 1) * rb;
-    auto w_addr = [&](int step) -> const uint8_t* {
+    // weights: load u of this wave fills raw chunk Q = 512 u + wave * 64 + lane
+    // (row Q / 3, part Q % 3)
+    int wpart[G::kWLoads];
+    const uint8_t* wrow[G::kWLoads];
+#pragma unroll
+    for (int u = 0; u < G::kWLoads; ++u) {
+        int Qw = 512 * u + wave * 64 + lane;
+        if (Qw >= G::kWChunks) Qw -= G::kWChunks;  // padding lanes repeat a real chunk
+        wpart[u] = Qw % 3;
+        wrow[u] = w + (size_t)min(n0 + Qw / 3, n - 1) * rb;
+    }
+    auto w_addr = [&](int u, int step) -> const uint8_t* {
         const int64_t c = (int64_t)(kb / BK + step);  // 64-element chunk of the row
         if constexpr (TILED) {
             const Q4KTileOffs o = q4k_tile_offsets(c, nblk);
-            return wrow + (wpart == 0 ? o.hd : wpart == 1 ? o.qa : o.qb);
+            return wrow[u] + (wpart[u] == 0 ? o.hd : wpart[u] == 1 ? o.qa : o.qb);
         } else {
             const size_t blk = (size_t)(c >> 2) * 144;
-            return wrow + blk + (wpart == 0 ? 0 : 16 + 32 * (int)(c & 3) + 16 * (wpart - 1));
+            return wrow[u] + blk + (wpart[u] == 0 ? 0 : 16 + 32 * (int)(c & 3) + 16 * (wpart[u] - 1));
         }
     };
     // sub-block sums: this wave's load fills ring chunk wave * 64 + lane
@@ -602,101 +623,122 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* _
     const uint16_t* sptr = ((s_slot >> 8) ? s_lo : s_hi) + (size_t)min(m0 + ((s_slot >> 1) & 127), m - 1) * lds +
                            8 * s_half;
     const int nsb = k / 32;
-    auto issue_stage = [&](int step) {
+    // load q (0 .. kLoadsStep - 1) of a stage: the activation chunks, then the
+    // weight chunks
+    auto issue_load = [&](int step, int q) {
         const int st = min(step, nsteps - 1);  // past the end: the last step again (never read)
         uint8_t* base = smem8 + (size_t)(step % NST) * kStage;
-        const int k0 = kb + st * BK;
+        if (q < 4) g2l16(aptr[q] + kb + st * BK, base + (wave * 4 + q) * 1024);
+        else g2l16(w_addr(q - 4, st), base + kStageA + (512 * (q - 4) + wave * 64) * 16);
+    };
+    auto issue_stage = [&](int step) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) g2l16(aptr[u] + k0, base + (wave * 4 + u) * 1024);
-        g2l16(w_addr(st), base + kStageA + wave * 1024);
+        for (int q = 0; q < kLoadsStep; ++q) issue_load(step, q);
     };
     auto issue_sums = [&](int round) {
         int j0 = kb / 32 + 16 * round;
         // chunks past the row (rounds beyond this work item) read sub-block 0
         if (j0 + 8 * s_half >= nsb) j0 = -8 * s_half;
-        g2l16(sptr + j0, ringS + (size_t)(round & 1) * kRingB4 + wave * 1024);
+        g2l16(sptr + j0, ringS + (size_t)(round & 1) * kRingS + wave * 1024);
     };
 
-    f32x16 acc[2], P[2];
+    f32x16 acc[2][WJ], P[2][WJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][e] = P[i][e] = 0.f;
+        for (int j = 0; j < WJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = P[i][j][e] = 0.f;
 
+    // this lane's weight rows in the tile: block j of the wave
+    int col[WJ];
+#pragma unroll
+    for (int j = 0; j < WJ; ++j) col[j] = wc * 32 * WJ + 32 * j + lr;
     // correction of round r over its first `used` sub-block slots:
     // acc += S . (-dmin m) with S and -dmin m split hi / lo
-    const int col = wc * 32 + lr;  // this lane's weight row in the tile
     auto correction = [&](int r, int used) {
-        const uint8_t* sb = ringS + (size_t)(r & 1) * kRingB4;
-        const uint8_t* bb = ringB + (size_t)(r & 1) * kRingB4;
-        f16x8 sh[2], sl[2];
-        f16x8 bh = *reinterpret_cast<const f16x8*>(bb + col * 32 + hh * 16);
-        f16x8 bl = *reinterpret_cast<const f16x8*>(bb + 4096 + col * 32 + hh * 16);
+        const uint8_t* sb = ringS + (size_t)(r & 1) * kRingS;
+        const uint8_t* bb = ringB + (size_t)(r & 1) * kRingB;
+        f16x8 sh[2], sl[2], bh[WJ], bl[WJ];
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            bh[j] = *reinterpret_cast<const f16x8*>(bb + col[j] * 32 + hh * 16);
+            bl[j] = *reinterpret_cast<const f16x8*>(bb + BN * 32 + col[j] * 32 + hh * 16);
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int row = wr * 64 + i * 32 + lr;
             sh[i] = *reinterpret_cast<const f16x8*>(sb + row * 32 + hh * 16);
-            sl[i] = *reinterpret_cast<const f16x8*>(sb + 4096 + row * 32 + hh * 16);
+            sl[i] = *reinterpret_cast<const f16x8*>(sb + BM * 32 + row * 32 + hh * 16);
         }
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             if (8 * hh + e >= used) {
-                bh[e] = bl[e] = (_Float16)0.f;
+#pragma unroll
+                for (int j = 0; j < WJ; ++j) bh[j][e] = bl[j][e] = (_Float16)0.f;
                 sh[0][e] = sl[0][e] = sh[1][e] = sl[1][e] = (_Float16)0.f;
             }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl[i], bh, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bl, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bh, acc[i], 0, 0, 0);
-        }
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < WJ; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sl[i], bh[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bl[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sh[i], bh[j], acc[i][j], 0, 0, 0);
+            }
     };
 
-    // prologue: round 0's sums, steps 0 and 1
+    // prologue: round 0's sums, the first NST - 1 steps
     issue_sums(0);
-    issue_stage(0);
-    issue_stage(1);
+#pragma unroll
+    for (int q = 0; q < NST - 1; ++q) issue_stage(q);
 
     for (int t = 0; t < nsteps; ++t) {
         // stage t complete: only the loads issued after it may be outstanding
-        if (t == 0 || ((t - 1) & 7) != 1) wait_vm<kLoadsStep>();
-        else wait_vm<kLoadsStep + 1>();
+        // (the later stages in flight, and round sums issued after them)
+        MXH_Q4P_STAMP(t, 0);
+        if (t == 0 || ((t - 1) & 7) != 1) wait_vm<(NST - 2) * kLoadsStep>();
+        else wait_vm<(NST - 2) * kLoadsStep + 1>();
+        MXH_Q4P_STAMP(t, 1);
         q4p_barrier();
+        MXH_Q4P_STAMP(t, 2);
         if (t > 0 && (t & 7) == 0) correction((t >> 3) - 1, 16);
-        issue_stage(t + 2);
-        if ((t & 7) == 1) issue_sums((t >> 3) + 1);
+        issue_stage(t + NST - 1);
+        MXH_Q4P_STAMP(t, 5);
 
         const uint8_t* stg = smem8 + (size_t)(t % NST) * kStage;
         const int k0 = kb + t * BK, g = (k0 >> 6) & 3;
-        // this lane's weight row: header and its 16-byte qs piece
-        f16x8 bw[4];
-        float dcol;
-        {
-            const uint4 hd = *reinterpret_cast<const uint4*>(stg + kStageA + col * 48);
-            const uint4 q = *reinterpret_cast<const uint4*>(stg + kStageA + col * 48 + 16 + 16 * hh);
+        // this lane's weight rows: header and its 16-byte qs piece
+        f16x8 bw[WJ][4];
+        float dcol[WJ];
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) {
+            const uint4 hd = *reinterpret_cast<const uint4*>(stg + kStageA + col[j] * 48);
+            const uint4 q = *reinterpret_cast<const uint4*>(stg + kStageA + col[j] * 48 + 16 + 16 * hh);
             uint32_t scp, mnp;
             k4_pair(hd.y, hd.z, hd.w, g, form, scp, mnp);
             // hardware conversion: d and dmin only scale sums (a NaN payload need not survive)
-            dcol = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xffffu)));
+            dcol[j] = __half2float(__ushort_as_half((uint16_t)(hd.x & 0xffffu)));
             const float dmin = __half2float(__ushort_as_half((uint16_t)(hd.x >> 16)));
             const _Float16 sc0 = (_Float16)(float)(scp & 0xffu), sc1 = (_Float16)(float)(scp >> 8);
             const h2v sv0 = {sc0, sc0}, sv1 = {sc1, sc1};
             const h2v ov0 = {(_Float16)(-1024.f) * sc0, (_Float16)(-1024.f) * sc0};
             const h2v ov1 = {(_Float16)(-1024.f) * sc1, (_Float16)(-1024.f) * sc1};
-            bw[0] = q4p_slice(q.x, q.y, 0, sv0, ov0);
-            bw[1] = q4p_slice(q.z, q.w, 0, sv0, ov0);
-            bw[2] = q4p_slice(q.x, q.y, 4, sv1, ov1);
-            bw[3] = q4p_slice(q.z, q.w, 4, sv1, ov1);
+            bw[j][0] = q4p_slice(q.x, q.y, 0, sv0, ov0);
+            bw[j][1] = q4p_slice(q.z, q.w, 0, sv0, ov0);
+            bw[j][2] = q4p_slice(q.x, q.y, 4, sv1, ov1);
+            bw[j][3] = q4p_slice(q.z, q.w, 4, sv1, ov1);
             if (wr == 0) {
                 // -dmin m of sub-block 2g (lanes of half 0) or 2g + 1 (half 1)
                 const float mt = -(dmin * (float)(hh ? (mnp >> 8) : (mnp & 0xffu)));
                 const uint32_t sp = split_f16(mt);
-                uint16_t* bb = reinterpret_cast<uint16_t*>(ringB + (size_t)((t >> 3) & 1) * kRingB4);
+                uint16_t* bb = reinterpret_cast<uint16_t*>(ringB + (size_t)((t >> 3) & 1) * kRingB);
                 const int slot = 2 * (t & 7) + hh;
-                bb[col * 16 + slot] = (uint16_t)sp;
-                bb[2048 + col * 16 + slot] = (uint16_t)(sp >> 16);
+                bb[col[j] * 16 + slot] = (uint16_t)sp;
+                bb[BN * 16 + col[j] * 16 + slot] = (uint16_t)(sp >> 16);
             }
         }
+        MXH_Q4P_STAMP(t, 3);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int c = (jj & 1) + 2 * hh + 4 * (jj >> 1);
@@ -709,20 +751,26 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* _
                 al[i] = *reinterpret_cast<const f16x8*>(stg + BM * 128 + off);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                P[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[jj], P[i], 0, 0, 0);
-                P[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[jj], P[i], 0, 0, 0);
-            }
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < WJ; ++j) {
+                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j][jj], P[i][j], 0, 0, 0);
+                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][jj], P[i][j], 0, 0, 0);
+                }
         }
+        if ((t & 7) == 1) issue_sums((t >> 3) + 1);
+        MXH_Q4P_STAMP(t, 4);
         if (((k0 + BK) & 255) == 0 || t == nsteps - 1) {
             // end of a super-block: acc += d[n] . P
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    acc[i][e] = fmaf(dcol, P[i][e], acc[i][e]);
-                    P[i][e] = 0.f;
-                }
+                for (int j = 0; j < WJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        acc[i][j][e] = fmaf(dcol[j], P[i][j][e], acc[i][j][e]);
+                        P[i][j][e] = 0.f;
+                    }
         }
     }
     wait_vm<0>();
@@ -735,20 +783,23 @@ __global__ __launch_bounds__(512, 1) void gemm_q4k_pipe_kernel(const uint16_t* _
     const bool partial = splits > 1;
     float* dst = partial ? part + (size_t)tz * m * n : out;
     const int ld = partial ? n : ldo;
-    const int ocol = n0 + col;
-    if (ocol < n) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < WJ; ++j) {
+        const int ocol = n0 + col[j];
+        if (ocol < n) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
-                if (row < m) {
-                    const size_t o = (size_t)row * ld + ocol;
-                    const float v = acc[i][e] * rscale[row];
-                    if (partial) dst[o] = v;
-                    else dst[o] = res ? v + res[o] : v;
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wr * 64 + i * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
+                    if (row < m) {
+                        const size_t o = (size_t)row * ld + ocol;
+                        const float v = acc[i][j][e] * rscale[row];
+                        if (partial) dst[o] = v;
+                        else dst[o] = res ? v + res[o] : v;
+                    }
                 }
-            }
+        }
     }
 }
 
@@ -967,15 +1018,16 @@ int q4p_splits(int tiles, int steps, int n_cu, size_t mn, size_t part_floats) {
     return best;
 }
 
-template <bool TILED>
+template <bool TILED, int WJ>
 int gemm_q4k_pipe_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi,
                          const uint16_t* s_lo, int lds, const float* rscale, const uint8_t* w, float* out, int ldo,
                          const float* res, int m, int n, int k, int form, float* part, size_t part_floats,
                          hipStream_t st) {
+    using G = Q4P<WJ>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void*)gemm_q4k_pipe_kernel<TILED>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)q4p::kLds) != hipSuccess)
+        if (hipFuncSetAttribute((const void*)gemm_q4k_pipe_kernel<TILED, WJ>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)G::kLds) != hipSuccess)
             return MXH_ERR_HIP;
         attr_set = true;
     }
@@ -986,16 +1038,56 @@ int gemm_q4k_pipe_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, co
             hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             n_cu = 256;
     }
-    const int tn = (n + q4p::BN - 1) / q4p::BN, tm = (m + q4p::BM - 1) / q4p::BM, steps = k / q4p::BK;
+    const int tn = (n + G::BN - 1) / G::BN, tm = (m + G::BM - 1) / G::BM, steps = k / G::BK;
     const int splits = q4p_splits(tn * tm, steps, n_cu, (size_t)m * n, part ? part_floats : 0);
     const int items = tn * tm * splits;
     const dim3 grid((unsigned)((items + 7) / 8 * 8));
-    hipLaunchKernelGGL((gemm_q4k_pipe_kernel<TILED>), grid, dim3(512), q4p::kLds, st, a_hi, a_lo, lda, s_hi, s_lo,
+    hipLaunchKernelGGL((gemm_q4k_pipe_kernel<TILED, WJ>), grid, dim3(512), G::kLds, st, a_hi, a_lo, lda, s_hi, s_lo,
                        lds, rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
     if (splits > 1)
         hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
                            res, m, n);
     return MXH_OK;
+}
+
+// Weight-row blocks per wave of the pipelined Q4_K GEMM for a shape: the
+// tiling with the lower estimate of rounds x (K steps per work item + 8, the
+// pipeline's fill and epilogue), a 256-row step counted as 1.7 128-row ones
+// (measured at M = 512: 256 rows faster for q|k|v 6144 x 4096 and down
+// 4096 x 12288, slower for o 4096 x 4096 and gate|up 24576 x 4096, whose
+// 384 wide tiles take two rounds on 256 CUs).
+static int q4p_wj(int m, int n, int k, size_t part_floats) {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n_cu = 256;
+    }
+    double best = 0.0;
+    int wj = 1;
+    for (int j = 1; j <= 2; ++j) {
+        const int bn = 128 * j, tiles = ((n + bn - 1) / bn) * ((m + 127) / 128), steps = k / 64;
+        const int s = q4p_splits(tiles, steps, n_cu, (size_t)m * n, part_floats);
+        const long rounds = ((long)tiles * s + n_cu - 1) / n_cu;
+        const double cost = (double)rounds * (steps / s + 8) * (j == 2 ? 1.7 : 1.0);
+        if (j == 1 || cost < best) {
+            best = cost;
+            wj = j;
+        }
+    }
+    return wj;
+}
+
+template <bool TILED>
+int gemm_q4k_pipe_run(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const uint16_t* s_hi, const uint16_t* s_lo,
+                      int lds, const float* rscale, const uint8_t* w, float* out, int ldo, const float* res, int m,
+                      int n, int k, int form, float* part, size_t part_floats, hipStream_t st) {
+    if (q4p_wj(m, n, k, part ? part_floats : 0) == 1)
+        return gemm_q4k_pipe_launch<TILED, 1>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, w, out, ldo, res, m, n, k,
+                                              form, part, part_floats, st);
+    return gemm_q4k_pipe_launch<TILED, 2>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, w, out, ldo, res, m, n, k, form,
+                                          part, part_floats, st);
 }
 
 // the pipelined kernel's 16-byte direct loads need 16-byte aligned rows
@@ -1064,9 +1156,9 @@ int gemm_q_f16_run(int type, const uint16_t* a_hi, const uint16_t* a_lo, int lda
     const uint8_t* wb = (const uint8_t*)w;
     if ((type == MXH_Q4_K || type == MXH_Q4_K_TILED) && q4p_aligned(a_hi, a_lo, lda, s_hi, s_lo, lds, w)) {
         if (type == MXH_Q4_K_TILED)
-            return gemm_q4k_pipe_launch<true>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
+            return gemm_q4k_pipe_run<true>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k,
                                               form, part, part_floats, st);
-        return gemm_q4k_pipe_launch<false>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
+        return gemm_q4k_pipe_run<false>(a_hi, a_lo, lda, s_hi, s_lo, lds, rscale, wb, out, ldo, res, m, n, k, form,
                                            part, part_floats, st);
     }
     if (q4_wide_tiles(m, n))
