@@ -59,36 +59,46 @@ constexpr int kAttnMaxGroup = 8;    // q heads per kv head
 constexpr int kAttnSplitPos = 256;  // positions per workgroup (split) before the next split opens
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
-// wave; `src` is the raw projection, the result goes to dst (LDS).
-__device__ void head_prep(const float* __restrict__ src, const float* __restrict__ bias,
-                          const float* __restrict__ nw, const double* __restrict__ cs, float* dst, int hd, float eps,
-                          int neox) {
+// wave in two parts: head_fetch requests every global input (so a kernel can
+// issue it ahead of its other loads, which complete in order), head_finish
+// computes into dst (LDS).  `src` is the raw projection; hd <= 128, lane l
+// holds elements l and l + 64.
+struct HeadIn {
+    float v[2], g[2];
+    double c, s;
+};
+
+__device__ __forceinline__ HeadIn head_fetch(const float* __restrict__ src, const float* __restrict__ bias,
+                                             const float* __restrict__ nw, const double* __restrict__ cs, int hd) {
     const int lane = threadIdx.x & 63, half = hd / 2;
-    // every global input is requested before any arithmetic
-    float v[2] = {0.f, 0.f}, g[2] = {1.f, 1.f};  // hd <= 128: elements lane and lane + 64
-    double c = 1.0, s = 0.0;
+    HeadIn in{{0.f, 0.f}, {1.f, 1.f}, 1.0, 0.0};
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int t = lane + 64 * r;
         if (t < hd) {
-            v[r] = src[t] + (bias ? bias[t] : 0.f);
-            if (nw) g[r] = nw[t];
+            in.v[r] = src[t] + (bias ? bias[t] : 0.f);
+            if (nw) in.g[r] = nw[t];
         }
     }
     if (lane < half) {
-        c = cs[2 * lane];
-        s = cs[2 * lane + 1];
+        in.c = cs[2 * lane];
+        in.s = cs[2 * lane + 1];
     }
-    if (nw) {
-        const double ss = wave_sum_d_all((double)v[0] * v[0] + (double)v[1] * v[1]);
+    return in;
+}
+
+__device__ void head_finish(HeadIn in, bool norm, float* dst, int hd, float eps, int neox) {
+    const int lane = threadIdx.x & 63, half = hd / 2;
+    if (norm) {
+        const double ss = wave_sum_d_all((double)in.v[0] * in.v[0] + (double)in.v[1] * in.v[1]);
         const double inv = 1.0 / sqrt(ss / (double)hd + (double)eps);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) v[r] = (float)((double)v[r] * inv) * g[r];
+        for (int r = 0; r < 2; ++r) in.v[r] = (float)((double)in.v[r] * inv) * in.g[r];
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int t = lane + 64 * r;
-        if (t < hd) dst[t] = v[r];
+        if (t < hd) dst[t] = in.v[r];
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -97,9 +107,15 @@ __device__ void head_prep(const float* __restrict__ src, const float* __restrict
     if (lane < half) {
         const int ia = neox ? lane : 2 * lane, ib = neox ? lane + half : 2 * lane + 1;
         const double x0 = dst[ia], x1 = dst[ib];
-        dst[ia] = (float)(x0 * c - x1 * s);
-        dst[ib] = (float)(x0 * s + x1 * c);
+        dst[ia] = (float)(x0 * in.c - x1 * in.s);
+        dst[ib] = (float)(x0 * in.s + x1 * in.c);
     }
+}
+
+__device__ void head_prep(const float* __restrict__ src, const float* __restrict__ bias,
+                          const float* __restrict__ nw, const double* __restrict__ cs, float* dst, int hd, float eps,
+                          int neox) {
+    head_finish(head_fetch(src, bias, nw, cs, hd), nw != nullptr, dst, hd, eps, neox);
 }
 
 // sum over aligned groups of LPP lanes (a power of two <= 16); every lane of
@@ -218,23 +234,27 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
             vraw[b][i] = in ? *reinterpret_cast<const uint4*>(a.vc + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
         }
     };
-    // the first DB chunks of this wave are requested before the q
-    // preparation (they do not depend on it)
+    // wave 0: q; in the last split wave 1: k, wave 2: v of the current
+    // token.  Their inputs are requested first, then the wave's first DB
+    // chunks (loads complete in order, so the preparation does not wait for
+    // the chunks).
+    const double* cs = a.rope_cs + (size_t)pos * HD;  // (hd/2) pairs of (cos, sin)
+    const bool prep = wave == 0 || (last && wave <= 2), is_k = wave == 1;
+    const size_t off = wave == 0 ? (size_t)qh * HD : (is_k ? qd : qd + kvd) + (size_t)g * HD;
+    HeadIn hin{};
+    if (prep)
+        hin = head_fetch(a.qkv + off, a.bias ? a.bias + off : nullptr,
+                         wave == 0 ? a.q_norm : is_k ? a.k_norm : nullptr, cs, HD);
 #pragma unroll
     for (int b = 0; b < DB; ++b)
         if (wave + NW * b < nch) load(b, wave + NW * b);
     MXH_ATTN_STAMP(2);
 
-    // wave 0: q; in the last split wave 1: k, wave 2: v of the current token
-    const double* cs = a.rope_cs + (size_t)pos * HD;  // (hd/2) pairs of (cos, sin)
     if (wave == 0) {
-        head_prep(a.qkv + (size_t)qh * HD, a.bias ? a.bias + (size_t)qh * HD : nullptr, a.q_norm, cs, qs, HD, a.eps,
-                  a.neox);
-    } else if (last && wave <= 2) {
-        const bool is_k = wave == 1;
-        const size_t off = (is_k ? qd : qd + kvd) + (size_t)g * HD;
+        head_finish(hin, a.q_norm != nullptr, qs, HD, a.eps, a.neox);
+    } else if (prep) {
         if (is_k) {
-            head_prep(a.qkv + off, a.bias ? a.bias + off : nullptr, a.k_norm, cs, kvt, HD, a.eps, a.neox);
+            head_finish(hin, a.k_norm != nullptr, kvt, HD, a.eps, a.neox);
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         }
@@ -242,11 +262,14 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
         // per kv head
         const bool append = qh % group == 0;
         __half* cache = (is_k ? a.kc : a.vc) + (size_t)pos * kvd + (size_t)g * HD;
-        for (int t = lane; t < HD; t += 64) {
-            const float v = is_k ? kvt[t] : a.qkv[off + t] + (a.bias ? a.bias[off + t] : 0.f);
-            const __half hv = __float2half_rn(v);
-            kvh[is_k ? 0 : 1][t] = hv;
-            if (append) cache[t] = hv;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int t = lane + 64 * r;
+            if (t < HD) {
+                const __half hv = __float2half_rn(is_k ? kvt[t] : hin.v[r]);
+                kvh[is_k ? 0 : 1][t] = hv;
+                if (append) cache[t] = hv;
+            }
         }
     }
     __syncthreads();
@@ -522,21 +545,37 @@ __global__ void attention_merge_kernel(const float* __restrict__ part, int S, in
     if (i >= nh * hd) return;
     const int h = i / hd, t = i % hd;
     const float* ml = part + (size_t)nh * S * hd + (size_t)h * S * 2;
+    const float* pv = part + (size_t)h * S * hd + t;
+    // eight splits' loads in flight at a time
     float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+    for (int s0 = 0; s0 < S; s0 += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (s0 + u < S) M = fmaxf(M, ml[2 * (s0 + u)]);
+    }
     float den = 0.f, v = 0.f;
-    for (int s = 0; s < S; ++s) {
-        if (ml[2 * s] == -INFINITY) continue;
-        const float w = __builtin_amdgcn_exp2f(ml[2 * s] - M);
-        den = fmaf(w, ml[2 * s + 1], den);
-        v = fmaf(w, part[((size_t)h * S + s) * hd + t], v);
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        float2 mu[8];
+        float vu[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const bool in = s0 + u < S;
+            mu[u] = in ? *reinterpret_cast<const float2*>(ml + 2 * (s0 + u)) : make_float2(-INFINITY, 0.f);
+            vu[u] = in ? pv[(size_t)(s0 + u) * hd] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float w = mu[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mu[u].x - M);
+            den = fmaf(w, mu[u].y, den);
+            v = fmaf(w, vu[u], v);
+        }
     }
     att[i] = v / den;
 }
 
 int attention_merge_launch(const float* part, int splits, int nh, int hd, float* att, hipStream_t st) {
     if (splits < 1 || nh < 1 || hd < 1) return MXH_ERR_ARG;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3((nh * hd + 255) / 256), dim3(256), 0, st, part, splits, nh, hd, att);
+    hipLaunchKernelGGL(attention_merge_kernel, dim3((nh * hd + 63) / 64), dim3(64), 0, st, part, splits, nh, hd, att);
     return MXH_OK;
 }
 
