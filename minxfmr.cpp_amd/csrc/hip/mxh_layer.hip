@@ -530,9 +530,9 @@ int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
     const dim3 grid(a.nh, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
     switch (a.hd) {
-    case 32: hipLaunchKernelGGL((attention_kernel<4, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    case 64: hipLaunchKernelGGL((attention_kernel<8, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    default: hipLaunchKernelGGL((attention_kernel<16, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 32: hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 64: hipLaunchKernelGGL((attention_kernel<8, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    default: hipLaunchKernelGGL((attention_kernel<16, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
     }
     return MXH_OK;
 }
