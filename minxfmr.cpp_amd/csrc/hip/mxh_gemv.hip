@@ -46,6 +46,7 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
 constexpr int kShortSteps = 3;  // steps per wave of the short form
+
 constexpr int kThreads = 64 * kWaves;
 
 // sum of the per-wave partials in a fixed order
@@ -968,10 +969,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     };
     Cursor ci{0, 0}, cc{0, 0};
     if constexpr (NS > 0) {
-        // All of a wave's steps are issued right after the x loads, so every
-        // weight byte of the wave is in flight during staging, and each step
-        // waits for a fixed count of younger loads, in straight-line code
-        // whose waits the compiler's own analysis leaves alone.
+        // The first step's weight loads are issued right after the x loads,
+        // the other steps' right after the staging arithmetic, and each step
+        // then waits for a fixed count of younger loads, in straight-line
+        // code whose waits the compiler's own analysis leaves alone.  A wave
+        // issues its loads in order and stalls at issue while the CU's memory
+        // queue is full; with every step issued before the staging (24 loads
+        // per wave) the staging arithmetic waited behind those stalls
+        // (decode 551 tok/s against 579 with one step first; none first: 543).
         static_assert(NS * kL <= 63, "short form: every step's loads in flight at once");
         Step sb[NS];
         auto issue_all = [&] {
@@ -979,8 +984,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             // so x is not queued behind weights in the CU's memory pipeline
             // (a bare s_barrier: no wait for the loads themselves)
             __builtin_amdgcn_s_barrier();
-            for_each_k([&](auto kc) { issue(ci, sb[decltype(kc)::value]); }, std::make_integer_sequence<int, NS>{});
-            wait_vmcnt<NS * kL>();
+            issue(ci, sb[0]);
+            wait_vmcnt<kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
             stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
@@ -991,17 +996,22 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             issue_all();
             stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
+        for_each_k(
+            [&](auto kc) {
+                if constexpr (decltype(kc)::value > 0) issue(ci, sb[decltype(kc)::value]);
+            },
+            std::make_integer_sequence<int, NS>{});
         consume_steps<0, NS, kL>([&](auto kc) { consume(cc, sb[decltype(kc)::value]); }, total);
         wait_vmcnt<0>();  // loads of steps past the end
     } else {
         Step s0, s1, s2;
-        // the first two steps' weight loads do not depend on x: they are
-        // issued right after the x loads, so both latencies overlap, and the
-        // staging arithmetic waits for x only
+        // the first step's weight loads do not depend on x: they are issued
+        // right after the x loads, so both latencies overlap, and the staging
+        // arithmetic waits for x only; the second step's follow the staging
+        // (two steps before it: 580 against 588 tok/s)
         auto issue_first = [&] {
             issue(ci, s0);
-            issue(ci, s1);
-            wait_vmcnt<kL2>();
+            wait_vmcnt<kL1>();
         };
         if constexpr (MODE == GEMV_ATTN) {
             stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
@@ -1012,6 +1022,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             issue_first();
             stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
+        issue(ci, s1);
         // before consuming a step, wait until only the loads issued after it
         // (0, 1 or 2 steps) may be outstanding
         for (int it = 0; it < total; it += 3) {
