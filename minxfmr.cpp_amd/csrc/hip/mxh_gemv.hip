@@ -833,20 +833,7 @@ __device__ __forceinline__ void for_each_k(F&& f, std::integer_sequence<int, K..
     (f(std::integral_constant<int, K>{}), ...);
 }
 
-// Consume steps K .. NS-1 of the short form: step K waits until only the
-// (NS - 1 - K) later steps' loads may be outstanding.
-template <int K, int NS, int KL, class F>
-__device__ __forceinline__ void consume_steps(F&& consume_k, int total) {
-    if constexpr (K < NS) {
-        if (K < total) {
-            wait_vmcnt<(NS - 1 - K) * KL>();
-            consume_k(std::integral_constant<int, K>{});
-            consume_steps<K + 1, NS, KL>(consume_k, total);
-        }
-    }
-}
-
-// NS = 0: persistent loop, two steps of loads ahead.  NS > 0: short form,
+// NS = 0: persistent loop, one step of loads ahead.  NS > 0: short form,
 // at most NS steps per wave (the launcher sizes the grid for it).
 template <template <int> class T, int R, int MODE, int NS>
 // The arguments a wave needs first (weights, x, norm weight, n, k) also come
@@ -884,9 +871,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     float best = -INFINITY;
     int best_i = 0x7fffffff;
 
-    // (chunk step j, row-group ordinal g) cursors: one issues weight loads two
-    // steps ahead, one consumes; the loop is unrolled by three so the three
-    // register buffers keep fixed names (no copies, no dynamic indexing)
+    // (chunk step j, row-group ordinal g) cursors: one issues weight loads
+    // ahead, one consumes; the loops are unrolled so the register buffers
+    // keep fixed names (no copies, no dynamic indexing)
     struct Cursor {
         int j, g;
     };
@@ -900,7 +887,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     // PLAIN mode also prefetches the residual of the row group with each step
     constexpr bool kRes = MODE == GEMV_PLAIN || MODE == GEMV_ATTN;
     constexpr int kL = Ty::kLoads * R + (kRes ? kOut : 0);  // vector loads per step
-    constexpr int kL1 = kL < 63 ? kL : 63, kL2 = 2 * kL < 63 ? 2 * kL : 63;
+    static_assert(kL <= 63, "a step's loads fit the wait counter");
     const float* res_src = a.res ? a.res : a.y;  // (not used without a residual)
     struct Step {
         Buf b;
@@ -974,22 +961,24 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     Cursor ci{0, 0}, cc{0, 0};
     if constexpr (NS > 0) {
         // The first step's weight loads are issued right after the x loads,
-        // the other steps' right after the staging arithmetic, and each step
-        // then waits for a fixed count of younger loads, in straight-line
-        // code whose waits the compiler's own analysis leaves alone.  A wave
-        // issues its loads in order and stalls at issue while the CU's memory
-        // queue is full; with every step issued before the staging (24 loads
-        // per wave) the staging arithmetic waited behind those stalls
-        // (decode 551 tok/s against 579 with one step first; none first: 543).
+        // and each later step's just before the step ahead of it is consumed,
+        // in straight-line code with fixed load counts whose waits the
+        // compiler's own analysis leaves alone.  A wave issues its loads in
+        // order and stalls at issue while the CU's memory queue is full, so
+        // loads queued ahead of the staging or of a step's arithmetic delay
+        // that arithmetic: every step issued before the staging (24 loads per
+        // wave) ran at 551 tok/s, one step first 579, none first 543.
         static_assert(NS * kL <= 63, "short form: every step's loads in flight at once");
+        // steps of loads issued ahead of consumption (two: 589 against 600-606 tok/s)
+        constexpr int kAhead = 1;
         Step sb[NS];
         auto issue_all = [&] {
             // every wave's x loads are issued before any wave's weight loads,
             // so x is not queued behind weights in the CU's memory pipeline
             // (a bare s_barrier: no wait for the loads themselves)
             __builtin_amdgcn_s_barrier();
-            issue(ci, sb[0]);
-            wait_vmcnt<kL>();
+            for_each_k([&](auto kc) { issue(ci, sb[decltype(kc)::value]); }, std::make_integer_sequence<int, kAhead>{});
+            wait_vmcnt<kAhead * kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
             stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
@@ -1000,22 +989,31 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             issue_all();
             stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
+        // then step K + kAhead is issued before step K is consumed: a wave
+        // never has more than kAhead + 1 steps of loads queued, so its
+        // consumption does not wait behind stalled issues (all steps queued
+        // after the staging: 589 against 606 tok/s)
         for_each_k(
             [&](auto kc) {
-                if constexpr (decltype(kc)::value > 0) issue(ci, sb[decltype(kc)::value]);
+                constexpr int K = decltype(kc)::value;
+                if constexpr (K + kAhead < NS) {
+                    issue(ci, sb[K + kAhead]);
+                    wait_vmcnt<kAhead * kL>();
+                } else {
+                    wait_vmcnt<(NS - 1 - K) * kL>();
+                }
+                if (K < total) consume(cc, sb[K]);
             },
             std::make_integer_sequence<int, NS>{});
-        consume_steps<0, NS, kL>([&](auto kc) { consume(cc, sb[decltype(kc)::value]); }, total);
-        wait_vmcnt<0>();  // loads of steps past the end
     } else {
-        Step s0, s1, s2;
+        Step s0, s1;
         // the first step's weight loads do not depend on x: they are issued
         // right after the x loads, so both latencies overlap, and the staging
-        // arithmetic waits for x only; the second step's follow the staging
-        // (two steps before it: 580 against 588 tok/s)
+        // arithmetic waits for x only (two steps before it: 580 against 588
+        // tok/s)
         auto issue_first = [&] {
             issue(ci, s0);
-            wait_vmcnt<kL1>();
+            wait_vmcnt<kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
             stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
@@ -1026,37 +1024,25 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             issue_first();
             stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
-        issue(ci, s1);
-        // before consuming a step, wait until only the loads issued after it
-        // (0, 1 or 2 steps) may be outstanding
-        for (int it = 0; it < total; it += 3) {
-            if (it + 2 < total) {
-                issue(ci, s2);
-                wait_vmcnt<kL2>();
+        // then one step ahead: step j + 1 is issued just before step j is
+        // consumed (two steps ahead measured the same at 12-350 MB shapes and
+        // 1-2% slower on the lm-head)
+        for (int it = 0; it < total; it += 2) {
+            if (it + 1 < total) {
+                issue(ci, s1);
+                wait_vmcnt<kL>();
             } else {
-                wait_vmcnt<kL1>();  // step it + 1 (or a repeat of step it) is younger
+                wait_vmcnt<0>();
             }
             consume(cc, s0);
             if (it + 1 >= total) break;
-            if (it + 3 < total) {
+            if (it + 2 < total) {
                 issue(ci, s0);
-                wait_vmcnt<kL2>();
-            } else if (it + 2 < total) {
-                wait_vmcnt<kL1>();
+                wait_vmcnt<kL>();
             } else {
                 wait_vmcnt<0>();
             }
             consume(cc, s1);
-            if (it + 2 >= total) break;
-            if (it + 4 < total) {
-                issue(ci, s1);
-                wait_vmcnt<kL2>();
-            } else if (it + 3 < total) {
-                wait_vmcnt<kL1>();
-            } else {
-                wait_vmcnt<0>();
-            }
-            consume(cc, s2);
         }
     }
     if constexpr (MODE == GEMV_ARGMAX) {
