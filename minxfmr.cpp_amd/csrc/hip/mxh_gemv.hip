@@ -46,9 +46,10 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup
 constexpr int kShortSteps = 3;  // steps per wave of the short form
-// the SwiGLU (gate|up) short form: 163 VGPRs, three workgroups per CU, so
-// 768 workgroups of four waves take the Qwen3-8B gate|up rows in one round
-// (591 against 587 tok/s for the loop form)
+// the SwiGLU (gate|up) short form: 768 workgroups of four waves (three per
+// CU) take the Qwen3-8B gate|up rows in one round (3, 5, 6, 12 steps:
+// 598.6, 586.0, 599-605, 578.0 against 599-602 tok/s; 6 was 1-2% slower on
+// the smaller models)
 constexpr int kSiluShortSteps = 4;
 
 constexpr int kThreads = 64 * kWaves;
@@ -968,9 +969,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
         // loads queued ahead of the staging or of a step's arithmetic delay
         // that arithmetic: every step issued before the staging (24 loads per
         // wave) ran at 551 tok/s, one step first 579, none first 543.
-        static_assert(NS * kL <= 63, "short form: every step's loads in flight at once");
         // steps of loads issued ahead of consumption (two: 589 against 600-606 tok/s)
         constexpr int kAhead = 1;
+        static_assert((kAhead + 1) * kL <= 63, "short form: the loads in flight fit the wait counter");
         Step sb[NS];
         auto issue_all = [&] {
             // every wave's x loads are issued before any wave's weight loads,
@@ -992,7 +993,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
         // then step K + kAhead is issued before step K is consumed: a wave
         // never has more than kAhead + 1 steps of loads queued, so its
         // consumption does not wait behind stalled issues (all steps queued
-        // after the staging: 589 against 606 tok/s)
+        // after the staging: 589 against 606 tok/s).  Steps past the wave's
+        // last are issued as well: branching between two wait counts there
+        // let the compiler add waits of its own (559 against 599 tok/s).
         for_each_k(
             [&](auto kc) {
                 constexpr int K = decltype(kc)::value;
@@ -1134,7 +1137,7 @@ int resident_grid(const void* kernel, size_t lds) {
 // quantized formats, whose staging merges the attention partials)
 template <template <int> class T, int R, int NS>
 const void* kernel_for(int mode) {
-    if constexpr (NS == kSiluShortSteps) {
+    if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {
         return (const void*)gemv_kernel<T, R, GEMV_SILU, NS>;  // SwiGLU only
     } else {
         if (mode == GEMV_SILU) return (const void*)gemv_kernel<T, R, GEMV_SILU, NS>;
@@ -1149,7 +1152,7 @@ const void* kernel_for(int mode) {
 // launch of a PLAIN, SILU or ATTN instance
 template <template <int> class T, int R, int NS>
 void launch_mode(int mode, unsigned grid, size_t lds, const GemvArgs& a, hipStream_t st) {
-    if constexpr (NS == kSiluShortSteps) {  // SwiGLU only
+    if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {  // SwiGLU only
         hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, NS>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x,
                            a.norm_w, a.n, a.k, a);
     } else {
@@ -1189,7 +1192,7 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
         if (mode != GEMV_ARGMAX && grid_cap <= 0 && cpl <= 3) {
             auto try_short = [&](auto nsc) -> bool {
                 constexpr int NSv = decltype(nsc)::value;
-                if constexpr (NSv * kLmax > 63) {
+                if constexpr (2 * kLmax > 63) {
                     return false;
                 } else {
                     if (NSv < cpl) return false;  // a row group's chunk steps exceed the form
@@ -1202,7 +1205,13 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
                     return true;
                 }
             };
-            if (mode == GEMV_SILU && try_short(std::integral_constant<int, kSiluShortSteps>{})) return MXH_OK;
+            // the longer SwiGLU form only where one workgroup per CU would
+            // leave waves more than kShortSteps steps (a wave issues the steps
+            // past its last too, to keep the wait counts fixed)
+            const int64_t steps_one_per_cu = (n_groups + (int64_t)n_cu * kWaves - 1) / ((int64_t)n_cu * kWaves) * cpl;
+            if (mode == GEMV_SILU && steps_one_per_cu > kShortSteps &&
+                try_short(std::integral_constant<int, kSiluShortSteps>{}))
+                return MXH_OK;
             if (try_short(std::integral_constant<int, kShortSteps>{})) return MXH_OK;
         }
     }
