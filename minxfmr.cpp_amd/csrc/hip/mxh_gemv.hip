@@ -64,10 +64,11 @@ __device__ __forceinline__ double rsqrt_d(double v) {
     return r * (1.5 - 0.5 * v * r * r);
 }
 
+template <int W>
 __device__ __forceinline__ double block_sum(const double* red) {
     double s = 0.0;
 #pragma unroll
-    for (int w = 0; w < kWaves; w += 2) s += red[w] + red[w + 1];
+    for (int w = 0; w < W; w += 2) s += red[w] + red[w + 1];
     return s;
 }
 
@@ -153,16 +154,20 @@ __host__ __device__ constexpr int limb_dwords(int k) { return k / 4 + k / 16; }
 // The arrays are sized for K rounded up to whole staging passes (1024
 // elements: 4 per thread), so a pass past K writes zeros into padding
 // instead of needing a per-lane guard.
-__host__ __device__ constexpr int xq_cap(int k) { return (k + kThreads * 4 - 1) / (kThreads * 4) * (kThreads * 4); }
+// (W waves per workgroup: one pass is 256 W elements)
+template <int W>
+__host__ __device__ constexpr int xq_cap(int k) { return (k + 256 * W - 1) / (256 * W) * (256 * W); }
+template <int W>
 __host__ __device__ constexpr int xq_dwords(int k) {
-    return 3 * limb_dwords(xq_cap(k)) + xq_cap(k) / 32 + xq_cap(k) / 16;
+    return 3 * limb_dwords(xq_cap<W>(k)) + xq_cap<W>(k) / 32 + xq_cap<W>(k) / 16;
 }
 
+template <int W>
 __device__ __forceinline__ XQ xq_view(const float* smem, int k) {
     const uint32_t* lo = reinterpret_cast<const uint32_t*>(smem);
-    const int n = limb_dwords(xq_cap(k));
+    const int n = limb_dwords(xq_cap<W>(k));
     return XQ{lo, lo + n, lo + 2 * n, reinterpret_cast<const float*>(lo + 3 * n),
-              reinterpret_cast<const float*>(lo + 3 * n) + xq_cap(k) / 32};
+              reinterpret_cast<const float*>(lo + 3 * n) + xq_cap<W>(k) / 32};
 }
 
 __device__ __forceinline__ uint4 lds16(const uint32_t* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -535,8 +540,10 @@ struct F32W {
 // reference rmsnorm float(x / sqrt(mean(x^2) + eps)) * w (rmsnorm.cpp:5-26,
 // transformer.cpp:189-214); the sum of squares is a double block reduction
 // in a fixed order, so every workgroup computes identical inputs.
+template <int W>
 __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, const float* __restrict__ nw,
                                         int k, float eps, double* red) {
+    constexpr int kThreads = 64 * W;
     if (!nw) {
 #pragma unroll 4
         for (int e = threadIdx.x * 4; e < k; e += kThreads * 4)
@@ -554,7 +561,7 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    const double inv = 1.0 / sqrt(block_sum(red) / (double)k + (double)eps);
+    const double inv = 1.0 / sqrt(block_sum<W>(red) / (double)k + (double)eps);
     // each thread rescales the elements it staged
     for (int e = threadIdx.x * 4; e < k; e += kThreads * 4) {
         float4 v = *reinterpret_cast<const float4*>(xs + xpad(e));
@@ -583,8 +590,9 @@ __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, 
 // lo = byte 0 of Y xor 0x80, mid = byte 1 of Y xor 0x80 and hi = byte 2 of Y,
 // gathered four elements to a dword by byte permutes; the sub-block sums of
 // X are exact in int32 (16 values below 2^23 each).
-template <int NB>
+template <int W, int NB>
 __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, int k, uint32_t* smem) {
+    constexpr int kPass = 256 * W;  // elements between a thread's units
     // |x| as integers: for non-negative floats the integer order is the
     // float order, and v_max_u32 takes a DPP operand directly; a NaN among
     // the bit patterns is the largest, so its sub-block's scale becomes NaN
@@ -622,9 +630,10 @@ __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, in
     for (int u = 0; u < NB; ++u) t[u] += dpp_i<0xb1>(t[u]);
 #pragma unroll
     for (int u = 0; u < NB; ++u) t[u] += dpp_i<0x4e>(t[u]);
-    // unit u sits 1024 u elements on: 320 u padded limb dwords, 32 u scales
-    // and 64 u sums further, so one address per array serves every unit
-    const int cap = xq_cap(k), n = limb_dwords(cap);
+    // unit u sits kPass u elements on: limb_dwords(kPass) u padded limb
+    // dwords, kPass / 32 u scales and kPass / 16 u sums further, so one
+    // address per array serves every unit
+    const int cap = xq_cap<W>(k), n = limb_dwords(cap);
     uint32_t* lo = smem + limb(e0 >> 2);
     uint32_t* mid = lo + n;
     uint32_t* hi = lo + 2 * n;
@@ -632,18 +641,18 @@ __device__ __forceinline__ void quantize_units(const float4 (&v)[NB], int e0, in
     uint32_t* sum16 = smem + 3 * n + cap / 32 + (e0 >> 4);
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-        if (u > 0 && 1024 * u >= cap) break;  // (uniform) passes beyond the arrays
+        if (u > 0 && kPass * u >= cap) break;  // (uniform) passes beyond the arrays
         const uint32_t y0 = (uint32_t)X[u][0] + 0x8080u, y1 = (uint32_t)X[u][1] + 0x8080u;
         const uint32_t y2 = (uint32_t)X[u][2] + 0x8080u, y3 = (uint32_t)X[u][3] + 0x8080u;
         const uint32_t a01 = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // y0.b0 y0.b1 y1.b0 y1.b1
         const uint32_t a23 = __builtin_amdgcn_perm(y3, y2, 0x05040100u);
-        lo[320 * u] = __builtin_amdgcn_perm(a23, a01, 0x06040200u) ^ 0x80808080u;
-        mid[320 * u] = __builtin_amdgcn_perm(a23, a01, 0x07050301u) ^ 0x80808080u;
+        lo[limb_dwords(kPass) * u] = __builtin_amdgcn_perm(a23, a01, 0x06040200u) ^ 0x80808080u;
+        mid[limb_dwords(kPass) * u] = __builtin_amdgcn_perm(a23, a01, 0x07050301u) ^ 0x80808080u;
         const uint32_t h01 = __builtin_amdgcn_perm(y1, y0, 0x06020602u);  // y0.b2 y1.b2 (twice)
         const uint32_t h23 = __builtin_amdgcn_perm(y3, y2, 0x06020602u);
-        hi[320 * u] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
-        scale[32 * u] = __float_as_uint(sc[u]);
-        sum16[64 * u] = __float_as_uint(sc[u] * (float)t[u]);
+        hi[limb_dwords(kPass) * u] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
+        scale[kPass / 32 * u] = __float_as_uint(sc[u]);
+        sum16[kPass / 16 * u] = __float_as_uint(sc[u] * (float)t[u]);
     }
 }
 
@@ -714,11 +723,11 @@ struct AttnIn {
     }
 };
 
-template <int NB, bool NORM, class XS, class F>
+template <int W, int NB, bool NORM, class XS, class F>
 __device__ __forceinline__ void stage_xq_nb(float* smem, const XS& xs, const float* __restrict__ nw,
                                             int k, float eps, double* red, F&& after_loads) {
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
-    constexpr int kStep = kThreads * 4;
+    constexpr int kStep = 256 * W;
     const int base = threadIdx.x * 4;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     typename XS::Raw raw[NB];
@@ -746,7 +755,7 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const XS& xs, const flo
         const double ss = wave_sum_d_lane63((double)sf);
         if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
-        const float inv = (float)rsqrt_d(block_sum(red) / (double)k + (double)eps);
+        const float inv = (float)rsqrt_d(block_sum<W>(red) / (double)k + (double)eps);
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             v[u].x = v[u].x * inv * g[u].x;
@@ -756,17 +765,18 @@ __device__ __forceinline__ void stage_xq_nb(float* smem, const XS& xs, const flo
         }
     }
     // units past k hold zeros and store into the spare dword
-    quantize_units<NB>(v, base, k, lo);
+    quantize_units<W, NB>(v, base, k, lo);
     __syncthreads();
 }
 
 // Staging for K above what one thread keeps in registers (k > 12288, or
 // k > 4096 with a norm): the same values, x read again per pass.
+template <int W>
 __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
                                             int k, float eps, double* red) {
     // (the first weight steps are issued by the caller before this call)
     uint32_t* lo = reinterpret_cast<uint32_t*>(smem);
-    constexpr int kStep = kThreads * 4;
+    constexpr int kStep = 256 * W;
     double inv = 1.0;
     if (nw) {
         double ss = 0.0;
@@ -777,7 +787,7 @@ __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict
         ss = wave_sum_d_lane63(ss);
         if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = ss;
         __syncthreads();
-        inv = 1.0 / sqrt(block_sum(red) / (double)k + (double)eps);
+        inv = 1.0 / sqrt(block_sum<W>(red) / (double)k + (double)eps);
     }
     // the trip count is uniform across the workgroup (k is a multiple of 32
     // and every pass covers kStep elements), so the DPP runs convergent
@@ -793,29 +803,29 @@ __device__ __noinline__ void stage_xq_2pass(float* smem, const float* __restrict
             v.w = (float)((double)v.w * inv) * g.w;
         }
         const float4 u1[1] = {v};
-        quantize_units<1>(u1, e, k, lo);
+        quantize_units<W, 1>(u1, e, k, lo);
     }
     __syncthreads();
 }
 
 // Stage x (limb layout) and issue the first weight loads through
 // `issue_first` right after the x loads.
-template <class F>
+template <int W, class F>
 __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ x, const float* __restrict__ nw,
                                          int k, float eps, double* red, F&& issue_first) {
-    const int nb = (k + kThreads * 4 - 1) / (kThreads * 4);
+    const int nb = (k + 256 * W - 1) / (256 * W);
     // register budget: the two weight buffers issued during staging stay
     // live, so at most 48 staged registers (x, and the norm weight)
     const PlainIn xs{x};
     if (nw) {
-        if (nb <= 4) return stage_xq_nb<4, true>(smem, xs, nw, k, eps, red, issue_first);
+        if (nb <= 4) return stage_xq_nb<W, 4, true>(smem, xs, nw, k, eps, red, issue_first);
     } else {
-        if (nb <= 4) return stage_xq_nb<4, false>(smem, xs, nw, k, eps, red, issue_first);
-        if (nb <= 8) return stage_xq_nb<8, false>(smem, xs, nw, k, eps, red, issue_first);
-        if (nb <= 12) return stage_xq_nb<12, false>(smem, xs, nw, k, eps, red, issue_first);
+        if (nb <= 4) return stage_xq_nb<W, 4, false>(smem, xs, nw, k, eps, red, issue_first);
+        if (nb <= 8) return stage_xq_nb<W, 8, false>(smem, xs, nw, k, eps, red, issue_first);
+        if (nb <= 12) return stage_xq_nb<W, 12, false>(smem, xs, nw, k, eps, red, issue_first);
     }
     issue_first();
-    stage_xq_2pass(smem, x, nw, k, eps, red);
+    stage_xq_2pass<W>(smem, x, nw, k, eps, red);
 }
 
 // Output modes (epilogues) of one GEMV launch.
@@ -836,12 +846,12 @@ __device__ __forceinline__ void for_each_k(F&& f, std::integer_sequence<int, K..
 
 // NS = 0: persistent loop, one step of loads ahead.  NS > 0: short form,
 // at most NS steps per wave (the launcher sizes the grid for it).
-template <template <int> class T, int R, int MODE, int NS>
+template <template <int> class T, int R, int MODE, int NS, int W = kWaves>
 // The arguments a wave needs first (weights, x, norm weight, n, k) also come
 // as leading scalars, which the command processor preloads into SGPRs
 // (-amdgpu-kernarg-preload-count), so the first loads do not wait for a
-// kernel-argument fetch; the rest stay in GemvArgs.
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const float* px, const float* pnw, int pn,
+// kernel-argument fetch; the rest stay in GemvArgs.  W waves per workgroup.
+__global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* pw, const float* px, const float* pnw, int pn,
                                                         int pk, GemvArgs a) {
     a.w = pw;
     a.x = px;
@@ -851,9 +861,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     using Ty = T<R>;
     using Buf = typename Ty::Buf;
     extern __shared__ float xs[];
-    __shared__ double red[kWaves];
-    __shared__ float wmax[kWaves];
-    __shared__ int widx[kWaves];
+    __shared__ double red[W];
+    __shared__ float wmax[W];
+    __shared__ int widx[W];
 
     // wave index in an SGPR: every per-wave quantity below is provably
     // uniform, so the pipeline's branches are scalar and its waits exact
@@ -866,7 +876,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
     const int nchunks = a.k >> Ty::kChunkShift;  // chunks of 32 (64 for Q4_K) elements
     const int cpl = (nchunks + 63) >> 6;         // chunk steps per lane per row group
     const size_t rbytes = row_bytes(Ty::kType, a.k);
-    const int wave_id = blockIdx.x * kWaves + wave, n_waves = gridDim.x * kWaves;
+    const int wave_id = blockIdx.x * W + wave, n_waves = gridDim.x * W;
     const int my_groups = wave_id < n_groups ? (n_groups - 1 - wave_id) / n_waves + 1 : 0;
     const int total = my_groups * cpl;           // (row group, chunk step) pairs of this wave
     float best = -INFINITY;
@@ -879,7 +889,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
         int j, g;
     };
     const auto xview = [&] {  // layout of the staged x (filled below)
-        if constexpr (Ty::kIntX) return xq_view(xs, a.k);
+        if constexpr (Ty::kIntX) return xq_view<W>(xs, a.k);
         else return (const float*)xs;
     }();
     float acc[R];
@@ -982,13 +992,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             wait_vmcnt<kAhead * kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
-            stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
+            stage_xq_nb<W, 4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
                                   red, issue_all);
         } else if constexpr (Ty::kIntX) {
-            stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
+            stage_xq<W>(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
         } else {
             issue_all();
-            stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
+            stage_x<W>(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
         // then step K + kAhead is issued before step K is consumed: a wave
         // never has more than kAhead + 1 steps of loads queued, so its
@@ -1019,13 +1029,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
             wait_vmcnt<kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
-            stage_xq_nb<4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
+            stage_xq_nb<W, 4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
                                   red, issue_first);
         } else if constexpr (Ty::kIntX) {
-            stage_xq(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
+            stage_xq<W>(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
         } else {
             issue_first();
-            stage_x(xs, a.x, a.norm_w, a.k, a.eps, red);
+            stage_x<W>(xs, a.x, a.norm_w, a.k, a.eps, red);
         }
         // then one step ahead: step j + 1 is issued just before step j is
         // consumed (two steps ahead measured the same at 12-350 MB shapes and
@@ -1057,7 +1067,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t* pw, const
         if (threadIdx.x == 0) {
             float bv = wmax[0];
             int bi = widx[0];
-            for (int w2 = 1; w2 < kWaves; ++w2)
+            for (int w2 = 1; w2 < W; ++w2)
                 if (wmax[w2] > bv || (wmax[w2] == bv && widx[w2] < bi)) {
                     bv = wmax[w2];
                     bi = widx[w2];
@@ -1114,7 +1124,7 @@ int device_cus() {
     return n_cu;
 }
 
-int resident_grid(const void* kernel, size_t lds) {
+int resident_grid(const void* kernel, size_t lds, int threads) {
     struct Entry {
         const void* k;
         size_t lds;
@@ -1126,7 +1136,7 @@ int resident_grid(const void* kernel, size_t lds) {
         if (cache[i].k == kernel && cache[i].lds == lds) return cache[i].grid;
     const int n_cu = device_cus();
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
     const int grid = per_cu * n_cu;
     if (n_cache < 64) cache[n_cache++] = Entry{kernel, lds, grid};
@@ -1134,10 +1144,13 @@ int resident_grid(const void* kernel, size_t lds) {
 }
 
 // the kernel instance of an epilogue mode (GEMV_ATTN only for the
-// quantized formats, whose staging merges the attention partials)
-template <template <int> class T, int R, int NS>
+// quantized formats, whose staging merges the attention partials); with W
+// waves other than kWaves only the plain epilogue is built
+template <template <int> class T, int R, int NS, int W>
 const void* kernel_for(int mode) {
-    if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {
+    if constexpr (W != kWaves) {
+        return (const void*)gemv_kernel<T, R, GEMV_PLAIN, NS, W>;
+    } else if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {
         return (const void*)gemv_kernel<T, R, GEMV_SILU, NS>;  // SwiGLU only
     } else {
         if (mode == GEMV_SILU) return (const void*)gemv_kernel<T, R, GEMV_SILU, NS>;
@@ -1150,9 +1163,12 @@ const void* kernel_for(int mode) {
 }
 
 // launch of a PLAIN, SILU or ATTN instance
-template <template <int> class T, int R, int NS>
+template <template <int> class T, int R, int NS, int W>
 void launch_mode(int mode, unsigned grid, size_t lds, const GemvArgs& a, hipStream_t st) {
-    if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {  // SwiGLU only
+    if constexpr (W != kWaves) {
+        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, NS, W>), dim3(grid), dim3(64 * W), lds, st, a.w, a.x,
+                           a.norm_w, a.n, a.k, a);
+    } else if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {  // SwiGLU only
         hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_SILU, NS>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x,
                            a.norm_w, a.n, a.k, a);
     } else {
@@ -1173,15 +1189,15 @@ void launch_mode(int mode, unsigned grid, size_t lds, const GemvArgs& a, hipStre
     }
 }
 
-template <template <int> class T, int R>
+template <template <int> class T, int R, int W = kWaves>
 int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     const int kout = mode == GEMV_SILU ? R / 2 : R;
     const int64_t n_out = mode == GEMV_SILU ? a.n / 2 : a.n;
     const int64_t n_groups = (n_out + kout - 1) / kout;
-    const int64_t need = (n_groups + kWaves - 1) / kWaves;
+    const int64_t need = (n_groups + W - 1) / W;
     const int64_t cpl = ((a.k >> T<R>::kChunkShift) + 63) >> 6;  // chunk steps per row group
     // fp32 x with padding, or the limb layout (2 bytes + 3/16 floats per element)
-    const size_t lds = T<R>::kIntX ? (size_t)xq_dwords(a.k) * 4
+    const size_t lds = T<R>::kIntX ? (size_t)xq_dwords<W>(a.k) * 4
                                    : (size_t)(a.k + (a.k >> 4)) * sizeof(float);
     const int n_cu = device_cus();
     // Short form: when every wave can finish in at most NS steps with a
@@ -1196,42 +1212,47 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
                     return false;
                 } else {
                     if (NSv < cpl) return false;  // a row group's chunk steps exceed the form
-                    const int64_t per_wg = (int64_t)kWaves * (NSv / cpl);
+                    const int64_t per_wg = (int64_t)W * (NSv / cpl);
                     const int64_t min_grid = (n_groups + per_wg - 1) / per_wg;
                     int64_t grid = need < n_cu ? need : n_cu;
                     if (grid < min_grid) grid = min_grid;
-                    if (grid > resident_grid(kernel_for<T, R, NSv>(mode), lds)) return false;
-                    launch_mode<T, R, NSv>(mode, (unsigned)grid, lds, a, st);
+                    if (grid > resident_grid(kernel_for<T, R, NSv, W>(mode), lds, 64 * W)) return false;
+                    launch_mode<T, R, NSv, W>(mode, (unsigned)grid, lds, a, st);
                     return true;
                 }
             };
-            // the longer SwiGLU form only where one workgroup per CU would
-            // leave waves more than kShortSteps steps (a wave issues the steps
-            // past its last too, to keep the wait counts fixed)
-            const int64_t steps_one_per_cu = (n_groups + (int64_t)n_cu * kWaves - 1) / ((int64_t)n_cu * kWaves) * cpl;
-            if (mode == GEMV_SILU && steps_one_per_cu > kShortSteps &&
-                try_short(std::integral_constant<int, kSiluShortSteps>{}))
-                return MXH_OK;
+            if constexpr (W == kWaves) {
+                // the longer SwiGLU form only where one workgroup per CU would
+                // leave waves more than kShortSteps steps (a wave issues the
+                // steps past its last too, to keep the wait counts fixed)
+                const int64_t steps_one_per_cu =
+                    (n_groups + (int64_t)n_cu * W - 1) / ((int64_t)n_cu * W) * cpl;
+                if (mode == GEMV_SILU && steps_one_per_cu > kShortSteps &&
+                    try_short(std::integral_constant<int, kSiluShortSteps>{}))
+                    return MXH_OK;
+            }
             if (try_short(std::integral_constant<int, kShortSteps>{})) return MXH_OK;
         }
     }
-    int cap = grid_cap > 0 ? grid_cap : resident_grid(kernel_for<T, R, 0>(mode), lds);
+    int cap = grid_cap > 0 ? grid_cap : resident_grid(kernel_for<T, R, 0, W>(mode), lds, 64 * W);
     // Short runs (a few row groups per wave with one workgroup per CU): one
     // workgroup per CU, so x is staged and quantized once per CU and no CU
     // carries two workgroups' staging while others carry one.  Long runs keep
     // the resident occupancy, whose extra waves hide latency.
-    if (grid_cap <= 0 && need > n_cu && (n_groups + (int64_t)n_cu * kWaves - 1) / ((int64_t)n_cu * kWaves) <= 8)
+    if (grid_cap <= 0 && need > n_cu && (n_groups + (int64_t)n_cu * W - 1) / ((int64_t)n_cu * W) <= 8)
         cap = n_cu;
     const unsigned grid = (unsigned)(need < cap ? need : cap);
-    if (mode == GEMV_ARGMAX) {
-        if ((int)grid > a.red_cap) return MXH_ERR_ARG;
-        hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x, a.norm_w,
-                           a.n, a.k, a);
-        hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, st, a.red_val, a.red_idx, (int)grid, a.tokens,
-                           a.pos);
-    } else {
-        launch_mode<T, R, 0>(mode, grid, lds, a, st);
+    if constexpr (W == kWaves) {
+        if (mode == GEMV_ARGMAX) {
+            if ((int)grid > a.red_cap) return MXH_ERR_ARG;
+            hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ARGMAX, 0>), dim3(grid), dim3(kThreads), lds, st, a.w, a.x,
+                               a.norm_w, a.n, a.k, a);
+            hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(1024), 0, st, a.red_val, a.red_idx, (int)grid,
+                               a.tokens, a.pos);
+            return MXH_OK;
+        }
     }
+    launch_mode<T, R, 0, W>(mode, grid, lds, a, st);
     return MXH_OK;
 }
 
@@ -1251,7 +1272,12 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.tokens || !a.pos)) return MXH_ERR_ARG;
     switch (type) {
     case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);
-    case MXH_Q4_K_TILED: return launch_gemv<Q4KT, 2>(a, mode, st);
+    case MXH_Q4_K_TILED:
+        // eight waves per workgroup for long plain rows (x staged once per
+        // CU for eight waves: the 4096 x 12288 down projection)
+        if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
+            return launch_gemv<Q4KT, 2, 8>(a, mode, st);
+        return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K_TILED: return launch_gemv<Q5KT, 4>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
