@@ -1279,7 +1279,10 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
             return launch_gemv<Q4KT, 2, 8>(a, mode, st);
         return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
-    case MXH_Q5_K_TILED: return launch_gemv<Q5KT, 4>(a, mode, st);
+    case MXH_Q5_K_TILED:
+        if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
+            return launch_gemv<Q5KT, 4, 8>(a, mode, st);
+        return launch_gemv<Q5KT, 4>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
     case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
     case MXH_Q5_0: return launch_gemv<Q50, 4>(a, mode, st);
