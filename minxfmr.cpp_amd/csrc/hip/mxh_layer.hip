@@ -56,7 +56,13 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, const float* __restr
 #endif
 
 constexpr int kAttnMaxGroup = 8;    // q heads per kv head
-constexpr int kAttnSplitPos = 256;  // positions per workgroup (split) before the next split opens
+// Splits per q head: the grid holds ceil(n_ctx / kAttnSplitPos) of them (at
+// most kAttnMaxSplits), and a launch uses min(grid, ceil(L / kAttnRunSplitPos)),
+// so short contexts spread over every split the grid has (the o-projection
+// merges the grid's partials whatever L is: 607 against 615 tok/s with
+// 256-position splits at run time too)
+constexpr int kAttnSplitPos = 256;
+constexpr int kAttnRunSplitPos = 128;
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
 // wave in two parts: head_fetch requests every global input (so a kernel can
@@ -163,7 +169,7 @@ __device__ __forceinline__ float fold_position_groups_max(float v) {
 // Workgroup (i, s): q head qh of kv head g = i % nkv (qh = g * group +
 // i / nkv, so the q heads that share a kv head have workgroup ids equal
 // modulo 8 and run on one XCD, whose L2 serves their common K/V rows once),
-// split s of S = min(gridDim.y, ceil(L / kAttnSplitPos)) contiguous position
+// split s of S = min(gridDim.y, ceil(L / kAttnRunSplitPos)) contiguous position
 // ranges.  It leaves the split's running max m (base-2 units), sum l and
 // exp-weighted V sums in `part`; the o-projection's x staging merges the S
 // partials of each q head (GEMV_ATTN), so no workgroup waits for another.
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane % LPP, pr = lane / LPP;
     const int pos = *a.pos, L = pos + 1;
-    const int S = min(SM, (L + kAttnSplitPos - 1) / kAttnSplitPos);
+    const int S = min(SM, (L + kAttnRunSplitPos - 1) / kAttnRunSplitPos);
     MXH_ATTN_STAMP(1);
     float* part_v = a.part;                              // [nh][SM][HD]
     float* part_ml = a.part + (size_t)a.nh * SM * HD;    // [nh][SM][2]
