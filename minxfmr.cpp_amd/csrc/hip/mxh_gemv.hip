@@ -992,8 +992,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* pw, const f
             wait_vmcnt<kAhead * kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
-            stage_xq_nb<W, 4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
-                                  red, issue_all);
+            stage_xq_nb<W, 4096 / (256 * W), false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd},
+                                                    nullptr, a.k, a.eps, red, issue_all);
         } else if constexpr (Ty::kIntX) {
             stage_xq<W>(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
         } else {
@@ -1029,8 +1029,8 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* pw, const f
             wait_vmcnt<kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
-            stage_xq_nb<W, 4, false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd}, nullptr, a.k, a.eps,
-                                  red, issue_first);
+            stage_xq_nb<W, 4096 / (256 * W), false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd},
+                                                    nullptr, a.k, a.eps, red, issue_first);
         } else if constexpr (Ty::kIntX) {
             stage_xq<W>(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
         } else {
@@ -1145,10 +1145,12 @@ int resident_grid(const void* kernel, size_t lds, int threads) {
 
 // the kernel instance of an epilogue mode (GEMV_ATTN only for the
 // quantized formats, whose staging merges the attention partials); with W
-// waves other than kWaves only the plain epilogue is built
+// waves other than kWaves only the plain and merge epilogues are built
 template <template <int> class T, int R, int NS, int W>
 const void* kernel_for(int mode) {
     if constexpr (W != kWaves) {
+        if constexpr (T<R>::kIntX)
+            if (mode == GEMV_ATTN) return (const void*)gemv_kernel<T, R, GEMV_ATTN, NS, W>;
         return (const void*)gemv_kernel<T, R, GEMV_PLAIN, NS, W>;
     } else if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {
         return (const void*)gemv_kernel<T, R, GEMV_SILU, NS>;  // SwiGLU only
@@ -1166,6 +1168,13 @@ const void* kernel_for(int mode) {
 template <template <int> class T, int R, int NS, int W>
 void launch_mode(int mode, unsigned grid, size_t lds, const GemvArgs& a, hipStream_t st) {
     if constexpr (W != kWaves) {
+        if constexpr (T<R>::kIntX) {
+            if (mode == GEMV_ATTN) {
+                hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_ATTN, NS, W>), dim3(grid), dim3(64 * W), lds, st, a.w,
+                                   a.x, a.norm_w, a.n, a.k, a);
+                return;
+            }
+        }
         hipLaunchKernelGGL((gemv_kernel<T, R, GEMV_PLAIN, NS, W>), dim3(grid), dim3(64 * W), lds, st, a.w, a.x,
                            a.norm_w, a.n, a.k, a);
     } else if constexpr (NS == kSiluShortSteps && NS != kShortSteps) {  // SwiGLU only
@@ -1221,15 +1230,19 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
                     return true;
                 }
             };
+            // steps per wave with one workgroup per CU
+            const int64_t steps_one_per_cu = (n_groups + (int64_t)n_cu * W - 1) / ((int64_t)n_cu * W) * cpl;
             if constexpr (W == kWaves) {
                 // the longer SwiGLU form only where one workgroup per CU would
                 // leave waves more than kShortSteps steps (a wave issues the
                 // steps past its last too, to keep the wait counts fixed)
-                const int64_t steps_one_per_cu =
-                    (n_groups + (int64_t)n_cu * W - 1) / ((int64_t)n_cu * W) * cpl;
                 if (mode == GEMV_SILU && steps_one_per_cu > kShortSteps &&
                     try_short(std::integral_constant<int, kSiluShortSteps>{}))
                     return MXH_OK;
+            } else {
+                // one step per wave: no steps past the last to issue (the
+                // eight-wave o-projection: 655 against 643 tok/s)
+                if (steps_one_per_cu == 1 && try_short(std::integral_constant<int, 1>{})) return MXH_OK;
             }
             if (try_short(std::integral_constant<int, kShortSteps>{})) return MXH_OK;
         }
@@ -1274,9 +1287,12 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     case MXH_Q4_K: return launch_gemv<Q4K, 4>(a, mode, st);
     case MXH_Q4_K_TILED:
         // eight waves per workgroup for long plain rows (x staged once per
-        // CU for eight waves: the 4096 x 12288 down projection)
+        // CU for eight waves: the 4096 x 12288 down projection), and for the
+        // o-projection's attention merge above 2048 inputs (each thread
+        // merges half as many elements: 643 against 625 tok/s)
         if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
             return launch_gemv<Q4KT, 2, 8>(a, mode, st);
+        if (mode == GEMV_ATTN && a.k > 2048) return launch_gemv<Q4KT, 2, 8>(a, mode, st);
         return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K_TILED:
