@@ -56,6 +56,7 @@ struct mxh_model {
     // device memory
     uint8_t* blob = nullptr;  // weights + norms
     size_t blob_bytes = 0;
+    uint8_t* out_copy = nullptr;  // tiled copy of an embedding table the output projection is tied to
     __half* kv = nullptr;
     double* rope_cs = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *h = nullptr, *logits = nullptr,
@@ -241,7 +242,7 @@ int free_model(mxh_model* m) {
     if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
     if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
     if (m->g_sample) (void)hipGraphExecDestroy(m->g_sample);
-    void* bufs[] = {m->blob, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
+    void* bufs[] = {m->blob, m->out_copy, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
                     m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
                     m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part,
                     m->pf_h16, m->pf_l16, m->pf_sh, m->pf_sl, m->pf_rscale, m->sprm, m->scand, m->eprm, m->esup,
@@ -467,7 +468,23 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         std::vector<DevW*> ws;
         for (Layer& D : m->layers)
             for (DevW* w : {&D.qkv, &D.q, &D.k, &D.v, &D.o, &D.gu, &D.g, &D.u, &D.down}) ws.push_back(w);
-        if (to) ws.push_back(&m->out);
+        if (to) {
+            ws.push_back(&m->out);
+        } else if (tiled_type(m->out.type, m->out.cols) != m->out.type) {
+            // a tied output projection reads a tiled copy of the table (the
+            // lm-head GEMV streams the whole table every token; Qwen3-0.6B:
+            // 51 against about 25 us per token)
+            const size_t nb = tensor_bytes(m->out.type, m->out.rows, m->out.cols);
+            int rc = dalloc(&m->out_copy, nb);
+            if (!rc)
+                rc = check_hip(hipMemcpy(m->out_copy, m->out.p, nb, hipMemcpyDeviceToDevice), "output table copy");
+            if (rc) {
+                free_model(m);
+                return rc;
+            }
+            m->out.p = m->out_copy;
+            ws.push_back(&m->out);
+        }
         for (DevW* w : ws) {
             const int tt = tiled_type(w->type, w->cols);
             if (!w->p || tt == w->type) continue;
