@@ -1272,30 +1272,32 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
     return MXH_OK;
 }
 
-// Twelve waves per workgroup and one workgroup per CU where the row groups
-// give every wave exactly one step (rows with the fused rmsnorm: the
-// Qwen3-8B q|k|v) or exactly kSiluShortSteps (SwiGLU: its gate|up), K <=
-// 4096 (one chunk step per row group).  x is staged once per CU for twelve
-// waves and no wave issues steps past its last: 660 against 653 tok/s
-// (q|k|v alone 658, gate|up alone 653).  False where the shape does not fit.
-template <template <int> class T, int R>
-bool launch_twelve(const GemvArgs& a, int mode, hipStream_t st) {
-    constexpr int W = 12;
+// W waves per workgroup and one workgroup per CU where the row groups give
+// every wave exactly one step (rows with the fused rmsnorm, or SwiGLU rows) or
+// exactly kSiluShortSteps (SwiGLU), with one chunk step per row group.  x is
+// staged once per CU for all W waves and no wave issues steps past its last.
+// Twelve waves for Q4_K (the Qwen3-8B q|k|v in one step, gate|up in four:
+// 660 against 653 tok/s; q|k|v alone 658, gate|up alone 653), six for Q8_0
+// (the Qwen3-0.6B gate|up in one step).  False where the shape does not fit.
+template <template <int> class T, int R, int W>
+bool launch_exact(const GemvArgs& a, int mode, hipStream_t st) {
     if (a.k > 64 << T<R>::kChunkShift || (mode == GEMV_PLAIN ? !a.norm_w : mode != GEMV_SILU)) return false;
     const int64_t n_groups = mode == GEMV_SILU ? a.n / R : (a.n + R - 1) / R;
-    const int64_t n_cu = device_cus();
-    if (n_groups != n_cu * W * (mode == GEMV_SILU ? kSiluShortSteps : 1)) return false;
+    const int64_t n_cu = device_cus(), per = n_cu * W;
+    if (n_groups % per) return false;
+    const int64_t steps = n_groups / per;
     const size_t lds = (size_t)xq_dwords<W>(a.k) * 4;
+    auto go = [&](auto kern) {
+        if (resident_grid((const void*)kern, lds, 64 * W) < n_cu) return false;
+        hipLaunchKernelGGL(kern, dim3(n_cu), dim3(64 * W), lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
+        return true;
+    };
     if (mode == GEMV_SILU) {
-        constexpr auto kern = gemv_kernel<T, R, GEMV_SILU, kSiluShortSteps, W>;
-        if (resident_grid((const void*)kern, lds, 64 * W) < n_cu) return false;
-        hipLaunchKernelGGL(kern, dim3(n_cu), dim3(64 * W), lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
-    } else {
-        constexpr auto kern = gemv_kernel<T, R, GEMV_PLAIN, 1, W>;
-        if (resident_grid((const void*)kern, lds, 64 * W) < n_cu) return false;
-        hipLaunchKernelGGL(kern, dim3(n_cu), dim3(64 * W), lds, st, a.w, a.x, a.norm_w, a.n, a.k, a);
+        if (steps == 1) return go(gemv_kernel<T, R, GEMV_SILU, 1, W>);
+        if (steps == kSiluShortSteps) return go(gemv_kernel<T, R, GEMV_SILU, kSiluShortSteps, W>);
+        return false;
     }
-    return true;
+    return steps == 1 && go(gemv_kernel<T, R, GEMV_PLAIN, 1, W>);
 }
 
 }  // namespace
@@ -1322,9 +1324,11 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
         if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
             return launch_gemv<Q4KT, 2, 8>(a, mode, st);
         if (mode == GEMV_ATTN && a.k > 2048) return launch_gemv<Q4KT, 2, 8>(a, mode, st);
-        if (launch_twelve<Q4KT, 2>(a, mode, st)) return MXH_OK;
+        if (launch_exact<Q4KT, 2, 12>(a, mode, st)) return MXH_OK;
         return launch_gemv<Q4KT, 2>(a, mode, st);
-    case MXH_Q8_0_TILED: return launch_gemv<Q80T, 4>(a, mode, st);
+    case MXH_Q8_0_TILED:
+        if (launch_exact<Q80T, 4, 6>(a, mode, st)) return MXH_OK;
+        return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K_TILED:
         if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
             return launch_gemv<Q5KT, 4, 8>(a, mode, st);
