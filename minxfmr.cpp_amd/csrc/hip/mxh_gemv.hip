@@ -1330,12 +1330,12 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
         if (launch_exact<Q80T, 4, 6>(a, mode, st)) return MXH_OK;
         return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K_TILED:
-        // long plain rows as for Q4_K, two rows per wave so that the row
-        // groups fill every CU (Llama-3-8B's 4096 x 14336 down projection:
-        // 256 workgroups instead of 128; config 4 491 -> 535 tok/s)
+        // two rows per wave, so the row groups fill more CUs (Llama-3-8B's
+        // 4096 x 14336 down projection at eight waves: 256 workgroups instead
+        // of 128, config 4 491 -> 535 tok/s; its 1024-row v: 547)
         if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
             return launch_gemv<Q5KT, 2, 8>(a, mode, st);
-        return launch_gemv<Q5KT, 4>(a, mode, st);
+        return launch_gemv<Q5KT, 2>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
     case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
     case MXH_Q5_0: return launch_gemv<Q50, 4>(a, mode, st);
