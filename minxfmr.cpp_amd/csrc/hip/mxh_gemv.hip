@@ -1327,6 +1327,10 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
         if (launch_exact<Q4KT, 2, 12>(a, mode, st)) return MXH_OK;
         return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED:
+        // plain rows without a norm and the attention merge at two rows per
+        // wave, so few row groups still fill more CUs (Qwen3-0.6B o and down:
+        // 128 workgroups instead of 64; config 1 1,476 -> 1,537 tok/s)
+        if (mode == GEMV_ATTN || (mode == GEMV_PLAIN && !a.norm_w)) return launch_gemv<Q80T, 2>(a, mode, st);
         if (launch_exact<Q80T, 4, 6>(a, mode, st)) return MXH_OK;
         return launch_gemv<Q80T, 4>(a, mode, st);
     case MXH_Q5_K_TILED:
