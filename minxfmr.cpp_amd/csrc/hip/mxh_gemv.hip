@@ -1277,8 +1277,10 @@ int launch_gemv(const GemvArgs& a, int mode, hipStream_t st, int grid_cap = 0) {
 // exactly kSiluShortSteps (SwiGLU), with one chunk step per row group.  x is
 // staged once per CU for all W waves and no wave issues steps past its last.
 // Twelve waves for Q4_K (the Qwen3-8B q|k|v in one step, gate|up in four:
-// 660 against 653 tok/s; q|k|v alone 658, gate|up alone 653), six for Q8_0
-// (the Qwen3-0.6B gate|up in one step).  False where the shape does not fit.
+// 660 against 653 tok/s; q|k|v alone 658, gate|up alone 653), then fourteen
+// and ten (the Llama-3-8B gate|up in four, its q|k in one: config 4 546 ->
+// 558 tok/s), six for Q8_0 (the Qwen3-0.6B gate|up in one step).  False
+// where the shape does not fit.
 template <template <int> class T, int R, int W>
 bool launch_exact(const GemvArgs& a, int mode, hipStream_t st) {
     if (a.k > 64 << T<R>::kChunkShift || (mode == GEMV_PLAIN ? !a.norm_w : mode != GEMV_SILU)) return false;
@@ -1324,7 +1326,9 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
         if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
             return launch_gemv<Q4KT, 2, 8>(a, mode, st);
         if (mode == GEMV_ATTN && a.k > 2048) return launch_gemv<Q4KT, 2, 8>(a, mode, st);
-        if (launch_exact<Q4KT, 2, 12>(a, mode, st)) return MXH_OK;
+        if (launch_exact<Q4KT, 2, 12>(a, mode, st) || launch_exact<Q4KT, 2, 14>(a, mode, st) ||
+            launch_exact<Q4KT, 2, 10>(a, mode, st))
+            return MXH_OK;
         return launch_gemv<Q4KT, 2>(a, mode, st);
     case MXH_Q8_0_TILED:
         // plain rows without a norm and the attention merge at two rows per
