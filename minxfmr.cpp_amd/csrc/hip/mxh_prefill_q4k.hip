@@ -814,6 +814,44 @@ __global__ void gemm_f16_reduce_kernel(const float* __restrict__ part, int split
     out[o] = res ? v + res[o] : v;
 }
 
+// the same sums, four adjacent outputs per thread (n, ldo multiples of 4 and
+// 16-byte aligned rows)
+__global__ void gemm_f16_reduce4_kernel(const float4* __restrict__ part, int splits, float* out, int ldo,
+                                        const float* res, int m, int n4) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * n4) return;
+    const int r = i / n4, c = i - r * n4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < splits; ++s) {
+        const float4 p = part[(size_t)s * m * n4 + i];
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    const size_t o = (size_t)r * ldo + 4 * (size_t)c;
+    if (res) {
+        const float4 q = *reinterpret_cast<const float4*>(res + o);
+        v.x += q.x;
+        v.y += q.y;
+        v.z += q.z;
+        v.w += q.w;
+    }
+    *reinterpret_cast<float4*>(out + o) = v;
+}
+
+void reduce_launch(const float* part, int splits, float* out, int ldo, const float* res, int m, int n,
+                   hipStream_t st) {
+    const bool vec = n % 4 == 0 && ldo % 4 == 0 && (uintptr_t)part % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                     (uintptr_t)res % 16 == 0;
+    if (vec)
+        hipLaunchKernelGGL(gemm_f16_reduce4_kernel, dim3((m * (n / 4) + 255) / 256), dim3(256), 0, st,
+                           reinterpret_cast<const float4*>(part), splits, out, ldo, res, m, n / 4);
+    else
+        hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out,
+                           ldo, res, m, n);
+}
+
 // power-of-two scale 2^e that brings the row maximum into [128, 256)
 __device__ __forceinline__ int row_exponent(float maxv) {
     if (!(maxv > 0.f) || maxv > 3.0e38f) return 0;
@@ -994,8 +1032,7 @@ int gemm_q_f16_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, const
     hipLaunchKernelGGL((gemm_q_f16_kernel<F, TN>), grid, dim3(2 * TN), lds_bytes, st, a_hi, a_lo, lda, s_hi,
                        s_lo, lds, rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
     if (splits > 1)
-        hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
-                           res, m, n);
+        reduce_launch(part, splits, out, ldo, res, m, n, st);
     return MXH_OK;
 }
 
@@ -1045,8 +1082,7 @@ int gemm_q4k_pipe_launch(const uint16_t* a_hi, const uint16_t* a_lo, int lda, co
     hipLaunchKernelGGL((gemm_q4k_pipe_kernel<TILED, WJ>), grid, dim3(512), G::kLds, st, a_hi, a_lo, lda, s_hi, s_lo,
                        lds, rscale, w, out, ldo, res, m, n, k, form, steps / splits, part);
     if (splits > 1)
-        hipLaunchKernelGGL(gemm_f16_reduce_kernel, dim3((m * n + 255) / 256), dim3(256), 0, st, part, splits, out, ldo,
-                           res, m, n);
+        reduce_launch(part, splits, out, ldo, res, m, n, st);
     return MXH_OK;
 }
 
