@@ -155,13 +155,14 @@ def extra_model(mxhip, name: str, seed: int) -> Path:
     return p
 
 
-def run_long_context(mxhip, path: Path, seed: int) -> dict:
+def run_long_context(mxhip, path: Path, seed: int, flags: int = 0) -> dict:
     """8192-token prompt prefilled in 512-token chunks on
-    the matrix cores, then 128 greedy decode tokens against the 8192+ cache."""
+    the matrix cores, then 128 greedy decode tokens against the 8192+ cache.
+    `flags` are the model's open flags (MODEL_NO_GRAPH under --eager)."""
     import numpy as np
 
     n_prompt, n_dec = 8192, 128
-    m = mxhip.Model(path, n_prompt + n_dec + 8)
+    m = mxhip.Model(path, n_prompt + n_dec + 8, flags)
     prompt = np.random.default_rng(seed + 1).integers(0, m.cfg.n_vocab, n_prompt).astype(np.int32)
     _, pf_ms, _ = m.generate(prompt, 1)
     mxhip.synchronize()
@@ -223,7 +224,7 @@ def run_gemv_microbench(mxhip, seed: int) -> dict:
     return {"type": "Q4_K (tiled layout)", "launches": 200, "shapes": out}
 
 
-def run_extra_configs(mxhip, seed: int) -> dict:
+def run_extra_configs(mxhip, seed: int, flags: int = 0) -> dict:
     """BASELINE configs 1 and 4: Qwen3-0.6B Q8_0 greedy (32-token prompt, 128
     tokens) and Llama-3-8B mixed Q4_K/Q5_K with seeded top-k 8, T 0.8 sampling
     (128-token prompt, 512 tokens)."""
@@ -233,7 +234,7 @@ def run_extra_configs(mxhip, seed: int) -> dict:
     for name, n_prompt, n_gen, sampling in (("qwen3_0_6b_q8", 32, 128, None),
                                             ("llama3_8b_mixed", 128, 512, (8, 0.8, 0xC0F3))):
         p = extra_model(mxhip, name, seed)
-        m = mxhip.Model(p, n_prompt + n_gen + 8)
+        m = mxhip.Model(p, n_prompt + n_gen + 8, flags)
         if sampling:
             m.set_sampling(sampling[0], sampling[1], seed=sampling[2])
         prompt = np.random.default_rng(seed + 2).integers(0, m.cfg.n_vocab, n_prompt).astype(np.int32)
@@ -272,7 +273,9 @@ def main() -> int:
     ap.add_argument("--gemv-reps", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--eager", action="store_true", help="enqueue kernels directly instead of replaying HIP graphs")
+    ap.add_argument("--eager", action="store_true",
+                    help="enqueue kernels directly instead of replaying HIP graphs, in every leg (the mode to profile "
+                         "under rocprofv3, whose kernel tracing has ended in a host fault below hipGraphLaunch)")
     ap.add_argument("--no-long-context", action="store_true", help="skip the 8192-token context measurement")
     ap.add_argument("--no-microbench", action="store_true", help="skip the isolated Q4_K GEMV shapes")
     ap.add_argument("--all-configs", action="store_true",
@@ -368,9 +371,9 @@ def main() -> int:
     if not args.no_microbench:
         out["gemv_microbench"] = run_gemv_microbench(mxhip, args.seed)
     if not args.no_long_context:
-        out["long_context"] = run_long_context(mxhip, path, args.seed)
+        out["long_context"] = run_long_context(mxhip, path, args.seed, mxhip.MODEL_NO_GRAPH if args.eager else 0)
     if args.all_configs:
-        out["configs"] = run_extra_configs(mxhip, args.seed)
+        out["configs"] = run_extra_configs(mxhip, args.seed, mxhip.MODEL_NO_GRAPH if args.eager else 0)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(path, prompt, args.cpu_seconds, min(16, os.cpu_count() or 8))
         if not args.no_microbench:

@@ -294,6 +294,14 @@ int mxh_model_generate(mxh_model *m, const int *prompt, int n_prompt, int n_gen,
 /* Continue greedy decoding for n_gen steps from the current position (the id
  * at the position is the input); out (nullable) receives n_gen ids. */
 int mxh_model_decode(mxh_model *m, int n_gen, int *out, float *decode_ms);
+/* Make `token` the id at the current position: the input of the next
+ * mxh_model_decode step and the newest entry of the history that the logit
+ * edits count (the device token array, which otherwise holds the id the
+ * device chose there).  For a host that changes the device's choice: the
+ * reference's first-token swap replaces `next` by a visible alternative of
+ * its top-k order before it becomes `last` and enters token_history
+ * (src/api/minxfmr.cpp:2189-2205, :2388-2389).  Synchronous. */
+int mxh_model_set_token(mxh_model *m, int token);
 /* Enqueue every GEMV of the model whose weights have `type` (in layer order,
  * then the lm-head) `reps` times on the library stream, on the model's own
  * HBM-resident weights and in the form the decode step launches it (norm

@@ -571,7 +571,10 @@ __global__ void attention_merge_kernel(const float* __restrict__ part, int S, in
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const float w = mu[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mu[u].x - M);
+            // an empty split's V partial is whatever an earlier launch left
+            // (possibly not finite): skip it rather than weight it by 0
+            if (mu[u].x == -INFINITY) continue;
+            const float w = __builtin_amdgcn_exp2f(mu[u].x - M);
             den = fmaf(w, mu[u].y, den);
             v = fmaf(w, vu[u], v);
         }

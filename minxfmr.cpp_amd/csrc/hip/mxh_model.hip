@@ -907,6 +907,17 @@ int mxh_model_decode(mxh_model* m, int n_gen, int* out, float* decode_ms) {
     return rc;
 }
 
+int mxh_model_set_token(mxh_model* m, int token) {
+    if (!m) return set_error(MXH_ERR_ARG, "set_token: null model");
+    if (token < 0 || token >= m->embd.rows) return set_error(MXH_ERR_ARG, "set_token: token %d out of range", token);
+    // tokens[] holds n_ctx + 1 ids, so the current position indexes it even
+    // when the context is full
+    hipStream_t st = lib_stream();
+    int rc = check_hip(hipMemcpyAsync(m->tokens + m->host_pos, &token, sizeof(int), hipMemcpyHostToDevice, st), "token");
+    if (!rc) rc = check_hip(hipStreamSynchronize(st), "set_token");
+    return rc;
+}
+
 int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* launches, int64_t* bytes) {
     if (!m || reps <= 0 || !ms) return set_error(MXH_ERR_ARG, "bench_gemv: bad arguments");
     hipStream_t st = lib_stream();

@@ -103,6 +103,7 @@ def _load() -> C.CDLL:
         "mxh_model_generate": (ip, [vp, vp, ip, ip, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
         "mxh_model_close": (None, [vp]),
         "mxh_model_decode": (ip, [vp, ip, vp, C.POINTER(C.c_float)]),
+        "mxh_model_set_token": (ip, [vp, ip]),
         "mxh_model_bench_gemv": (ip, [vp, ip, ip, C.POINTER(C.c_float), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
         "mxh_write_synthetic_gguf": (ip, [C.c_char_p, C.POINTER(SynthArch), C.c_uint64, ip]),
     }
@@ -120,7 +121,7 @@ EXPORTED = (
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matmul_q mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_model_set_logit_edits mxh_sample mxh_model_generate mxh_model_close "
-    "mxh_write_synthetic_gguf mxh_model_decode mxh_model_bench_gemv"
+    "mxh_write_synthetic_gguf mxh_model_decode mxh_model_set_token mxh_model_bench_gemv"
 ).split()
 
 
@@ -334,6 +335,10 @@ class Model:
         ms = C.c_float()
         check(lib.mxh_model_decode(self.h, n_gen, ptr(out), C.byref(ms)), "decode")
         return out, ms.value
+
+    def set_token(self, token: int) -> None:
+        """Make `token` the id at the current position (the next decode input)."""
+        check(lib.mxh_model_set_token(self.h, token), "set_token")
 
     def bench_gemv(self, type_: int, reps: int = 1):
         """(device ms, launches, algorithmic bytes) of every `type_` GEMV of the model."""

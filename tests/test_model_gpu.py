@@ -67,12 +67,18 @@ def test_per_layer_activations_and_logits(mxh, tmp_path, name, flags):
     gm.close()
 
 
-@pytest.mark.parametrize("name,n_ctx,warm", [("q4k-qknorm", 600, 300), ("q5_0-gqa8", 1100, 40),
-                                             ("f32-hd128", 4000, 520), ("q4k-qknorm", 8200, 4150)])
+@pytest.mark.parametrize("name,n_ctx,warm", [("q4k-qknorm", 600, 300), ("q5_0-gqa8", 1100, 300),
+                                             ("q8-tied", 1100, 300), ("f32-hd128", 4000, 520),
+                                             ("q4k-qknorm", 8200, 4150)])
 def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
-    """Contexts long enough for several attention workgroups per kv head
-    (merged by the last to finish), from one active workgroup up to 64, and
-    (8200) workgroups that take two 64-position chunks each."""
+    """Contexts long enough for several attention splits per q head.  The
+    grid holds min(8, ceil(n_ctx / 256)) splits and a launch uses
+    min(grid, ceil(L / 128)) of them; the rest leave empty partials that the
+    merge must skip.  Checked at positions warm .. warm+5 (and 0 .. 2):
+    3 of 3 splits (Q4_K o-projection merging in its x staging), 3 of 5
+    (Q5_0 with hd 32 and 8 q heads per kv head; Q8_0 tied, the tiled
+    two-row merge), 5 of 8 (F32 o-projection: the separate merge kernel)
+    and 8 of 8 at L about 4150."""
     p = build(tmp_path, name)
     gm = mxhip.Model(p, n_ctx)
     om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
@@ -120,11 +126,90 @@ def test_graph_generate_matches_eager_steps_and_oracle(mxh, tmp_path, name):
     assert ids.tolist() == want
 
 
+SWAP_EDITS = dict(suppress=[7, 11], repeat_last_n=24, repeat_penalty=1.3, frequency_penalty=0.4, presence_penalty=2.0)
+
+
+@pytest.mark.parametrize("host_steps", [1, 2], ids=["handover-at-swap", "handover-after-host-step"])
+@pytest.mark.parametrize("sampled", [False, True], ids=["greedy", "topk8"])
+def test_first_token_swap_then_device(mxh, tmp_path, sampled, host_steps):
+    """The coarse-step protocol of INTEGRATION.md against the oracle.
+
+    Host phase (device edits off, greedy head): the device returns the head's
+    raw logits; the host applies the reference's edits (minxfmr.cpp:2047-2089)
+    and takes the runner-up of its order, as the reference's first-token swap
+    does when order[0] is invisible (:2189-2205).  With host_steps=2 one more
+    step runs on the host: the swapped id is the device's input and the host
+    chooses again.  Then the hand-over: the same edits and sampling set on the
+    device, mxh_model_set_token with the host's last id, and 16 device-chosen
+    ids.  They equal the oracle's continuing from the same ids, whose
+    penalties count the swapped id in the history (:2388)."""
+    p = build(tmp_path, "q4k-qknorm")
+    prompt = np.random.default_rng(31).integers(0, TINY["n_vocab"], 16).astype(np.int32)
+    e = SWAP_EDITS
+    k, temp, seed, n_dev = 8, 0.8, 99, 16
+
+    def edit(lg, hist):
+        return mxo.logit_edits(lg, hist, e["suppress"], e["repeat_last_n"], e["repeat_penalty"],
+                               e["frequency_penalty"], e["presence_penalty"])
+
+    # oracle: prompt, the swap, the host steps, then the device's choice rule
+    om = mxo.Model(p, 128)
+    lg = None
+    for t in prompt:
+        lg, _ = om.step(int(t))
+    hist = prompt.tolist()
+    want_host_logits, host_ids = [], []
+    for s in range(host_steps):
+        want_host_logits.append(lg)
+        ed = edit(lg, hist)
+        order = np.argsort(-ed.astype(np.float64), kind="stable")
+        nxt = int(order[1]) if s == 0 else int(order[0])
+        host_ids.append(nxt)
+        hist.append(nxt)
+        lg, _ = om.step(nxt)
+    want, state = [], seed
+    for _ in range(n_dev):
+        ed = edit(lg, hist)
+        if sampled:
+            nxt, state = mxo.sample(ed, k, temp, 1.0, 0.0, state)
+        else:
+            nxt = int(np.argmax(ed))
+        want.append(nxt)
+        hist.append(nxt)
+        lg, _ = om.step(nxt)
+    om.close()
+
+    gm = mxhip.Model(p, 128)
+    gm.set_logit_edits()
+    gm.set_sampling(1, 0.0)
+    gm.prefill(prompt[:-1])
+    last = int(prompt[-1])
+    dev_hist = prompt.tolist()
+    for s in range(host_steps):
+        lg, _ = gm.step(last)
+        ok, err = close_enough(lg, want_host_logits[s])
+        assert ok and err < 1e-3, f"host-phase step {s}: logits error {err}"
+        order = np.argsort(-edit(lg, dev_hist).astype(np.float64), kind="stable")
+        last = int(order[1]) if s == 0 else int(order[0])
+        assert last == host_ids[s], f"host-phase step {s}: the host chose {last}, the oracle {host_ids[s]}"
+        dev_hist.append(last)
+    gm.set_logit_edits(**e)
+    if sampled:
+        gm.set_sampling(k, temp, seed=seed)
+    gm.set_token(last)
+    ids, _ = gm.decode(n_dev)
+    gm.close()
+    assert ids.tolist() == want
+    assert not set(e["suppress"]) & set(ids.tolist())
+
+
 def test_step_errors_are_reported(mxh, tmp_path):
     p = build(tmp_path, "q8-tied")
     gm = mxhip.Model(p, 4)
     with pytest.raises(mxhip.MxhError, match="out of range"):
         gm.step(TINY["n_vocab"])
+    with pytest.raises(mxhip.MxhError, match="out of range"):
+        gm.set_token(-1)
     for t in range(4):
         gm.step(t, logits=False)
     with pytest.raises(mxhip.MxhError, match="full"):
