@@ -24,14 +24,18 @@ extern "C" {
 #endif
 
 /* Tensor element types, numbered as GGUF type ids.  Replaces DataType
- * (src/tensor/tensor.h:5-14), which lacks F16 and Q5_K. */
+ * (src/tensor/tensor.h:5-14), which lacks F16, Q5_K and Q6_K: the
+ * reference converts F16 and Q6_K tensors to F32 when it loads them
+ * (third_party/gguf/gguf_reader.cpp:759-785, :905-1008) and has no Q5_K;
+ * here all three stay packed in HBM and are decoded by the kernels. */
 enum {
     MXH_F32 = 0,
     MXH_F16 = 1,
     MXH_Q5_0 = 6,
     MXH_Q8_0 = 8,
     MXH_Q4_K = 12,
-    MXH_Q5_K = 13
+    MXH_Q5_K = 13,
+    MXH_Q6_K = 14
 };
 
 /* flag of the tiled weight layout (mxh_tile_rows): MXH_TILED_FLAG | type */
@@ -92,8 +96,10 @@ int mxh_timer_end(float *ms);
 
 /* y[n] = sum_k x[k] * dequant(W[n, k]) for W a row-major [n x k] tensor of
  * raw GGUF blocks (k a multiple of the block size).  W must be 16-byte
- * aligned for Q4_K/Q5_K/F32 and 4-byte aligned for Q8_0/Q5_0.  `type` may
- * also be the tiled id mxh_tile_rows returned for W's rows (16-byte aligned).
+ * aligned for Q4_K/Q5_K/F16/F32 and 4-byte aligned for Q8_0/Q5_0/Q6_K.
+ * `type` may also be the tiled id mxh_tile_rows returned for W's rows
+ * (16-byte aligned).  F16 and Q6_K rows are multiplied as the values the
+ * reference's loader converts them to (gguf_reader.cpp:759-785, :905-1008).
  * Replaces the m == 1 case of backend_matmul_rhs_transposed
  * (src/backend/backend_runtime.cpp:266-376, cuda_backend.cu:1198-1415). */
 int mxh_gemv(int type, const void *w, const float *x, float *y, int64_t n, int64_t k, int form);
@@ -102,8 +108,9 @@ int mxh_gemv(int type, const void *w, const float *x, float *y, int64_t n, int64
  * place into the tiled order the GEMV reads fastest (every 16-byte load of a
  * wave within whole cache lines), and sets *tiled to the type id to pass to
  * mxh_gemv from then on: MXH_TILED_FLAG | type for Q4_K, Q5_K and Q8_0 with
- * cols a multiple of 256 up to 15360; otherwise the rows are left as they
- * are and *tiled = type.  W must be 16-byte aligned.  Results through the
+ * cols a multiple of 256 up to 15360 and for Q6_K with cols a multiple of
+ * 2048 up to 15360; otherwise the rows are left as they are and
+ * *tiled = type.  W must be 16-byte aligned.  Results through the
  * tiled rows are identical to those through the GGUF rows.  No reference
  * counterpart: the reference has one weight layout, the GGUF block order the
  * CUDA backend uploads (cuda_backend.cu:364-394). */

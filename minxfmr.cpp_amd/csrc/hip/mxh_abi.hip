@@ -136,7 +136,8 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 int check_weight_ptr(int type, const void* w) {
     if (!w) return set_error(MXH_ERR_ARG, "null weight pointer");
-    const size_t need = (type == MXH_Q8_0 || type == MXH_Q5_0) ? 4 : 16;
+    // blocks of 34, 22 and 210 bytes: 2-aligned blocks read through 4-aligned windows
+    const size_t need = (type == MXH_Q8_0 || type == MXH_Q5_0 || type == MXH_Q6_K) ? 4 : 16;
     if (!aligned(w, need)) return set_error(MXH_ERR_ARG, "weight pointer must be %zu-byte aligned", need);
     return MXH_OK;
 }

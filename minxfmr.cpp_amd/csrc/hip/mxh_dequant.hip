@@ -1,6 +1,7 @@
 // mxh_dequant.hip — GGUF block -> fp32 decode on the device, bit-exact with
-// the reference CPU decoders (src/tensor/tensor.cpp:405-457; see
-// mxh_quant.h).  One thread writes one run of 32 consecutive outputs.
+// the reference CPU decoders (src/tensor/tensor.cpp:405-457) and with its
+// load-time F16 / Q6_K conversions (third_party/gguf/gguf_reader.cpp:759-785,
+// :905-1008; see mxh_quant.h).  One thread writes one run of 32 consecutive outputs.
 #include <hip/hip_runtime.h>
 
 #include "mxh_device.h"
@@ -40,6 +41,7 @@ int dequant_launch(int type, const void* w, float* out, int64_t rows, int64_t co
     case MXH_Q5_K: launch<MXH_Q5_K>(w, out, rows, cols, form, st); break;
     case MXH_Q8_0: launch<MXH_Q8_0>(w, out, rows, cols, form, st); break;
     case MXH_Q5_0: launch<MXH_Q5_0>(w, out, rows, cols, form, st); break;
+    case MXH_Q6_K: launch<MXH_Q6_K>(w, out, rows, cols, form, st); break;
     case MXH_F16: launch<MXH_F16>(w, out, rows, cols, form, st); break;
     case MXH_F32: launch<MXH_F32>(w, out, rows, cols, form, st); break;
     default: return MXH_ERR_UNSUPPORTED;

@@ -503,6 +503,196 @@ struct Q50 {
     }
 };
 
+// Q6_K, 64-element chunks c = 4 b + 2 h + p (mxh_types.h): for l in
+// [16 p, 16 p + 16) the elements 128 h + l + 32 g of block b, g = 0..3, with
+// codes from the 16 ql bytes 64 h + 16 p (qa: g = 0 low, g = 2 high
+// nibbles), the 16 ql bytes 64 h + 32 + 16 p (qb: g = 1, 3) and the 16 qh
+// bytes 32 h + 16 p (2-bit field g), and the int8 scale 8 h + p + 2 g.  The
+// code minus 32 is formed as a signed byte (the 6-bit value with bit 5
+// flipped, sign-extended), so each 16-element sum of X_i (q_i - 32) is an
+// exact int32 v_dot4 sum and the weights, (d * sc) * (q - 32), are exact.
+struct Q6KPieces {
+    uint4 qa, qb, qh;
+    uint2 sc;  // scales 8 h .. 8 h + 7 of the block
+    float d;
+};
+// q - 32 of four bytes as signed bytes from 4-bit parts lo (bits 0-3 of each
+// byte) and 2-bit parts hi (bits 0-1): (hi ^ 2) is the signed top field
+__device__ __forceinline__ uint32_t q6_signed(uint32_t lo, uint32_t hi) {
+    const uint32_t f = (hi & 0x03030303u) ^ 0x02020202u;
+    return (lo & 0x0f0f0f0fu) | (f << 4) | ((f & 0x02020202u) * 0x60u);
+}
+template <int R>
+__device__ __forceinline__ void q6k_accum(const Q6KPieces (&pc)[R], int c, const XQ& x, float (&acc)[R]) {
+    const int blk = c >> 2, h = (c >> 1) & 1, p = c & 1;
+    const int e0 = 256 * blk + 128 * h + 16 * p;
+    XP xg[4];
+    float sg[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        xg[g] = xp_load(x, (e0 + 32 * g) >> 2);
+        sg[g] = x.scale[(e0 + 32 * g) >> 5];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t A[4] = {pc[r].qa.x, pc[r].qa.y, pc[r].qa.z, pc[r].qa.w};
+        const uint32_t B[4] = {pc[r].qb.x, pc[r].qb.y, pc[r].qb.z, pc[r].qb.w};
+        const uint32_t H[4] = {pc[r].qh.x, pc[r].qh.y, pc[r].qh.z, pc[r].qh.w};
+        LimbSum ls[4] = {limb_zero(), limb_zero(), limb_zero(), limb_zero()};
+        uint32_t q0[4], q1[4], q2[4], q3[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            q0[i] = q6_signed(A[i], H[i]);
+            q1[i] = q6_signed(B[i], H[i] >> 2);
+            q2[i] = q6_signed(A[i] >> 4, H[i] >> 4);
+            q3[i] = q6_signed(B[i] >> 4, H[i] >> 6);
+        }
+        limb_acc(ls[0], xg[0], q0[0], q0[1], q0[2], q0[3]);
+        limb_acc(ls[1], xg[1], q1[0], q1[1], q1[2], q1[3]);
+        limb_acc(ls[2], xg[2], q2[0], q2[1], q2[2], q2[3]);
+        limb_acc(ls[3], xg[3], q3[0], q3[1], q3[2], q3[3]);
+        const uint32_t scw = p ? (pc[r].sc.x >> 8) | (pc[r].sc.y << 24) : pc[r].sc.x;  // bytes p, p+1, ...
+        const uint32_t scw2 = p ? (pc[r].sc.y >> 8) : pc[r].sc.y;                     // bytes p+4, ...
+        const float d = pc[r].d;
+        float a = acc[r];
+        a = fmaf(d * (float)(int)(int8_t)(scw & 0xffu) * sg[0], limb_total(ls[0]), a);
+        a = fmaf(d * (float)(int)(int8_t)((scw >> 16) & 0xffu) * sg[1], limb_total(ls[1]), a);
+        a = fmaf(d * (float)(int)(int8_t)(scw2 & 0xffu) * sg[2], limb_total(ls[2]), a);
+        a = fmaf(d * (float)(int)(int8_t)((scw2 >> 16) & 0xffu) * sg[3], limb_total(ls[3]), a);
+        acc[r] = a;
+    }
+}
+
+// Q6_K in the tiled device layout (q6k_tile_offsets): three 16-byte code
+// pieces, the block's 8 scales of half h and d
+template <int R>
+struct Q6KT {
+    static constexpr int kType = MXH_Q6_K_TILED;
+    static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 6;
+    static constexpr int kLoads = 5;
+    struct Buf {
+        uint4 qa[R], qb[R], qh[R];
+        uint2 sc[R];
+        uint32_t d[R];
+    };
+    static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
+        const Q6KTileOffs o = q6k_tile_offsets(c, (int64_t)(rb / 210));
+        const int h = (c >> 1) & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t* rp = w + (size_t)rows[r] * rb;
+            b.qa[r] = ldg16(rp + o.qa);
+            b.qb[r] = ldg16(rp + o.qb);
+            b.qh[r] = ldg16(rp + o.qh);
+            b.sc[r] = *reinterpret_cast<const uint2*>(rp + o.sc + 8 * h);
+            b.d[r] = *reinterpret_cast<const uint16_t*>(rp + o.d);
+        }
+    }
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
+        Q6KPieces pc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) pc[r] = Q6KPieces{b.qa[r], b.qb[r], b.qh[r], b.sc[r], h2f(b.d[r])};
+        q6k_accum<R>(pc, c, x, acc);
+    }
+};
+
+// Q6_K in the GGUF block order, whose 210-byte blocks are only 2-aligned:
+// each piece is read as the dwords of its aligned window (one dword before
+// the piece when the block starts at 2 mod 4) plus the piece's last 16 bits,
+// the same loads whatever the alignment, and realigned in compute().  Every
+// byte read lies in [block - 2, block + 210); a block at offset 2 mod 4 is
+// never the first of its allocation.
+template <int R>
+struct Q6K {
+    static constexpr int kType = MXH_Q6_K;
+    static constexpr bool kIntX = true;
+    static constexpr int kChunkShift = 6;
+    static constexpr int kLoads = 19;
+    struct Buf {
+        uint32_t qa[R][5], qb[R][5], qh[R][5], sc[R][3], d[R];
+        bool odd[R];  // the block starts at 2 mod 4
+    };
+    static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
+        const int blk = c >> 2, h = (c >> 1) & 1, p = c & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t* bp = w + (size_t)rows[r] * rb + (size_t)blk * 210;
+            b.odd[r] = ((uintptr_t)bp & 2) != 0;
+            const uint8_t* ap = bp - ((uintptr_t)bp & 2);  // 4-aligned
+            auto piece = [&](int off, int nd, uint32_t* out) {
+                const uint32_t* wp = reinterpret_cast<const uint32_t*>(ap + off);
+                for (int i = 0; i < nd; ++i) out[i] = __builtin_nontemporal_load(wp + i);
+                out[nd] = *reinterpret_cast<const uint16_t*>(bp + off + 4 * nd - 2);
+            };
+            piece(64 * h + 16 * p, 4, b.qa[r]);
+            piece(64 * h + 32 + 16 * p, 4, b.qb[r]);
+            piece(128 + 32 * h + 16 * p, 4, b.qh[r]);
+            piece(192 + 8 * h, 2, b.sc[r]);
+            b.d[r] = *reinterpret_cast<const uint16_t*>(bp + 208);
+        }
+    }
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const XQ& x, int, float (&acc)[R]) {
+        Q6KPieces pc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool o = b.odd[r];
+            auto u4 = [&](const uint32_t* v) {
+                return o ? make_uint4((v[0] >> 16) | (v[1] << 16), (v[1] >> 16) | (v[2] << 16),
+                                      (v[2] >> 16) | (v[3] << 16), (v[3] >> 16) | (v[4] << 16))
+                         : make_uint4(v[0], v[1], v[2], v[3]);
+            };
+            const uint32_t* s = b.sc[r];
+            const uint2 sc = o ? make_uint2((s[0] >> 16) | (s[1] << 16), (s[1] >> 16) | (s[2] << 16))
+                               : make_uint2(s[0], s[1]);
+            pc[r] = Q6KPieces{u4(b.qa[r]), u4(b.qb[r]), u4(b.qh[r]), sc, h2f(b.d[r])};
+        }
+        q6k_accum<R>(pc, c, x, acc);
+    }
+};
+
+// F16 rows, 32-element chunks (64 bytes, four 16-byte loads); x in fp32
+template <int R>
+struct F16W {
+    static constexpr int kType = MXH_F16;
+    static constexpr bool kIntX = false;
+    static constexpr int kChunkShift = 5;
+    static constexpr int kLoads = 4;
+    struct Buf {
+        uint4 v[R][4];
+    };
+    static __device__ __forceinline__ void load(const uint8_t* w, size_t rb, const int (&rows)[R], int c, Buf& b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint8_t* p = w + (size_t)rows[r] * rb + (size_t)c * 64;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b.v[r][i] = ldg16(p + 16 * i);
+        }
+    }
+    static __device__ __forceinline__ void compute(const Buf& b, int c, const float* xs, int, float (&acc)[R]) {
+        const int e0 = 32 * c;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 xa = lds4(xs, e0 + 8 * i), xb = lds4(xs, e0 + 8 * i + 4);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float2 w0 = h2f2(b.v[r][i].x), w1 = h2f2(b.v[r][i].y), w2 = h2f2(b.v[r][i].z),
+                             w3 = h2f2(b.v[r][i].w);
+                float a = acc[r];
+                a = fmaf(xa.x, w0.x, a);
+                a = fmaf(xa.y, w0.y, a);
+                a = fmaf(xa.z, w1.x, a);
+                a = fmaf(xa.w, w1.y, a);
+                a = fmaf(xb.x, w2.x, a);
+                a = fmaf(xb.y, w2.y, a);
+                a = fmaf(xb.z, w3.x, a);
+                a = fmaf(xb.w, w3.y, a);
+                acc[r] = a;
+            }
+        }
+    }
+};
+
 template <int R>
 struct F32W {
     static constexpr int kType = MXH_F32;
@@ -1313,7 +1503,7 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
     // weights, whole q heads of 4 to 128 elements, no norm
     if (mode == GEMV_ATTN &&
         (a.k > 4096 || !a.part || a.norm_w || a.part_splits < 1 || a.part_splits > kAttnMaxSplits ||
-         a.part_hd < 4 || a.part_hd > 128 || a.part_hd % 4 || a.k % a.part_hd || storage_type(type) == MXH_F32))
+         a.part_hd < 4 || a.part_hd > 128 || a.part_hd % 4 || a.k % a.part_hd || !gemv_int_x(type)))
         return MXH_ERR_ARG;
     if (mode == GEMV_ARGMAX && (!a.red_val || !a.red_idx || !a.tokens || !a.pos)) return MXH_ERR_ARG;
     switch (type) {
@@ -1344,9 +1534,17 @@ int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st) {
         if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
             return launch_gemv<Q5KT, 2, 8>(a, mode, st);
         return launch_gemv<Q5KT, 2>(a, mode, st);
+    case MXH_Q6_K_TILED:
+        // eight waves for long plain rows, as for Q4_K (the Q6_K ffn_down of
+        // Q4_K_M files: 4096 x 12288 / 14336)
+        if (mode == GEMV_PLAIN && a.k > 8192 && !a.norm_w && xq_dwords<8>(a.k) * 4 <= 65536)
+            return launch_gemv<Q6KT, 2, 8>(a, mode, st);
+        return launch_gemv<Q6KT, 2>(a, mode, st);
     case MXH_Q5_K: return launch_gemv<Q5K, 4>(a, mode, st);
+    case MXH_Q6_K: return launch_gemv<Q6K, 2>(a, mode, st);
     case MXH_Q8_0: return launch_gemv<Q80, 4>(a, mode, st);
     case MXH_Q5_0: return launch_gemv<Q50, 4>(a, mode, st);
+    case MXH_F16: return launch_gemv<F16W, 2>(a, mode, st);
     case MXH_F32: return launch_gemv<F32W, 2>(a, mode, st);
     }
     return MXH_ERR_UNSUPPORTED;

@@ -45,6 +45,13 @@ struct GemvArgs {
     int part_splits, part_hd;
 };
 int gemv_run(int type, const GemvArgs& a, int mode, hipStream_t st);
+// Whether the GEMV of this (storage) type stages x as 24-bit block fixed
+// point (every quantized type); F32 and F16 rows multiply fp32 x.  Only those
+// GEMVs take the attention merge in their staging (GEMV_ATTN).
+inline bool gemv_int_x(int type) {
+    const int t = type & 0xff;
+    return t != MXH_F32 && t != MXH_F16;
+}
 
 // Tiled device layout for a weight of this type and row length (the type
 // itself when there is none), and the in-place regrouping of `rows` rows at w

@@ -14,6 +14,7 @@
 
 #include "mxh_device.h"
 #include "mxh_internal.h"
+#include "mxh_quant.h"
 
 namespace mxh {
 namespace {
@@ -464,6 +465,10 @@ __global__ void embed_kernel(const uint8_t* __restrict__ w, const int* __restric
         for (int i = 0; i < 32; ++i) y[i] = d * (float)(int)(int8_t)blk[2 + i];
     } else if constexpr (TYPE == MXH_F16) {
         for (int i = 0; i < 32; ++i) y[i] = half_bits_to_float((uint32_t)rp[2 * (run * 32 + i)] | ((uint32_t)rp[2 * (run * 32 + i) + 1] << 8));
+    } else if constexpr (TYPE == MXH_Q5_0 || TYPE == MXH_Q6_K) {
+        float t[32];
+        dequant_run32<TYPE>(rp, run, form, t);
+        for (int i = 0; i < 32; ++i) y[i] = t[i];
     } else {
         for (int i = 0; i < 32; ++i) y[i] = reinterpret_cast<const float*>(rp)[run * 32 + i];
     }
@@ -615,6 +620,8 @@ int embed_launch(int type, const void* w, const int* tokens, const int* pos, flo
     case MXH_Q4_K: hipLaunchKernelGGL(embed_kernel<MXH_Q4_K>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
     case MXH_Q5_K: hipLaunchKernelGGL(embed_kernel<MXH_Q5_K>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
     case MXH_Q8_0: hipLaunchKernelGGL(embed_kernel<MXH_Q8_0>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
+    case MXH_Q5_0: hipLaunchKernelGGL(embed_kernel<MXH_Q5_0>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
+    case MXH_Q6_K: hipLaunchKernelGGL(embed_kernel<MXH_Q6_K>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
     case MXH_F16: hipLaunchKernelGGL(embed_kernel<MXH_F16>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
     case MXH_F32: hipLaunchKernelGGL(embed_kernel<MXH_F32>, grid, block, 0, st, (const uint8_t*)w, tokens, pos, x, cols, form); break;
     default: return MXH_ERR_UNSUPPORTED;

@@ -127,7 +127,7 @@ int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hi
 // (GEMV_ATTN: quantized rows of at most 4096 inputs); otherwise a merge
 // kernel writes the attention output first.
 bool o_merges(const mxh_model* m, const DevW& o) {
-    return storage_type(o.type) != MXH_F32 && o.cols <= 4096;
+    return gemv_int_x(o.type) && o.cols <= 4096;
 }
 
 // the o-projection and residual of the decode step, from the attention partials
@@ -263,7 +263,10 @@ int dalloc(T** p, size_t count) {
     return MXH_OK;
 }
 
-bool gemv_type_ok(int t) { return t == MXH_Q4_K || t == MXH_Q5_K || t == MXH_Q8_0 || t == MXH_Q5_0 || t == MXH_F32; }
+bool gemv_type_ok(int t) {
+    return t == MXH_Q4_K || t == MXH_Q5_K || t == MXH_Q6_K || t == MXH_Q8_0 || t == MXH_Q5_0 || t == MXH_F16 ||
+           t == MXH_F32;
+}
 
 }  // namespace
 

@@ -356,6 +356,9 @@ int gemm_dispatch(int type, const uint16_t* a, const uint16_t* a_lo, int lda, co
     case MXH_Q5_K: return gemm_launch<MXH_Q5_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q8_0: return gemm_launch<MXH_Q8_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_Q5_0: return gemm_launch<MXH_Q5_0, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q6_K: return gemm_launch<MXH_Q6_K, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
+    case MXH_Q6_K_TILED:
+        return gemm_launch<MXH_Q6_K_TILED, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_F16: return gemm_launch<MXH_F16, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     case MXH_F32: return gemm_launch<MXH_F32, SPLIT>(a, a_lo, lda, w, out, ldo, res, m, n, k, form, part, pf, st);
     }
@@ -396,6 +399,7 @@ int embed_rows_launch(int type, const void* w, const int* tokens, int p0, int m,
     case MXH_Q5_K: hipLaunchKernelGGL(embed_rows_kernel<MXH_Q5_K>, grid, block, 0, st, wb, tokens, p0, m, x, cols, form); break;
     case MXH_Q8_0: hipLaunchKernelGGL(embed_rows_kernel<MXH_Q8_0>, grid, block, 0, st, wb, tokens, p0, m, x, cols, form); break;
     case MXH_Q5_0: hipLaunchKernelGGL(embed_rows_kernel<MXH_Q5_0>, grid, block, 0, st, wb, tokens, p0, m, x, cols, form); break;
+    case MXH_Q6_K: hipLaunchKernelGGL(embed_rows_kernel<MXH_Q6_K>, grid, block, 0, st, wb, tokens, p0, m, x, cols, form); break;
     case MXH_F16: hipLaunchKernelGGL(embed_rows_kernel<MXH_F16>, grid, block, 0, st, wb, tokens, p0, m, x, cols, form); break;
     case MXH_F32: hipLaunchKernelGGL(embed_rows_kernel<MXH_F32>, grid, block, 0, st, wb, tokens, p0, m, x, cols, form); break;
     default: return MXH_ERR_UNSUPPORTED;

@@ -55,6 +55,43 @@ __device__ __forceinline__ void dequant_run32(const uint8_t* __restrict__ rp, in
             q |= ((rd_u8(qh + i) >> j) & 1u) << 4;
             y[i] = ds * (float)q - ms;
         }
+    } else if constexpr (TYPE == MXH_Q6_K || TYPE == MXH_Q6_K_TILED) {
+        // run r of block b: elements 128 h + 32 g + i (i < 32) with h = r / 4,
+        // g = r % 4; the code of i comes from ql byte 64 h + 32 (g & 1) + i
+        // (low nibble for g < 2) and the 2-bit field g of qh byte 32 h + i,
+        // minus 32; value (d * sc) * q with sc = scales[8 h + 2 g + i / 16]
+        // (gguf_reader.cpp:905-1008, the reference's load-time conversion)
+        const int64_t b = run >> 3;
+        const int r = (int)(run & 7), h = r >> 2, g = r & 3;
+        const uint8_t *ql0, *ql1, *qh0, *qh1, *sc;
+        float d;
+        if constexpr (TYPE == MXH_Q6_K) {
+            const uint8_t* blk = rp + (size_t)b * 210;
+            ql0 = blk + 64 * h + 32 * (g & 1);
+            ql1 = ql0 + 16;
+            qh0 = blk + 128 + 32 * h;
+            qh1 = qh0 + 16;
+            sc = blk + 192;
+            d = half_bits_to_float(rd_u16(blk + 208));
+        } else {
+            // elements i < 16 lie in chunk 4 b + 2 h, the rest in chunk + 1
+            const Q6KTileOffs o0 = q6k_tile_offsets(4 * b + 2 * h, row_blocks);
+            const Q6KTileOffs o1 = q6k_tile_offsets(4 * b + 2 * h + 1, row_blocks);
+            ql0 = rp + ((g & 1) ? o0.qb : o0.qa);
+            ql1 = rp + ((g & 1) ? o1.qb : o1.qa);
+            qh0 = rp + o0.qh;
+            qh1 = rp + o1.qh;
+            sc = rp + o0.sc;
+            d = half_bits_to_float(rd_u16(rp + o0.d));
+        }
+        const int nib = (g >> 1) * 4, hs = 2 * g;
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) {
+            const uint32_t lq = rd_u8(i < 16 ? ql0 + i : ql1 + i - 16);
+            const uint32_t hq = rd_u8(i < 16 ? qh0 + i : qh1 + i - 16);
+            const int q = (int)(((lq >> nib) & 15u) | (((hq >> hs) & 3u) << 4)) - 32;
+            y[i] = d * (float)(int)(int8_t)sc[8 * h + 2 * g + (i >> 4)] * (float)q;
+        }
     } else if constexpr (TYPE == MXH_Q8_0_TILED) {
         const Q80TileOffs o = q80_tile_offsets(run, row_blocks);
         const float d = half_bits_to_float(rd_u16(rp + o.d));

@@ -1,5 +1,6 @@
 // mxh_repack.hip — in-place regrouping of device weight rows into the tiled
-// layouts of mxh_types.h (q4k_tile_offsets, q5k_tile_offsets, q80_tile_offsets).
+// layouts of mxh_types.h (q4k_tile_offsets, q5k_tile_offsets, q6k_tile_offsets,
+// q80_tile_offsets).
 //
 // A GGUF Q4_K row interleaves 16 header bytes and 128 quant bytes per block,
 // so the 16-byte loads of one wave instruction (one 64-element chunk per
@@ -27,7 +28,7 @@ __device__ __forceinline__ uint4 lds_u16x8(const uint8_t* p) {  // 2-aligned 16 
 template <int TYPE>
 __global__ __launch_bounds__(256) void tile_rows_kernel(uint8_t* __restrict__ w, int64_t rows, int nblocks) {
     extern __shared__ __align__(16) uint8_t row_buf[];
-    constexpr int BB = TYPE == MXH_Q4_K ? 144 : TYPE == MXH_Q5_K ? 176 : 34;
+    constexpr int BB = TYPE == MXH_Q4_K ? 144 : TYPE == MXH_Q5_K ? 176 : TYPE == MXH_Q6_K ? 210 : 34;
     const size_t rb = (size_t)nblocks * BB;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         uint8_t* rp = w + (size_t)r * rb;
@@ -55,6 +56,20 @@ __global__ __launch_bounds__(256) void tile_rows_kernel(uint8_t* __restrict__ w,
                 }
                 *reinterpret_cast<uint4*>(rp + o.qs) = *reinterpret_cast<const uint4*>(src + 48 + 16 * p);
             }
+        } else if constexpr (TYPE == MXH_Q6_K) {
+            // 210-byte blocks are 2-aligned in the LDS copy: 16-bit reads
+            for (int c = threadIdx.x; c < 4 * nblocks; c += blockDim.x) {
+                const Q6KTileOffs o = q6k_tile_offsets(c, nblocks);
+                const uint8_t* src = row_buf + (size_t)(c >> 2) * 210;
+                const int h = (c >> 1) & 1, p = c & 1;
+                *reinterpret_cast<uint4*>(rp + o.qa) = lds_u16x8(src + 64 * h + 16 * p);
+                *reinterpret_cast<uint4*>(rp + o.qb) = lds_u16x8(src + 64 * h + 32 + 16 * p);
+                *reinterpret_cast<uint4*>(rp + o.qh) = lds_u16x8(src + 128 + 32 * h + 16 * p);
+                if ((c & 3) == 0) {
+                    *reinterpret_cast<uint4*>(rp + o.sc) = lds_u16x8(src + 192);
+                    *reinterpret_cast<uint16_t*>(rp + o.d) = *reinterpret_cast<const uint16_t*>(src + 208);
+                }
+            }
         } else {
             for (int b = threadIdx.x; b < nblocks; b += blockDim.x) {
                 const Q80TileOffs o = q80_tile_offsets(b, nblocks);
@@ -76,6 +91,8 @@ int tiled_type(int type, int64_t cols) {
     if (type == MXH_Q4_K && cols % 256 == 0 && cols <= 15360) return MXH_Q4_K_TILED;
     if (type == MXH_Q8_0 && cols % 256 == 0 && cols <= 15360) return MXH_Q8_0_TILED;
     if (type == MXH_Q5_K && cols % 256 == 0 && cols <= 15360) return MXH_Q5_K_TILED;
+    // 210-byte blocks: rows stay 16-byte aligned when K is a multiple of 2048
+    if (type == MXH_Q6_K && cols % 2048 == 0 && cols <= 15360) return MXH_Q6_K_TILED;
     return type;
 }
 
@@ -88,6 +105,8 @@ int tile_rows_launch(int type, void* w, int64_t rows, int64_t cols, hipStream_t 
         hipLaunchKernelGGL(tile_rows_kernel<MXH_Q4_K>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
     else if (type == MXH_Q5_K)
         hipLaunchKernelGGL(tile_rows_kernel<MXH_Q5_K>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
+    else if (type == MXH_Q6_K)
+        hipLaunchKernelGGL(tile_rows_kernel<MXH_Q6_K>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
     else
         hipLaunchKernelGGL(tile_rows_kernel<MXH_Q8_0>, dim3(grid), dim3(256), lds, st, (uint8_t*)w, rows, nblocks);
     return hipGetLastError() == hipSuccess ? MXH_OK : MXH_ERR_HIP;

@@ -24,13 +24,16 @@ constexpr int kTiledFlag = 0x100;
 constexpr int MXH_Q4_K_TILED = kTiledFlag | MXH_Q4_K;
 constexpr int MXH_Q8_0_TILED = kTiledFlag | MXH_Q8_0;
 constexpr int MXH_Q5_K_TILED = kTiledFlag | MXH_Q5_K;
+constexpr int MXH_Q6_K_TILED = kTiledFlag | MXH_Q6_K;
 
 __host__ __device__ constexpr int storage_type(int type) { return type & (kTiledFlag - 1); }
 
 __host__ __device__ constexpr BlockGeom block_geom(int t) {
-    const int type = t == MXH_Q4_K_TILED || t == MXH_Q8_0_TILED || t == MXH_Q5_K_TILED ? storage_type(t) : t;
+    const int type =
+        t == MXH_Q4_K_TILED || t == MXH_Q8_0_TILED || t == MXH_Q5_K_TILED || t == MXH_Q6_K_TILED ? storage_type(t) : t;
     return type == MXH_Q4_K   ? BlockGeom{256, 144}
            : type == MXH_Q5_K ? BlockGeom{256, 176}
+           : type == MXH_Q6_K ? BlockGeom{256, 210}
            : type == MXH_Q8_0 ? BlockGeom{32, 34}
            : type == MXH_Q5_0 ? BlockGeom{32, 22}
            : type == MXH_F16  ? BlockGeom{1, 2}
@@ -86,6 +89,28 @@ __host__ __device__ constexpr Q80TileOffs q80_tile_offsets(int64_t block, int64_
     const int64_t nb = nblocks - 64 * j < 64 ? nblocks - 64 * j : 64;
     const uint32_t base = (uint32_t)(j * 2176);
     return Q80TileOffs{base + 16u * (uint32_t)l, base + 16u * (uint32_t)(nb + l), base + (uint32_t)(32 * nb + 2 * l)};
+}
+
+// Q6_K (ql[128], qh[64], int8 scales[16], fp16 d; 210 bytes per 256
+// elements).  The GEMV takes a block in four 64-element chunks
+// c = 4 b + 2 h + p (half h, run p): for l in [16 p, 16 p + 16) the elements
+// 128 h + l + 32 g, g = 0..3, whose 6-bit codes come from the 16 ql bytes
+// 64 h + 16 p.. (g = 0: low nibbles, g = 2: high), the 16 ql bytes
+// 64 h + 32 + 16 p.. (g = 1, 3) and the 16 qh bytes 32 h + 16 p.. (2-bit
+// field g).  Tiles of 16 blocks (3360 bytes; the last may hold fewer, nb):
+// for each chunk l of the tile its first 16 ql bytes, then for each chunk its
+// second 16, then for each chunk its 16 qh bytes, then the nb 16-byte scale
+// fields, then the nb fp16 d.  A row is 16-byte aligned when its block count
+// is a multiple of 8.
+struct Q6KTileOffs {
+    uint32_t qa, qb, qh, sc, d;
+};
+__host__ __device__ constexpr Q6KTileOffs q6k_tile_offsets(int64_t chunk, int64_t nblocks) {
+    const int64_t j = chunk >> 6, l = chunk & 63;
+    const int64_t nb = nblocks - 16 * j < 16 ? nblocks - 16 * j : 16;
+    const uint32_t base = (uint32_t)(j * 3360), nc = (uint32_t)(4 * nb);
+    return Q6KTileOffs{base + 16u * (uint32_t)l, base + 16u * (nc + (uint32_t)l), base + 16u * (2u * nc + (uint32_t)l),
+                       base + 48u * nc + 16u * (uint32_t)(l >> 2), base + 48u * nc + 16u * (uint32_t)nb + 2u * (uint32_t)(l >> 2)};
 }
 
 }  // namespace mxh

@@ -28,6 +28,7 @@ BlockInfo block_info(int type) {
     case 8: return {32, 34};
     case 12: return {256, 144};
     case 13: return {256, 176};
+    case 14: return {256, 210};
     }
     return {0, 0};
 }
@@ -241,6 +242,40 @@ void quantize_row(int type, const float* x, int64_t n, uint8_t* out) {
                     qs[32 * g + i] = (uint8_t)((a & 15) | ((c & 15) << 4));
                     if (type == 13) o[16 + i] |= (uint8_t)(((a >> 4) << (2 * g)) | ((c >> 4) << (2 * g + 1)));
                 }
+        }
+    } else if (type == 14) {
+        // Q6_K: per 16 elements a signed 8-bit scale (amax / 31 over d, d the
+        // largest of them / 127), codes q + 32 in [0, 63]; layout as the
+        // reference's gguf_dequant_q6_k reads it (gguf_reader.cpp:905-1008)
+        for (int64_t b = 0; b < n / 256; ++b) {
+            const float* v = x + 256 * b;
+            uint8_t* o = out + (size_t)210 * b;
+            float sf[16], smax = 0.f;
+            for (int j = 0; j < 16; ++j) {
+                float amax = 0.f;
+                for (int i = 0; i < 16; ++i) amax = std::max(amax, std::fabs(v[16 * j + i]));
+                sf[j] = amax / 31.f;
+                smax = std::max(smax, sf[j]);
+            }
+            const uint16_t dh = f2h(smax / 127.f);
+            const float d = h2f(dh);
+            int q[256];
+            for (int j = 0; j < 16; ++j) {
+                const int sc = d > 0.f ? qround(sf[j] / d, -128, 127) : 0;
+                o[192 + j] = (uint8_t)(int8_t)sc;
+                const float ds = d * (float)sc;
+                for (int i = 0; i < 16; ++i) q[16 * j + i] = (ds != 0.f ? qround(v[16 * j + i] / ds, -32, 31) : 0) + 32;
+            }
+            std::memset(o, 0, 192);
+            for (int h = 0; h < 2; ++h)
+                for (int l = 0; l < 32; ++l) {
+                    const int* qq = q + 128 * h + l;
+                    o[64 * h + l] = (uint8_t)((qq[0] & 15) | ((qq[64] & 15) << 4));
+                    o[64 * h + 32 + l] = (uint8_t)((qq[32] & 15) | ((qq[96] & 15) << 4));
+                    o[128 + 32 * h + l] =
+                        (uint8_t)((qq[0] >> 4) | ((qq[32] >> 4) << 2) | ((qq[64] >> 4) << 4) | ((qq[96] >> 4) << 6));
+                }
+            put16(o + 208, dh);
         }
     } else if (type == 6) {
         for (int64_t b = 0; b < n / 32; ++b) {

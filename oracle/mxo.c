@@ -183,12 +183,41 @@ void mxo_dequant_q5_0_block(const uint8_t *blk, float *y)
     }
 }
 
+/* Q6_K (GGML type 14), which the reference converts to F32 at load
+ * (gguf_reader.cpp:905-1008): ql@0 (128 B), qh@128 (64 B), scales@192
+ * (16 x int8), d@208 (fp16).  Half h (elements 128h..128h+127) reads
+ * ql[64h..], qh[32h..], scales[8h..]; for l < 32 its elements l, l+32,
+ * l+64, l+96 take the low nibble of ql[l], the low nibble of ql[l+32], the
+ * high nibble of ql[l], the high nibble of ql[l+32], each with the 2-bit
+ * field 0, 1, 2, 3 of qh[l] above it, minus 32; element e scales by
+ * scales[e / 16].  value = (d * sc) * q, in that float order. */
+void mxo_dequant_q6k_block(const uint8_t *blk, float *y)
+{
+    const uint8_t *ql = blk, *qh = blk + 128;
+    const int8_t *sc = (const int8_t *)(blk + 192);
+    const float d = mxo_fp16_to_fp32(rd16(blk + 208));
+    for (int h = 0; h < 2; ++h) {
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t a = ql[64 * h + l], b = ql[64 * h + 32 + l], c = qh[32 * h + l];
+            const int q0 = (int)((a & 15u) | ((c & 3u) << 4)) - 32;
+            const int q1 = (int)((b & 15u) | (((c >> 2) & 3u) << 4)) - 32;
+            const int q2 = (int)((a >> 4) | (((c >> 4) & 3u) << 4)) - 32;
+            const int q3 = (int)((b >> 4) | (((c >> 6) & 3u) << 4)) - 32;
+            const int e = 128 * h + l;
+            y[e] = d * (float)sc[e >> 4] * (float)q0;
+            y[e + 32] = d * (float)sc[(e + 32) >> 4] * (float)q1;
+            y[e + 64] = d * (float)sc[(e + 64) >> 4] * (float)q2;
+            y[e + 96] = d * (float)sc[(e + 96) >> 4] * (float)q3;
+        }
+    }
+}
+
 size_t mxo_block_elems(int type)
 {
     switch (type) {
     case MXO_F32: case MXO_F16: return 1;
     case MXO_Q5_0: case MXO_Q8_0: return 32;
-    case MXO_Q4_K: case MXO_Q5_K: return 256;
+    case MXO_Q4_K: case MXO_Q5_K: case MXO_Q6_K: return 256;
     }
     return 0;
 }
@@ -202,6 +231,7 @@ size_t mxo_block_bytes(int type)
     case MXO_Q8_0: return 34;
     case MXO_Q4_K: return 144;
     case MXO_Q5_K: return 176;
+    case MXO_Q6_K: return 210;
     }
     return 0;
 }
@@ -221,6 +251,7 @@ static void dequant_block(int type, const uint8_t *blk, float *y, int form)
     case MXO_Q5_K: mxo_dequant_q5k_block(blk, y, form); break;
     case MXO_Q8_0: mxo_dequant_q8_0_block(blk, y); break;
     case MXO_Q5_0: mxo_dequant_q5_0_block(blk, y); break;
+    case MXO_Q6_K: mxo_dequant_q6k_block(blk, y); break;
     case MXO_F32: memcpy(y, blk, 4); break;
     case MXO_F16: y[0] = mxo_fp16_to_fp32(rd16(blk)); break;
     }
@@ -290,6 +321,25 @@ int mxo_matmul_rhs_t(int type, const float *A, size_t M, size_t K, const void *B
                      float *out, int form, int nthreads)
 {
     if (!A || !B || !out) return -1;
+    if (type == MXO_F16 || type == MXO_Q6_K) {
+        /* the reference converts F16 and Q6_K weights to F32 when it loads
+         * them (gguf_reader.cpp:759-785, :905-1008) and multiplies the F32
+         * values: each row is decoded, then summed as an F32 row below */
+        const size_t rb = mxo_row_bytes(type, K);
+        if (!rb) return -1;
+#pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static)
+        for (long long j = 0; j < (long long)N; ++j) {
+            float *w = (float *)malloc(K * sizeof(float));
+            mxo_dequant_rows(type, (const uint8_t *)B + (size_t)j * rb, 1, K, w, form);
+            for (size_t i = 0; i < M; ++i) {
+                float s = 0.0f;
+                for (size_t k = 0; k < K; ++k) s = fmaf(A[i * K + k], w[k], s);
+                out[i * N + (size_t)j] = s;
+            }
+            free(w);
+        }
+        return 0;
+    }
     if (type == MXO_F32) {
         const float *W = (const float *)B;
         long long work = (long long)(M * N);
@@ -359,6 +409,45 @@ void mxo_quantize_q5_0_row(const float *x, size_t n, uint8_t *out)
         o[0] = (uint8_t)(dh & 0xff);
         o[1] = (uint8_t)(dh >> 8);
         o[2] = (uint8_t)qh; o[3] = (uint8_t)(qh >> 8); o[4] = (uint8_t)(qh >> 16); o[5] = (uint8_t)(qh >> 24);
+    }
+}
+
+/* Q6_K: per 16-element sub-block a signed scale (amax / 31 over d, d the
+ * largest such scale / 127), codes q + 32 in [0, 63], packed as
+ * mxo_dequant_q6k_block reads them. */
+void mxo_quantize_q6k_row(const float *x, size_t n, uint8_t *out)
+{
+    for (size_t b = 0; b < n / 256; ++b) {
+        const float *v = x + 256 * b;
+        uint8_t *o = out + 210 * b;
+        float sf[16], smax = 0.0f;
+        for (int j = 0; j < 16; ++j) {
+            float amax = 0.0f;
+            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[16 * j + i]));
+            sf[j] = amax / 31.0f;
+            smax = fmaxf(smax, sf[j]);
+        }
+        const uint16_t dh = mxo_fp32_to_fp16(smax / 127.0f);
+        const float d = mxo_fp16_to_fp32(dh);
+        int q[256];
+        for (int j = 0; j < 16; ++j) {
+            const int sc = d > 0.0f ? clampi(iround(sf[j] / d), -128, 127) : 0;
+            o[192 + j] = (uint8_t)(int8_t)sc;
+            const float ds = d * (float)sc;
+            for (int i = 0; i < 16; ++i)
+                q[16 * j + i] = (ds != 0.0f ? clampi(iround(v[16 * j + i] / ds), -32, 31) : 0) + 32;
+        }
+        memset(o, 0, 192);
+        for (int h = 0; h < 2; ++h)
+            for (int l = 0; l < 32; ++l) {
+                const int *qq = q + 128 * h + l;
+                o[64 * h + l] = (uint8_t)((qq[0] & 15) | ((qq[64] & 15) << 4));
+                o[64 * h + 32 + l] = (uint8_t)((qq[32] & 15) | ((qq[96] & 15) << 4));
+                o[128 + 32 * h + l] =
+                    (uint8_t)((qq[0] >> 4) | ((qq[32] >> 4) << 2) | ((qq[64] >> 4) << 4) | ((qq[96] >> 4) << 6));
+            }
+        o[208] = (uint8_t)dh;
+        o[209] = (uint8_t)(dh >> 8);
     }
 }
 

@@ -18,6 +18,9 @@
  * against the reference's own KATs, vectors from the reference source
  * compiled under oracle/_ref, closed forms and brute force.  Where the
  * reference has no code:
+ *   - mxo_dequant_q6k_block and the F16 decode: pinned against the
+ *     reference's own GGUF loader (gguf_dequant_q6_k, gguf_read_f32_tensor)
+ *     compiled under oracle/_ref, on random and special blocks;
  *   - mxo_dequant_q5k_block (no reference Q5_K): pinned to the published
  *     ggml layout by its exact reduction to Q4_K with a zero high-bit plane,
  *     the position of each high bit, and quantizer round trips;
@@ -49,6 +52,7 @@ enum {
     MXO_Q8_0 = 8,
     MXO_Q4_K = 12,
     MXO_Q5_K = 13,
+    MXO_Q6_K = 14,
 };
 
 /* Q4_K / Q5_K 6-bit scale unpacking forms.
@@ -67,6 +71,7 @@ void mxo_dequant_q4k_block(const uint8_t *blk, float *y256, int form);
 void mxo_dequant_q5k_block(const uint8_t *blk, float *y256, int form);
 void mxo_dequant_q8_0_block(const uint8_t *blk, float *y32);
 void mxo_dequant_q5_0_block(const uint8_t *blk, float *y32);
+void mxo_dequant_q6k_block(const uint8_t *blk, float *y256);
 
 size_t mxo_block_elems(int type);
 size_t mxo_block_bytes(int type);
@@ -85,6 +90,7 @@ void mxo_quantize_q8_0_row(const float *x, size_t n, uint8_t *out);
 void mxo_quantize_q4k_row(const float *x, size_t n, uint8_t *out);
 void mxo_quantize_q5k_row(const float *x, size_t n, uint8_t *out);
 void mxo_quantize_q5_0_row(const float *x, size_t n, uint8_t *out);
+void mxo_quantize_q6k_row(const float *x, size_t n, uint8_t *out);
 
 /* Layer ops (seq = 1). */
 void mxo_rmsnorm(const float *x, const float *w, float *y, size_t n, float eps);

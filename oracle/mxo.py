@@ -15,10 +15,11 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libmxref.so"
 
-F32, F16, Q5_0, Q8_0, Q4_K, Q5_K = 0, 1, 6, 8, 12, 13
+F32, F16, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 6, 8, 12, 13, 14
 FORM_REF, FORM_GGML = 0, 1
 OPEN_ROPE_NEOX, OPEN_KV_FP16, OPEN_GGML_FORM, OPEN_NO_QK_NORM = 1, 2, 4, 8
-BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176)}
+BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
+         Q6_K: (256, 210)}
 
 
 def _p(a: np.ndarray) -> int:
@@ -48,6 +49,7 @@ def _load():
         "mxo_quantize_q4k_row": (None, [vp, sz, vp]),
         "mxo_quantize_q5k_row": (None, [vp, sz, vp]),
         "mxo_quantize_q5_0_row": (None, [vp, sz, vp]),
+        "mxo_quantize_q6k_row": (None, [vp, sz, vp]),
         "mxo_rmsnorm": (None, [vp, vp, vp, sz, fp]),
         "mxo_rope": (None, [vp, sz, sz, sz, sz, fp, ip]),
         "mxo_softmax": (None, [vp, sz]),
@@ -100,7 +102,7 @@ def matmul_rhs_t(t: int, a: np.ndarray, w: np.ndarray, n: int, form: int = FORM_
 
 
 _QUANT = {Q8_0: "mxo_quantize_q8_0_row", Q4_K: "mxo_quantize_q4k_row", Q5_K: "mxo_quantize_q5k_row",
-          Q5_0: "mxo_quantize_q5_0_row"}
+          Q5_0: "mxo_quantize_q5_0_row", Q6_K: "mxo_quantize_q6k_row"}
 
 
 def quantize(t: int, x: np.ndarray) -> np.ndarray:
@@ -202,6 +204,7 @@ def load_ref():
         "ref_cache_new": (vp, [sz, sz, sz]),
         "ref_cache_free": (None, [vp]),
         "ref_layer_forward": (ip, [vp, vp, sz, sz, vp, sz, sz, sz, vp, vp, vp, vp, vp, vp, fp, fp, ip]),
+        "ref_gguf_to_f32": (ip, [ip, vp, sz, C.c_uint32, C.c_uint32, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(r, name)

@@ -17,6 +17,7 @@
 #include "transformer/softmax.h"
 #include "transformer/transformer.h"
 #include "backend/backend_context.h"
+#include "../third_party/gguf/gguf_reader.h"
 
 namespace {
 
@@ -123,6 +124,27 @@ int ref_layer_forward(const float* in, float* out, size_t seq, size_t d, void* c
                                                      &W[0], &W[1], &W[2], nullptr, nullptr, nullptr, &W[3], &an, &fn,
                                                      &W[4], &W[5], &W[6], scores.data(), scores.size(), theta, 0, eps);
     return ok ? 0 : -1;
+}
+
+// The reference's load-time conversion of a GGUF tensor to F32
+// (gguf_reader.cpp:759-785 for F32 / F16, :905-1008 for Q6_K) over `nbytes`
+// of tensor data held in memory; out receives rows x cols floats.  -1 when
+// the reference declines the tensor.
+int ref_gguf_to_f32(int ggml_type, const void* data, size_t nbytes, uint32_t rows, uint32_t cols, float* out) {
+    GGUF_File f;
+    f.data.assign(static_cast<const uint8_t*>(data), static_cast<const uint8_t*>(data) + nbytes);
+    GGUF_TensorInfo info;
+    info.offset = 0;
+    info.nbytes = nbytes;
+    info.rows = rows;
+    info.cols = cols;
+    info.ggml_type = (uint32_t)ggml_type;
+    Tensor* t = nullptr;
+    const bool ok = ggml_type == 14 ? gguf_dequant_q6_k(f, info, t) : gguf_read_f32_tensor(f, info, t);
+    if (!ok || !t) return -1;
+    std::memcpy(out, t->data, sizeof(float) * (size_t)rows * cols);
+    tensor_free(t);
+    return 0;
 }
 
 }  // extern "C"

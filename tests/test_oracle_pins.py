@@ -185,7 +185,58 @@ def _q5k_elem(blk, e, form):
     return np.float32((d * sc) * q - dm * m)
 
 
-@pytest.mark.parametrize("t,tol", [(mxo.Q8_0, 0.008), (mxo.Q4_K, 0.12), (mxo.Q5_K, 0.06), (mxo.Q5_0, 0.06)])
+def _q6k_closed_form(blk: np.ndarray) -> np.ndarray:
+    """The published Q6_K layout in numpy: element 128h + 32g + l (l < 32)
+    has the code nibble of ql[64h + 32(g & 1) + l] (low for g < 2) with the
+    2-bit field g of qh[32h + l] above it, minus 32, scaled by
+    d * scales[e // 16]; the products are exact in float64, so one rounding
+    to float32 gives the value (d * sc) * q the reference computes in float."""
+    ql, qh = blk[0:128].astype(np.int64), blk[128:192].astype(np.int64)
+    sc = blk[192:208].view(np.int8).astype(np.float64)
+    d = float(blk[208:210].view(np.float16)[0])
+    out = np.empty(256)
+    for e in range(256):
+        h, r = divmod(e, 128)
+        g, l = divmod(r, 32)
+        nib = ql[64 * h + 32 * (g & 1) + l]
+        nib = (nib >> 4) if g >= 2 else (nib & 15)
+        q = nib | (((qh[32 * h + l] >> (2 * g)) & 3) << 4)
+        out[e] = (d * sc[e // 16]) * (q - 32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return out.astype(np.float32)
+
+
+def test_q6k_dequant_closed_form():
+    rng = np.random.default_rng(61)
+    for _ in range(100):
+        blk = rng.integers(0, 256, 210, dtype=np.uint8)
+        blk[208:210] = (rng.standard_normal(1) * 0.05).astype(np.float16).view(np.uint8)
+        assert same_bits(mxo.dequant(mxo.Q6_K, blk, 1, 256)[0], _q6k_closed_form(blk))
+
+
+@pytest.mark.skipif(REF is None, reason="oracle/_ref not built (reference tree absent)")
+def test_q6k_and_f16_decode_vs_reference_loader():
+    """The reference converts Q6_K and F16 tensors to F32 when it loads them
+    (gguf_reader.cpp:905-1008, :759-785); its own functions, compiled under
+    oracle/_ref, give the same bits as the oracle for blocks with any bytes
+    (fp16 d subnormal, inf or NaN), for quantized rows, and for every fp16
+    value."""
+    rng = np.random.default_rng(62)
+    rows, cols = 6, 1024
+    for raw in (rng.integers(0, 256, rows * cols // 256 * 210, dtype=np.uint8),
+                mxo.quantize(mxo.Q6_K, rng.standard_normal((rows, cols)).astype(np.float32) * 0.02)):
+        want = np.empty((rows, cols), np.float32)
+        assert REF.ref_gguf_to_f32(14, raw.ctypes.data, raw.size, rows, cols, want.ctypes.data) == 0
+        assert same_bits(mxo.dequant(mxo.Q6_K, raw, rows, cols), want)
+    h = np.arange(65536, dtype=np.uint16)
+    want = np.empty(65536, np.float32)
+    assert REF.ref_gguf_to_f32(1, h.ctypes.data, h.nbytes, 1, 65536, want.ctypes.data) == 0
+    got = mxo.dequant(mxo.F16, h.view(np.uint8), 1, 65536)[0]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,tol", [(mxo.Q8_0, 0.008), (mxo.Q4_K, 0.12), (mxo.Q5_K, 0.06), (mxo.Q5_0, 0.06),
+                                   (mxo.Q6_K, 0.03)])
 def test_quantizer_round_trip(t, tol):
     """Generators used for synthetic models: relative RMS error of the round
     trip, decoded with the ggml scale form the quantizer packs for (the
@@ -213,7 +264,7 @@ def test_matmul_vs_reference_vectors(key):
         np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("t", [mxo.Q4_K, mxo.Q5_K, mxo.Q8_0, mxo.Q5_0, mxo.F32])
+@pytest.mark.parametrize("t", [mxo.Q4_K, mxo.Q5_K, mxo.Q6_K, mxo.Q8_0, mxo.Q5_0, mxo.F16, mxo.F32])
 def test_matmul_vs_float64_brute_force(t):
     rng = np.random.default_rng(t)
     k, n = 512, 33

@@ -39,7 +39,7 @@ def test_writer_quantizers_round_trip(tmp_path):
     """Dequantized weights (ggml scale form, which the writer packs for) have
     the requested N(0, 0.02) statistics."""
     import struct
-    for t in (mxhip.Q4_K, mxhip.Q5_K, mxhip.Q8_0, mxhip.Q5_0):
+    for t in (mxhip.Q4_K, mxhip.Q5_K, mxhip.Q6_K, mxhip.Q8_0, mxhip.Q5_0, mxhip.F16):
         p = _write(tmp_path / f"w{t}.gguf", 2, wtype=t, n_layer=1)
         raw = p.read_bytes()
         # locate blk.0.ffn_gate.weight through the oracle-independent header walk
@@ -62,3 +62,18 @@ def test_writer_quantizers_round_trip(tmp_path):
         vals = mxo.dequant(t, w, 512, 256, mxo.FORM_GGML)
         assert abs(vals.mean()) < 2e-3
         assert abs(vals.std() - 0.02) < 0.02 * (0.12 if t == mxhip.Q4_K else 0.06)
+
+
+def test_q4_k_m_mix_opens_in_the_oracle(tmp_path):
+    """A llama.cpp Q4_K_M-style mix (Q6_K head, attn_v and ffn_down, F16
+    embedding) written by the library opens in the oracle, which multiplies
+    Q6_K and F16 rows as the F32 values the reference's loader makes of
+    them; the step is finite and the types are as written."""
+    p = _write(tmp_path / "q4km.gguf", 2, wtype=mxhip.Q4_K, out_type=mxhip.Q6_K, embd_type=mxhip.F16,
+               attn_v_type=mxhip.Q6_K, ffn_down_type=mxhip.Q6_K)
+    m = mxo.Model(p, 4)
+    i = m.info
+    assert (i.type_wq, i.type_wffn_down, i.type_output, i.type_embd) == (mxo.Q4_K, mxo.Q6_K, mxo.Q6_K, mxo.F16)
+    lg, tr = m.step(1, trace=True)
+    assert np.all(np.isfinite(lg)) and np.all(np.isfinite(tr))
+    m.close()

@@ -6,7 +6,7 @@ unchanged.  Opening the same file with MXH_MODEL_GGUF_LAYOUT keeps the GGUF
 block order, and both must give bit-identical logits and greedy ids, through
 the batched prefill (matrix-core GEMM) and the decode step (GEMV), including
 rows whose last tile is partial (K = 4608: 18 Q4_K blocks, tiles of 16 and 2;
-Q5_K tiles of 8, 8 and 2).
+Q5_K tiles of 8, 8 and 2; K = 6144: 24 Q6_K blocks, tiles of 16 and 8).
 """
 from __future__ import annotations
 
@@ -29,6 +29,11 @@ CASES = {
     "q5k-partial-tiles": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q4_K, qk_norm=False,
                               attn_v_type=mxhip.Q5_K, ffn_down_type=mxhip.Q5_K, arch="llama", rope_theta=5e5,
                               n_embd=512, n_ff=4608, head_dim=128),
+    # Q4_K_M mix with tiled Q6_K: head and attn_v at K = 2048 (one 16-block
+    # tile), ffn_down at K = 6144 (tiles of 16 and 8)
+    "q6k-partial-tiles": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q6_K, embd_type=mxhip.Q4_K, qk_norm=False,
+                              attn_v_type=mxhip.Q6_K, ffn_down_type=mxhip.Q6_K, arch="llama", rope_theta=5e5,
+                              n_embd=2048, n_head=16, n_head_kv=4, n_ff=6144, head_dim=128),
 }
 
 
