@@ -62,17 +62,35 @@ def ensure_model(mxhip, seed: int) -> Path:
     return p
 
 
-def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
-    """Oracle decode on the host cores: greedy steps from position 0 until the
-    time budget is spent (a bounded sample of the same workload)."""
+def cpu_model_name() -> str:
+    """The host CPU's model name (the `lscpu` 'Model name' field, read from
+    /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(path: Path, prompt, budget_s: float, threads: int, p0: int, n_ctx: int) -> dict:
+    """Oracle decode on the host cores: greedy steps at the positions the
+    timed GPU steps run at (from p0 on, the context the bench's prompt and
+    warm-up reach) until the time budget is spent, a bounded sample of the
+    same workload.  The oracle jumps to p0 instead of prefilling the prompt
+    (minutes on the CPU): the cache rows below hold zeros, and the work of a
+    step (every weight, and attention over p0 + 1 rows) does not depend on
+    their values."""
     import numpy as np
 
     import mxo
 
-    m = mxo.Model(path, n_ctx=64, threads=threads)
+    m = mxo.Model(path, n_ctx=n_ctx, threads=threads)
+    m.set_pos(p0)
     t0 = time.perf_counter()
     n = 0
-    tok = int(prompt[0])
+    tok = int(prompt[-1])
     while True:
         lg, _ = m.step(tok)
         tok = int(np.argmax(lg))
@@ -82,8 +100,10 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int) -> dict:
             break
     m.close()
     return {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode steps (positions 0..{n - 1}, lm-head included) of the same model "
-                      f"by the C oracle with {threads} OpenMP threads, {el:.1f}s"}
+            "cpu_model": cpu_model_name(),
+            "sample": f"{n} greedy decode steps at positions {p0}..{p0 + n - 1} (the timed GPU steps' context; "
+                      f"cache rows below zero-filled, same work per step), lm-head included, of the same model by "
+                      f"the C oracle with {threads} OpenMP threads, {el:.1f}s"}
 
 
 def cpu_reference_gemv(budget_s: float, seed: int) -> dict | None:
@@ -123,7 +143,7 @@ def cpu_reference_gemv(budget_s: float, seed: int) -> dict | None:
         tot_s += el / calls
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     return {"value": round(tot_bytes / tot_s / 1e9, 2),
-            "unit": "GB/s", "cores": threads, "kind": "reference",
+            "unit": "GB/s", "cores": threads, "kind": "reference", "cpu_model": cpu_model_name(),
             "sample": "the reference's backend_matmul_rhs_transposed (its CPU sources, OpenMP) on the four Q4_K shapes "
                       "of BASELINE config 2, each repeated for about a quarter of the budget; value = algorithmic bytes "
                       "of one call per shape over the summed per-call times",
@@ -375,7 +395,8 @@ def main() -> int:
     if args.all_configs:
         out["configs"] = run_extra_configs(mxhip, args.seed, mxhip.MODEL_NO_GRAPH if args.eager else 0)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(path, prompt, args.cpu_seconds, min(16, os.cpu_count() or 8))
+        out["cpu_baseline"] = cpu_baseline(path, prompt, args.cpu_seconds, min(16, os.cpu_count() or 8),
+                                           p0=args.prompt + args.warmup, n_ctx=n_ctx)
         if not args.no_microbench:
             ref_gemv = cpu_reference_gemv(8.0, args.seed)
             if ref_gemv:

@@ -1022,6 +1022,22 @@ __device__ __forceinline__ void stage_xq(float* smem, const float* __restrict__ 
     stage_xq_2pass<W>(smem, x, nw, k, eps, red);
 }
 
+// Staging of GEMV_ATTN (k <= 4096): the attention partials merged by
+// AttnIn, in as many units per thread as k needs (a unit past k would load
+// every split's partial for nothing), then quantized as any x.
+template <int W, class F>
+__device__ __forceinline__ void stage_attn(float* smem, const GemvArgs& a, double* red, F&& issue_first) {
+    const AttnIn in{a.part, a.part_splits, a.part_hd, a.k / a.part_hd};
+    const int nb = (a.k + 256 * W - 1) / (256 * W);
+    if constexpr (4096 / (256 * W) >= 4) {
+        if (nb > 2) return stage_xq_nb<W, 4096 / (256 * W), false>(smem, in, nullptr, a.k, a.eps, red, issue_first);
+    }
+    if constexpr (4096 / (256 * W) >= 2) {
+        if (nb > 1) return stage_xq_nb<W, 2, false>(smem, in, nullptr, a.k, a.eps, red, issue_first);
+    }
+    stage_xq_nb<W, 1, false>(smem, in, nullptr, a.k, a.eps, red, issue_first);
+}
+
 // Output modes (epilogues) of one GEMV launch.
 //  GEMV_PLAIN : y[r] = W[r].x (+ res[r])
 //  GEMV_SILU  : W = [gate; up] with n = 2F rows; y[i] = silu(gate_i) * up_i
@@ -1186,8 +1202,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* pw, const f
             wait_vmcnt<kAhead * kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
-            stage_xq_nb<W, 4096 / (256 * W), false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd},
-                                                    nullptr, a.k, a.eps, red, issue_all);
+            stage_attn<W>(xs, a, red, issue_all);
         } else if constexpr (Ty::kIntX) {
             stage_xq<W>(xs, a.x, a.norm_w, a.k, a.eps, red, issue_all);
         } else {
@@ -1223,8 +1238,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint8_t* pw, const f
             wait_vmcnt<kL>();
         };
         if constexpr (MODE == GEMV_ATTN) {
-            stage_xq_nb<W, 4096 / (256 * W), false>(xs, AttnIn{a.part, a.part_splits, a.part_hd, a.k / a.part_hd},
-                                                    nullptr, a.k, a.eps, red, issue_first);
+            stage_attn<W>(xs, a, red, issue_first);
         } else if constexpr (Ty::kIntX) {
             stage_xq<W>(xs, a.x, a.norm_w, a.k, a.eps, red, issue_first);
         } else {

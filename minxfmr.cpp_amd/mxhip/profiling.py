@@ -9,6 +9,10 @@
     rocprofv3 --pmc WRITE_SIZE -d OUT/write -o run --output-format csv -- \
         python3 -m mxhip.profiling workload MODEL
     python3 -m mxhip.profiling traffic OUT/fetch OUT/write > summary.md
+    # bytes the CUs read from L2 for the same launches
+    rocprofv3 --pmc TCP_TCC_READ_REQ_sum -d OUT/l2 -o run --output-format csv -- \
+        python3 -m mxhip.profiling workload MODEL
+    python3 -m mxhip.profiling l2reads OUT/l2
 
     # per-kernel time table from a --kernel-trace --stats run
     python3 -m mxhip.profiling stats OUT/trace/run_kernel_stats.csv
@@ -20,9 +24,10 @@
         --warmup 0 --gemv-reps 1 --no-cpu-baseline --no-long-context
     python3 -m mxhip.profiling mfma OUT/mfma OUT/trace/run_kernel_stats.csv
 
-The workload runs every Q4_K GEMV of the model (per layer: fused q|k|v, o,
-fused gate|up, down) `reps` times, as the bench's roofline pass does, and
-copies 256 MiB once per rep.  FETCH_SIZE and WRITE_SIZE are reported by
+The workload decodes the bench's context (512-token prompt, position 528:
+the o-projection merges four attention splits), then runs every Q4_K GEMV
+of the model (per layer: fused q|k|v, o, fused gate|up, down) `reps` times,
+as the bench's roofline pass does, and copies 256 MiB once per rep.  FETCH_SIZE and WRITE_SIZE are reported by
 rocprofv3 in KiB per dispatch; the calibration factor is the copy's known
 byte count divided by what the counter reads for it.
 """
@@ -47,17 +52,28 @@ def algorithmic_bytes(n: int, k: int) -> int:
     return n * k // 256 * 144 + 4 * k + 4 * n
 
 
+# the bench's context: a 512-token prompt, 16 warm-up steps and 256 timed
+# ones fit 792 positions (four attention splits in the grid); the workload
+# decodes to position 528, so the o-projection merges four live splits
+BENCH_CTX, BENCH_PROMPT, BENCH_STEPS = 792, 512, 17
+
+
 def workload(path: str, reps: int = 4) -> None:
+    import numpy as np
+
     import mxhip
 
     mxhip.init(0)
-    m = mxhip.Model(path, 64)
+    m = mxhip.Model(path, BENCH_CTX, mxhip.MODEL_NO_GRAPH)  # profiled runs stay off graph replay
+    prompt = np.random.default_rng(8).integers(0, m.cfg.n_vocab, BENCH_PROMPT).astype(np.int32)
+    m.generate(prompt, BENCH_STEPS)
     src = mxhip.DeviceBuffer(COPY_BYTES)
     dst = mxhip.DeviceBuffer(COPY_BYTES)
     mxhip.memset(src, 1)
     for _ in range(reps):
         m.bench_gemv(mxhip.Q4_K, 1)
         mxhip.copy(dst, src, COPY_BYTES)
+        m.bench_gemv(mxhip.Q8_0, 1)  # the 661 MB lm-head: a second stream of known size
     mxhip.synchronize()
     m.close()
     print(f"[workload] {reps} passes over the model's Q4_K GEMVs, copy {COPY_BYTES} B each", file=sys.stderr,
@@ -93,6 +109,14 @@ def _per_dispatch(rows, counter: str, reduce=None):
     return out
 
 
+def _big(vals):
+    """The calibration copies among copy dispatches: those of the largest
+    size (the runtime's own small copies, such as the id read-back of a
+    decode, are left out)."""
+    top = max(vals, default=0.0)
+    return [v for v in vals if v > 0.9 * top]
+
+
 def traffic(fetch_dir: str, write_dir: str) -> None:
     rows_f = _counter_rows(fetch_dir)
     rows_w = _counter_rows(write_dir)
@@ -117,8 +141,8 @@ def traffic(fetch_dir: str, write_dir: str) -> None:
     gf, gw = ordered(rows_f, "FETCH_SIZE", is_gemv), ordered(rows_w, "WRITE_SIZE", is_gemv)
     if not gf or not gw:
         raise SystemExit("no Q4_K GEMV dispatch found")
-    cf = [v for k, v in ordered(rows_f, "FETCH_SIZE", is_copy) if k > gf[0][0]]
-    cw = [v for k, v in ordered(rows_w, "WRITE_SIZE", is_copy) if k > gw[0][0]]
+    cf = _big([v for k, v in ordered(rows_f, "FETCH_SIZE", is_copy) if k > gf[0][0]])
+    cw = _big([v for k, v in ordered(rows_w, "WRITE_SIZE", is_copy) if k > gw[0][0]])
     if not cf or not cw:
         raise SystemExit("no calibration copy found")
     kib = COPY_BYTES / 1024
@@ -146,6 +170,83 @@ def traffic(fetch_dir: str, write_dir: str) -> None:
           f"{copy_f:,.0f} KiB and WRITE_SIZE {copy_w:,.0f} KiB per dispatch; factors "
           f"{f_cal:.4f} (fetch) and {w_cal:.4f} (write) are applied above.")
     print(f"TRAFFIC_PER_LAUNCH_BYTES={tot_traffic / len(SHAPES):.0f}")
+
+
+def l2reads(d: str, counter: str = "TCP_TCC_READ_REQ_sum") -> None:
+    """Bytes the vector L1 caches (TCP) request from the L2 (TCC) per Q4_K
+    GEMV launch of the workload, calibrated by the copy (its known read bytes
+    over the requests it issues), against the launch's algorithmic bytes:
+    above 1, the CUs read the same lines from L2 more than once (the
+    o-projection's staging reads every attention split's partials in every
+    workgroup)."""
+    rows = _counter_rows(d)
+    acc: dict[int, tuple[str, float]] = {}
+    for r in rows:
+        if r.get("Counter_Name") == counter:
+            i = int(r["Dispatch_Id"])
+            name, v = acc.get(i, (r["Kernel_Name"], 0.0))
+            acc[i] = (name, v + float(r["Counter_Value"]))
+    items = sorted(acc.items())
+    gemv = [(i, v) for i, (n, v) in items if "gemv_kernel" in n and "Q4KT" in n]
+    copies = _big([v for i, (n, v) in items if "copy" in n.lower() and gemv and i > gemv[0][0]])
+    if not gemv or not copies:
+        raise SystemExit("no Q4_K GEMV or calibration copy dispatch found")
+    per_req = COPY_BYTES / (sum(copies) / len(copies))
+    vals = [v for _, v in gemv]
+    per_pass = 4 * N_LAYER
+    print(f"| shape (N x K) | algorithmic B | L2-to-CU read (scaled) B | L2 reads / algorithmic |")
+    print("|---|---:|---:|---:|")
+    for j, (name, n, k) in enumerate(SHAPES):
+        vs = [vals[i] for i in range(per_pass, len(vals)) if i % 4 == j]
+        b = sum(vs) / len(vs) * per_req
+        alg = algorithmic_bytes(n, k)
+        print(f"| {name} {n} x {k} | {alg:,} | {b:,.0f} | {b / alg:.3f} |")
+    print()
+    print(f"Calibration: the {COPY_BYTES:,} B copy issues {sum(copies) / len(copies):,.0f} {counter} "
+          f"requests per dispatch, {per_req:.1f} B each.")
+
+
+def rdreq(d: str) -> None:
+    """Bytes the L2 reads from memory per dispatch from the request counts by
+    size (TCC_EA0_RDREQ_32B / _64B / _128B, summed over instances), next to
+    the algorithmic bytes: for the Q4_K GEMVs per shape, the copy, and the
+    Q8_0 lm-head (661 MB streamed once per pass)."""
+    rows = _counter_rows(d)
+    per: dict[int, dict] = {}
+    for r in rows:
+        e = per.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"]})
+        e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+
+    def nbytes(e):
+        return 32 * e.get("TCC_EA0_RDREQ_32B_sum", 0) + 64 * e.get("TCC_EA0_RDREQ_64B_sum", 0) + \
+            128 * e.get("TCC_EA0_RDREQ_128B_sum", 0)
+
+    items = sorted(per.items())
+    gemv = [e for _, e in items if "gemv_kernel" in e["name"] and "Q4KT" in e["name"]]
+    first = next(i for i, e in items if "gemv_kernel" in e["name"] and "Q4KT" in e["name"])
+    copies = [e for i, e in items if "copy" in e["name"].lower() and i > first]
+    big = max((nbytes(e) for e in copies), default=0.0)
+    copies = [e for e in copies if nbytes(e) > 0.9 * big]
+    heads = [e for i, e in items if "gemv_kernel" in e["name"] and "Q80T" in e["name"] and i > first]
+    per_pass = 4 * N_LAYER
+    print("| dispatch | algorithmic B | read B (32 / 64 / 128-byte requests) | read / algorithmic | "
+          "requests 32 / 64 / 128 B (share) |")
+    print("|---|---:|---:|---:|---|")
+
+    def row(label, es, alg):
+        b = sum(nbytes(e) for e in es) / len(es)
+        n = [sum(e.get(f"TCC_EA0_RDREQ_{w}B_sum", 0) for e in es) for w in (32, 64, 128)]
+        tot = sum(n) or 1
+        print(f"| {label} | {alg:,} | {b:,.0f} | {b / alg:.3f} | "
+              f"{' / '.join(f'{100 * x / tot:.0f}%' for x in n)} |")
+
+    for j, (name, n, k) in enumerate(SHAPES):
+        row(f"Q4_K {name} {n} x {k}", [gemv[i] for i in range(per_pass, len(gemv)) if i % 4 == j],
+            algorithmic_bytes(n, k))
+    if copies:
+        row("copy (device to device)", copies, COPY_BYTES)
+    if heads:
+        row("Q8_0 lm-head 151936 x 4096", heads, 151936 * 4096 // 32 * 34 + 4 * 4096 + 4 * 151936)
 
 
 def mfma(d: str, stats_csv: str | None = None) -> None:
@@ -228,6 +329,10 @@ def main(argv: list[str]) -> int:
         workload(argv[1], int(argv[2]) if len(argv) > 2 else 4)
     elif cmd == "traffic":
         traffic(argv[1], argv[2])
+    elif cmd == "rdreq":
+        rdreq(argv[1])
+    elif cmd == "l2reads":
+        l2reads(argv[1], *argv[2:3])
     elif cmd == "stats":
         stats(argv[1])
     elif cmd == "mfma":

@@ -1007,6 +1007,12 @@ void mxo_model_info_get(const mxo_model *m, mxo_model_info *info)
 
 void mxo_model_reset(mxo_model *m) { m->pos = 0; }
 int mxo_model_pos(const mxo_model *m) { return m->pos; }
+int mxo_model_set_pos(mxo_model *m, int pos)
+{
+    if (pos < 0 || pos >= m->n_ctx) return -1;
+    m->pos = pos;
+    return 0;
+}
 
 static void proj(const mxo_model *m, const wt *w, const float *x, float *y)
 {

@@ -125,6 +125,11 @@ void mxo_model_reset(mxo_model *m);
  * after each layer) followed by n_embd floats of the final-normed hidden. */
 int mxo_model_step(mxo_model *m, int token, float *logits, float *hidden_trace);
 int mxo_model_pos(const mxo_model *m);
+/* Move the position to `pos` (0 <= pos < n_ctx) without running the
+ * positions before it: their cache rows keep what they hold (zeros after
+ * open).  For timing steps at a given context length, whose work does not
+ * depend on the cached values; not a reference operation. */
+int mxo_model_set_pos(mxo_model *m, int pos);
 
 /* argmax with lowest index on ties (minxfmr.cpp:2091-2115, greedy = order[0]) */
 int mxo_argmax(const float *logits, size_t n);

@@ -60,6 +60,7 @@ def _load():
         "mxo_model_reset": (None, [vp]),
         "mxo_model_step": (ip, [vp, ip, vp, vp]),
         "mxo_model_pos": (ip, [vp]),
+        "mxo_model_set_pos": (ip, [vp, ip]),
         "mxo_argmax": (ip, [vp, sz]),
         "mxo_sample": (ip, [vp, sz, ip, C.c_double, C.c_double, C.c_double, C.POINTER(C.c_uint64)]),
         "mxo_logit_edits": (None, [vp, sz, vp, sz, vp, sz, ip, C.c_double, C.c_double, C.c_double]),
@@ -178,6 +179,11 @@ class Model:
 
     def reset(self):
         lib.mxo_model_reset(self.h)
+
+    def set_pos(self, pos: int):
+        """Jump to position `pos` (cache rows below keep their contents); for timing."""
+        if lib.mxo_model_set_pos(self.h, pos) != 0:
+            raise ValueError(f"position {pos} outside the context")
 
     def close(self):
         if self.h:
