@@ -256,7 +256,7 @@ int mxh_model_position(const mxh_model *m);
  * and trace ((n_layer + 1) * n_embd floats: hidden after each layer, then the
  * final-normed hidden) are host buffers and may be NULL.  Synchronous. */
 /* Sampling of the next token after each step (replaces the greedy argmax):
- * the top_k (1..64) largest logits, softmax at `temperature` in double,
+ * the top_k (1..4096) largest logits, softmax at `temperature` in double,
  * then the top-p and min-p cuts, then a draw from a seeded splitmix64
  * stream (the d-th draw uses state seed + (d+1) * 0x9E3779B97F4A7C15).
  * temperature <= 0 restores greedy decoding.  mxh_model_reset rewinds the

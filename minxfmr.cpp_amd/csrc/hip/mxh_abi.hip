@@ -358,7 +358,8 @@ int mxh_sample(const float* logits, int n, int top_k, double temperature, double
                uint64_t draw, int* token) {
     if (int rc = ensure_ready()) return rc;
     if (!logits || !token || n <= 0) return set_error(MXH_ERR_ARG, "sample: bad arguments");
-    if (top_k < 1 || top_k > 64 || top_k > n) return set_error(MXH_ERR_ARG, "sample: top_k %d outside 1..min(64, n)", top_k);
+    if (top_k < 1 || top_k > kSampleTopKMax || top_k > n)
+        return set_error(MXH_ERR_ARG, "sample: top_k %d outside 1..min(%d, n)", top_k, kSampleTopKMax);
     void *prm = nullptr, *cand = nullptr;
     if (int rc = stage(0, sizeof(SampleParams) + sizeof(int), &prm)) return rc;
     if (int rc = stage(1, sample_scratch_keys(n, top_k) * sizeof(uint64_t), &cand)) return rc;

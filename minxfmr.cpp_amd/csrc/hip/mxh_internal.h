@@ -131,6 +131,9 @@ struct SampleParams {
     uint64_t draws;
 };
 size_t sample_scratch_keys(int n, int top_k);
+// largest top_k the device sampler takes (two passes up to 64, a one-
+// workgroup radix select above)
+constexpr int kSampleTopKMax = 4096;
 // Logit edits before the choice (minxfmr.cpp:2047-2089), parameters in
 // device memory: suppressed ids to -inf, then over the last last_n ids of
 // tokens[0 .. *pos] (all when last_n < 0) each distinct id with count c:

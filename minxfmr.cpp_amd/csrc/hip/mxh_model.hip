@@ -751,8 +751,8 @@ bool batched_prefill_supported(const mxh_model* m) {
 
 int mxh_model_set_sampling(mxh_model* m, int top_k, double temperature, double top_p, double min_p, uint64_t seed) {
     if (!m) return set_error(MXH_ERR_ARG, "set_sampling: null model");
-    if (temperature > 0.0 && (top_k < 1 || top_k > 64))
-        return set_error(MXH_ERR_ARG, "set_sampling: top_k %d outside 1..64", top_k);
+    if (temperature > 0.0 && (top_k < 1 || top_k > kSampleTopKMax))
+        return set_error(MXH_ERR_ARG, "set_sampling: top_k %d outside 1..%d", top_k, kSampleTopKMax);
     hipStream_t st = lib_stream();
     if (int rc = check_hip(hipStreamSynchronize(st), "set_sampling")) return rc;
     if (!(temperature > 0.0)) {

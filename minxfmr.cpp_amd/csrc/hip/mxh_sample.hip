@@ -1,7 +1,7 @@
 // mxh_sample.hip — top-k / temperature / top-p / min-p sampling on the device
 // (reference: src/api/minxfmr.cpp:2091-2171, with a seeded draw).
 //
-// Pass 1: each of W workgroups sorts its slice of the logits in LDS (bitonic,
+// top_k up to 64, two passes.  Pass 1: each of W workgroups sorts its slice of the logits in LDS (bitonic,
 // 64-bit keys: order-preserving bits of the logit above the complemented id,
 // so ties go to the lower id, as the reference's partial_sort with `>` and an
 // increasing initial order) and keeps its best kk = pow2(top_k) candidates.
@@ -9,7 +9,9 @@
 // maxima (they hold every candidate that can rank in the top k), then thread
 // 0 forms the probabilities in double exactly as the reference does (exp of
 // (l - max) / T, normalise, top-p cut and renormalise, min-p cut and
-// renormalise) and draws.  The uniform of draw d is splitmix64 at state
+// renormalise) and draws.  top_k from 65 to 4096: one workgroup selects the
+// k best keys by a radix select, sorts them and chooses the same way.  The
+// uniform of draw d is splitmix64 at state
 // seed + (d + 1) * 0x9E3779B97F4A7C15, the d-th value of the sequence that
 // starts at `seed`.
 #include <hip/hip_runtime.h>
@@ -22,7 +24,8 @@ namespace mxh {
 namespace {
 
 constexpr int kSortMax = 4096;  // keys one workgroup sorts in LDS
-constexpr int kTopKMax = 64;
+constexpr int kTopKMax = 64;      // the two-pass form
+constexpr int kTopKLarge = kSampleTopKMax;  // the one-workgroup radix-select form
 constexpr int kMaxGroups = 2048;  // pass-1 lists one pass-2 workgroup ranks
 
 __device__ __forceinline__ uint64_t sort_key(float v, int idx) {
@@ -81,46 +84,25 @@ __device__ __forceinline__ double draw_uniform(uint64_t seed, uint64_t d) {
     return (double)(z >> 11) * (1.0 / 9007199254740992.0);
 }
 
-// Candidates -> token.  The token goes to out[0] or, with tokens/pos, to
-// tokens[*pos + 1] with the position advanced (the decode loop on device);
-// the draw counter advances either way.
-//
-// Each group's list is sorted, so its first key is the group's maximum.  The
-// k-th largest group maximum T bounds the k-th largest key from below (k
-// group maxima reach it), and only the k groups whose maximum reaches T can
-// hold keys >= T: their lists are the only ones sorted.  Keys are distinct
-// (they carry the id), so the order is the full sort's.
-__global__ __launch_bounds__(1024) void topk_pass2_kernel(const float* __restrict__ logits, const uint64_t* cand,
-                                                          int groups, int kk, SampleParams* prm, int* out,
-                                                          int* tokens, int* pos) {
-    __shared__ uint64_t s[kSortMax];
-    __shared__ uint64_t gmax[kMaxGroups];
-    __shared__ double pr[kTopKMax];
-    const int k = prm->top_k;
-    for (int j = threadIdx.x; j < groups; j += blockDim.x) gmax[j] = cand[(size_t)j * kk];
-    __syncthreads();
-    const int sel = groups < k ? groups : k;  // groups taken
-    for (int j = threadIdx.x; j < groups; j += blockDim.x) {
-        const uint64_t v = gmax[j];
-        int rank = 0;
-        for (int i = 0; i < groups; ++i) rank += gmax[i] > v;
-        if (rank < sel)
-            for (int i = 0; i < kk; ++i) s[rank * kk + i] = cand[(size_t)j * kk + i];
-    }
-    const int p = pow2_at_least(sel * kk);
-    for (int i = sel * kk + threadIdx.x; i < p; i += blockDim.x) s[i] = 0ull;
-    __syncthreads();
-    bitonic_desc(s, p);
+// The choice among the k best ids in order (ids[0 .. k)), as the reference
+// makes it (minxfmr.cpp:2104-2171): the k unnormalised probabilities
+// exp((l - max) / T) in double, computed by the workgroup into pr, then in
+// thread 0, in the reference's order: normalise, top-p cut and renormalise,
+// min-p cut and renormalise, and the draw.  The token goes to out[0] or,
+// with tokens/pos, to tokens[*pos + 1] with the position advanced (the
+// decode loop on the device); the draw counter advances either way.
+// Called by every thread of the workgroup.
+__device__ void choose(const float* __restrict__ logits, const int* ids, int k, double* pr, SampleParams* prm,
+                       int* out, int* tokens, int* pos) {
     const double temperature = prm->temperature;
-    if (temperature > 0.0 && threadIdx.x < k) {
-        // the k unnormalised probabilities, each exp as the reference forms it
-        const double mx = logits[key_id(s[0])];
-        pr[threadIdx.x] = exp(((double)logits[key_id(s[threadIdx.x])] - mx) / temperature);
+    if (temperature > 0.0) {
+        const double mx = logits[ids[0]];
+        for (int i = threadIdx.x; i < k; i += blockDim.x) pr[i] = exp(((double)logits[ids[i]] - mx) / temperature);
     }
     __syncthreads();
     if (threadIdx.x != 0) return;
     double top_p = prm->top_p, min_p = prm->min_p;
-    int pick = key_id(s[0]);
+    int pick = ids[0];
     if (temperature > 0.0) {
         if (top_p <= 0.0 || top_p > 1.0) top_p = 1.0;
         if (min_p < 0.0) min_p = 0.0;
@@ -160,11 +142,11 @@ __global__ __launch_bounds__(1024) void topk_pass2_kernel(const float* __restric
             for (int i = 0; i < m; ++i) total += pr[i];
             const double u = draw_uniform(prm->seed, prm->draws) * total;
             double cum = 0.0;
-            pick = key_id(s[m - 1]);
+            pick = ids[m - 1];
             for (int i = 0; i < m; ++i) {
                 cum += pr[i];
                 if (u < cum) {
-                    pick = key_id(s[i]);
+                    pick = ids[i];
                     break;
                 }
             }
@@ -177,6 +159,93 @@ __global__ __launch_bounds__(1024) void topk_pass2_kernel(const float* __restric
         tokens[q + 1] = pick;
         *pos = q + 1;
     }
+}
+
+// Pass 2 (top_k <= kTopKMax): candidates -> token.
+//
+// Each group's list is sorted, so its first key is the group's maximum.  The
+// k-th largest group maximum T bounds the k-th largest key from below (k
+// group maxima reach it), and only the k groups whose maximum reaches T can
+// hold keys >= T: their lists are the only ones sorted.  Keys are distinct
+// (they carry the id), so the order is the full sort's.
+__global__ __launch_bounds__(1024) void topk_pass2_kernel(const float* __restrict__ logits, const uint64_t* cand,
+                                                          int groups, int kk, SampleParams* prm, int* out,
+                                                          int* tokens, int* pos) {
+    __shared__ uint64_t s[kSortMax];
+    __shared__ uint64_t gmax[kMaxGroups];
+    __shared__ double pr[kTopKMax];
+    __shared__ int ids[kTopKMax];
+    const int k = prm->top_k;
+    for (int j = threadIdx.x; j < groups; j += blockDim.x) gmax[j] = cand[(size_t)j * kk];
+    __syncthreads();
+    const int sel = groups < k ? groups : k;  // groups taken
+    for (int j = threadIdx.x; j < groups; j += blockDim.x) {
+        const uint64_t v = gmax[j];
+        int rank = 0;
+        for (int i = 0; i < groups; ++i) rank += gmax[i] > v;
+        if (rank < sel)
+            for (int i = 0; i < kk; ++i) s[rank * kk + i] = cand[(size_t)j * kk + i];
+    }
+    const int p = pow2_at_least(sel * kk);
+    for (int i = sel * kk + threadIdx.x; i < p; i += blockDim.x) s[i] = 0ull;
+    __syncthreads();
+    bitonic_desc(s, p);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) ids[i] = key_id(s[i]);
+    __syncthreads();
+    choose(logits, ids, k, pr, prm, out, tokens, pos);
+}
+
+// top_k in (kTopKMax, kTopKLarge]: one workgroup finds the k-th largest key T
+// by a radix select over the 64-bit keys (8-bit digits, most significant
+// first: per digit a histogram of the keys that share the digits chosen so
+// far, then the digit whose bin holds the k-th), gathers the k keys >= T
+// (exactly k: keys are distinct), sorts them and chooses as pass 2 does.
+// Same keys, same order, same choice as the two-pass form.
+__global__ __launch_bounds__(1024) void topk_large_kernel(const float* __restrict__ logits, int n, SampleParams* prm,
+                                                          int* out, int* tokens, int* pos) {
+    __shared__ uint64_t s[kTopKLarge];  // the k keys, then their probabilities (doubles)
+    __shared__ int ids[kTopKLarge];
+    __shared__ unsigned hist[256];
+    __shared__ uint64_t prefix_s;
+    __shared__ int need_s, count_s;
+    const int k = prm->top_k;
+    uint64_t prefix = 0;
+    int need = k;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int b = threadIdx.x; b < 256; b += blockDim.x) hist[b] = 0u;
+        __syncthreads();
+        const uint64_t hi_mask = shift == 56 ? 0ull : ~0ull << (shift + 8);
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const uint64_t key = sort_key(logits[i], i);
+            if ((key & hi_mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int above = 0, b = 255;
+            for (; b > 0; --b) {
+                if (above + (int)hist[b] >= need) break;
+                above += (int)hist[b];
+            }
+            prefix_s = prefix | ((uint64_t)b << shift);
+            need_s = need - above;
+            count_s = 0;
+        }
+        __syncthreads();
+        prefix = prefix_s;
+        need = need_s;
+    }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t key = sort_key(logits[i], i);
+        if (key >= prefix) s[atomicAdd(&count_s, 1)] = key;
+    }
+    const int p = pow2_at_least(k);
+    __syncthreads();
+    for (int i = k + threadIdx.x; i < p; i += blockDim.x) s[i] = 0ull;
+    __syncthreads();
+    bitonic_desc(s, p);
+    for (int i = threadIdx.x; i < k; i += blockDim.x) ids[i] = key_id(s[i]);
+    __syncthreads();
+    choose(logits, ids, k, reinterpret_cast<double*>(s), prm, out, tokens, pos);
 }
 
 }  // namespace
@@ -199,6 +268,7 @@ void sample_shape(int n, int top_k, int* groups, int* slice, int* kk) {
 }
 
 size_t sample_scratch_keys(int n, int top_k) {
+    if (top_k > kTopKMax) return 1;  // the radix-select form needs no candidate lists
     int g, sl, kk;
     sample_shape(n, top_k, &g, &sl, &kk);
     return (size_t)g * kk;
@@ -206,7 +276,11 @@ size_t sample_scratch_keys(int n, int top_k) {
 
 int sample_launch(const float* logits, int n, SampleParams* prm, int top_k, uint64_t* cand, int* out, int* tokens,
                   int* pos, hipStream_t st) {
-    if (n <= 0 || top_k < 1 || top_k > kTopKMax || top_k > n) return MXH_ERR_ARG;
+    if (n <= 0 || top_k < 1 || top_k > kTopKLarge || top_k > n) return MXH_ERR_ARG;
+    if (top_k > kTopKMax) {
+        hipLaunchKernelGGL(topk_large_kernel, dim3(1), dim3(1024), 0, st, logits, n, prm, out, tokens, pos);
+        return MXH_OK;
+    }
     int g, sl, kk;
     sample_shape(n, top_k, &g, &sl, &kk);
     if ((size_t)g * kk > (size_t)kSortMax || g > kMaxGroups) return MXH_ERR_UNSUPPORTED;
