@@ -234,6 +234,18 @@ __device__ __forceinline__ float4 ld_agent4(__amdgpu_buffer_rsrc_t r, int byte_o
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte load through a buffer descriptor over [base, base + bytes) with
+// the default cache policy; offsets at or past `bytes` read 0 without a
+// branch, so a run of such loads keeps a fixed count for s_waitcnt
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld_buf16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // wait until every memory operation this thread issued has completed
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 

@@ -64,6 +64,13 @@ constexpr int kAttnMaxGroup = 8;    // q heads per kv head
 // 256-position splits at run time too)
 constexpr int kAttnSplitPos = 256;
 constexpr int kAttnRunSplitPos = 128;
+// Contexts of at least kAttnGroupMinCtx positions run the grouped kernel
+// (attention_group_kernel: one workgroup per kv head and split), with the
+// grid's splits sized to its capacity and at least kAttnGroupRunPos
+// positions per active split
+constexpr int kAttnGroupMinCtx = 4096;
+constexpr int kAttnGroupRunPos = 64;
+constexpr int kAttnGroupBlocks = 3;  // 16-position blocks per wave: 384 positions per workgroup
 
 // Bias, per-head rmsnorm (QK-norm) and RoPE of one head slice, done by one
 // wave in two parts: head_fetch requests every global input (so a kernel can
@@ -390,6 +397,316 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
     }
 }
 
+// Fold v[0..N) (N a multiple of 4) over the lanes of equal lane % LPP
+// (sums over the position groups of a wave), two values per lane swap for
+// lane bits 5 and 4: afterwards register w[k] holds, in 16-lane row r, the
+// sum of v[4 k + c(r)], c = {0, 2, 1, 3}; lanes below 16 in row r with
+// lane % 16 < LPP carry it (lane bits below 4 and at or above log2 LPP were
+// folded lane by lane first).
+template <int LPP, int N>
+__device__ __forceinline__ void fold_pairs(float (&v)[N], float (&w)[N / 4]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if constexpr (LPP <= 4) v[k] += lane_xor<4>(v[k]);
+        if constexpr (LPP <= 8) v[k] += lane_xor<8>(v[k]);
+    }
+    float u[N / 2];
+#pragma unroll
+    for (int k = 0; k < N / 2; ++k) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[2 * k]), __float_as_uint(v[2 * k + 1]),
+                                                        false, false);
+        u[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[2 * k]), __float_as_uint(u[2 * k + 1]),
+                                                        false, false);
+        w[k] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+}
+
+// Decode attention for long contexts (transformer.cpp:529-629), grouped by
+// kv head: workgroup (g, s) serves all G = nh / nkv q heads of kv head g over
+// split s of the L = pos + 1 positions, so each K/V byte of the cache is read
+// into one CU once.
+//
+// S = min(gridDim.y, ceil(L / kAttnGroupRunPos)) splits are active; split s
+// holds positions [L s / S, L (s + 1) / S), at most 8 waves x NB blocks x 16
+// = 384, which the grid size guarantees (attention_splits).  Wave w takes the
+// 16-position blocks w, w + 8, w + 16; waves 0 .. G-1 first prepare one q
+// head each (bias, QK-norm, RoPE) and publish it through an LDS counter that
+// the others poll before their first scores (no barrier behind any wave's
+// load issue), and each wave issues block b + 1's K and V loads before block
+// b is computed (a
+// wave's loads issue in order and stall while the CU's memory queue is full,
+// so work placed behind later loads waits for their issue).  Loads go through buffer
+// descriptors over the cache rows [0, rows_end): rows past them read 0
+// without a branch, so every wait is for exactly the loads it needs; blocks
+// past the split are loaded as zeros and not computed.  Per block:
+//   - scores on the matrix cores: S[p][h] = K[p] . q'[h] by
+//     v_mfma_f32_16x16x32_f16 with K (exact fp16) as A, lane l holding
+//     position l % 16 and dims 32 ks + 8 (l / 16) .. +8 of k-step ks, and q' =
+//     q scale log2 e as B, columns h < G, split into fp16 hi and lo (two
+//     products, about 22 significant bits of q).  Lane l then holds head
+//     l % 16 at positions 4 (l / 16) + i;
+//   - the running max and sum per head (online softmax); the probabilities
+//     and the rescale factor go through LDS to the layout of the V rows;
+//   - exp-weighted V on the VALU, lane l holding 8 dims (l % LPP) of position
+//     row l / LPP, V as loaded (16 bytes per lane and row).
+// The eight wave partials merge through LDS; the split's partial (max in
+// base-2 units, sum, V sums) goes to `part` in attention_kernel's layout,
+// slot (g G + h) gridDim.y + s, for attention_merge_kernel.  In the last
+// split the wave whose blocks hold position pos prepares the current token's
+// k and v, rounds them through fp16, appends them to the cache and uses them
+// from LDS, as attention_kernel does.
+template <int LPP, int G>
+__global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, __half* pkc, __half* pvc,
+                                                              const float* pqkv, AttnArgs a) {
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    MXH_ATTN_STAMP(0);
+    a.pos = ppos;
+    a.kc = pkc;
+    a.vc = pvc;
+    a.qkv = pqkv;
+    constexpr int HD = LPP * 8, PR = 64 / LPP, NW = 8, NB = kAttnGroupBlocks, KS = HD / 32, RB = 16 / PR;
+    static_assert(G <= NW, "one preparing wave per q head");
+    __shared__ float qs[G][HD];
+    __shared__ int qready;  // q heads published in qs
+    __shared__ float kvt[HD];
+    __shared__ __align__(16) __half kvh[2][HD];
+    __shared__ __align__(16) float ps[NW][16][G];
+    __shared__ __align__(16) float pal[NW][G];
+    __shared__ float wm[NW][G], wl[NW][G];
+    __shared__ float wacc[NW][G * 8][16];
+
+    const int kvd = a.nkv * HD, qd = a.nh * HD;
+    const int g = blockIdx.x, s = blockIdx.y, SM = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sub = lane % LPP, pr = lane / LPP, l16 = lane & 15, quad = lane >> 4;
+    const int pos = *a.pos, L = pos + 1;
+    const int S = min(SM, (L + kAttnGroupRunPos - 1) / kAttnGroupRunPos);
+    float* part_v = a.part;                            // [nh][SM][HD]
+    float* part_ml = a.part + (size_t)a.nh * SM * HD;  // [nh][SM][2]
+    if (s >= S) {
+        if (tid < G) {
+            const size_t slot = (size_t)(g * G + tid) * SM + s;
+            part_ml[slot * 2] = -INFINITY;
+            part_ml[slot * 2 + 1] = 0.f;
+        }
+        return;
+    }
+    const int p0 = (int)((int64_t)L * s / S), p1 = (int)((int64_t)L * (s + 1) / S);
+    const bool last = s == S - 1;
+    const int rows_end = last ? pos : p1;  // cache rows read: [p0, rows_end)
+    // wave t < G prepares q head t and publishes it; the wave whose blocks
+    // hold position pos (last split) prepares the current token's k and v
+    const bool q_wave = wave < G;
+    const bool kv_wave = last && ((pos - p0) >> 4) % NW == wave;
+    if (tid == 0) qready = 0;
+    __syncthreads();
+
+    const double* cs = a.rope_cs + (size_t)pos * HD;
+    HeadIn qin{}, kin_h{}, vin_h{};
+    if (q_wave) {
+        const size_t off = (size_t)(g * G + wave) * HD;
+        qin = head_fetch(a.qkv + off, a.bias ? a.bias + off : nullptr, a.q_norm, cs, HD);
+    }
+    if (kv_wave) {
+        const size_t ko = (size_t)qd + (size_t)g * HD, vo = (size_t)(qd + kvd) + (size_t)g * HD;
+        kin_h = head_fetch(a.qkv + ko, a.bias ? a.bias + ko : nullptr, a.k_norm, cs, HD);
+        vin_h = head_fetch(a.qkv + vo, a.bias ? a.bias + vo : nullptr, nullptr, cs, HD);
+    }
+    if (q_wave) {
+        head_finish(qin, a.q_norm != nullptr, qs[wave], HD, a.eps, a.neox);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&qready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (kv_wave) {
+        head_finish(kin_h, a.k_norm != nullptr, kvt, HD, a.eps, a.neox);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        // rounded through fp16 like every cached position and appended (this
+        // workgroup is the only one of kv head g holding position pos)
+        __half* kdst = a.kc + (size_t)pos * kvd + (size_t)g * HD;
+        __half* vdst = a.vc + (size_t)pos * kvd + (size_t)g * HD;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int e = lane + 64 * r;
+            if (e < HD) {
+                const __half kh = __float2half_rn(kvt[e]), vh = __float2half_rn(vin_h.v[r]);
+                kvh[0][e] = kh;
+                kvh[1][e] = vh;
+                kdst[e] = kh;
+                vdst[e] = vh;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+    // K (matrix-core operand layout) and V (row layout) of block b into slot b % 2
+    uint4 kraw[2][KS], vraw[2][RB];
+    const __amdgpu_buffer_rsrc_t krs = buf_rsrc(a.kc, rows_end * kvd * 2);
+    const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(a.vc, rows_end * kvd * 2);
+    auto issue = [&](int b) {
+        const int b0 = p0 + (wave + NW * b) * 16;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            kraw[b & 1][ks] = ld_buf16(krs, ((b0 + l16) * kvd + g * HD + 32 * ks + 8 * quad) * 2);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) vraw[b & 1][r] = ld_buf16(vrs, ((b0 + r * PR + pr) * kvd + g * HD + sub * 8) * 2);
+    };
+    issue(0);
+    MXH_ATTN_STAMP(1);
+    // wait until the G q heads are published (the preparing waves never
+    // wait on anything; the bound only keeps a wave from spinning forever)
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+        if (__hip_atomic_load(&qready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= G) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    MXH_ATTN_STAMP(2);
+
+    // q' = q scale log2 e as the B operand: column l16 < G is head l16, fp16
+    // hi and lo halves
+    const float scale2 = a.scale * 1.4426950408889634f;
+    h8 qhi[KS], qlo[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = l16 < G ? qs[l16 < G ? l16 : 0][32 * ks + 8 * quad + e] * scale2 : 0.f;
+            const _Float16 hi = (_Float16)v;
+            qhi[ks][e] = hi;
+            qlo[ks][e] = (_Float16)(v - (float)hi);
+        }
+    // running max / sum per head (score layout: column l16) and V sums
+    // (row layout: acc[h 8 + e] is dim sub 8 + e of head h)
+    float m_run = -INFINITY, l_run = 0.f;
+    float acc[G * 8];
+#pragma unroll
+    for (int k = 0; k < G * 8; ++k) acc[k] = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (b + 1 < NB) issue(b + 1);
+        const int b0 = p0 + (wave + NW * b) * 16;  // wave-uniform
+        if (b0 >= p1) continue;
+        // scores (base-2 units) on the matrix cores; the current position's k
+        // (last split) from the LDS copy in place of the zeros its load returned
+        uint4 kin[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kin[ks] = kraw[b & 1][ks];
+        if (last && pos - b0 < 16) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                if (b0 + l16 == pos) kin[ks] = *reinterpret_cast<const uint4*>(&kvh[0][32 * ks + 8 * quad]);
+        }
+        f4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const h8 kv = __builtin_bit_cast(h8, kin[ks]);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qhi[ks], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qlo[ks], sacc, 0, 0, 0);
+        }
+        float sc[4];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = (l16 < G && b0 + 4 * quad + i < p1) ? sacc[i] : -INFINITY;
+            bm = fmaxf(bm, sc[i]);
+        }
+        bm = fmaxf(bm, lane_xor<16>(bm));
+        bm = fmaxf(bm, lane_xor<32>(bm));
+        // the block holds at least one position, so mn is finite for l16 < G
+        const float mn = fmaxf(m_run, bm);
+        const float al = __builtin_amdgcn_exp2f(m_run - mn);  // 0 while m_run = -inf
+        float bs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sc[i] = __builtin_amdgcn_exp2f(sc[i] - mn);
+            bs += sc[i];
+        }
+        bs += lane_xor<16>(bs);
+        bs += lane_xor<32>(bs);
+        l_run = fmaf(l_run, al, bs);
+        m_run = mn;
+        // probabilities and rescale factors to the row layout
+        if (l16 < G) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ps[wave][4 * quad + i][l16] = sc[i];
+            if (quad == 0) pal[wave][l16] = al;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        float alh[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) alh[h] = pal[wave][h];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[h * 8 + e] *= alh[h];
+        // exp-weighted V; the current position's v from the LDS copy
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int q = r * PR + pr;
+            uint4 vin = vraw[b & 1][r];
+            if (last && pos - b0 - r * PR >= 0 && pos - b0 - r * PR < PR) {
+                if (b0 + q == pos) vin = *reinterpret_cast<const uint4*>(&kvh[1][sub * 8]);
+            }
+            float p[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) p[h] = ps[wave][q][h];
+            float vf[8];
+            half8_to_float(vin, vf);
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h * 8 + e] = fmaf(p[h], vf[e], acc[h * 8 + e]);
+        }
+        // the next block's writes to ps / pal come after these reads
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+    MXH_ATTN_STAMP(5);
+    // the wave's partials (V sums folded over its position rows) to LDS:
+    // wacc[wave][h 8 + e][sub] holds dim sub 8 + e of head h
+    float wsum[G * 2];
+    fold_pairs<LPP, G * 8>(acc, wsum);
+    if (l16 < LPP) {
+        const int r = quad, c = ((r & 1) << 1) | (r >> 1);
+#pragma unroll
+        for (int k = 0; k < G * 2; ++k) wacc[wave][4 * k + c][l16] = wsum[k];
+    }
+    if (lane < G) {
+        wm[wave][lane] = m_run;
+        wl[wave][lane] = l_run;
+    }
+    __syncthreads();
+    MXH_ATTN_STAMP(6);
+    // merge the waves per head and store the split's partials
+    for (int i = tid; i < G * HD; i += 64 * NW) {
+        const int h = i / HD, t = i % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][h]);
+        float l = 0.f, v = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = wm[w][h];
+            const float ww = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+            l = fmaf(ww, wl[w][h], l);
+            v = fmaf(ww, wacc[w][h * 8 + t % 8][t / 8], v);
+        }
+        const size_t slot = (size_t)(g * G + h) * SM + s;
+        part_v[slot * HD + t] = v;
+        if (t == 0) {
+            part_ml[slot * 2] = M;
+            part_ml[slot * 2 + 1] = l;
+        }
+    }
+    MXH_ATTN_STAMP(7);
+}
+
 // ---- batched prefill ---------------------------------------------------------
 
 // Row-batched head preparation for prompt tokens p0 .. p0+m-1: workgroup
@@ -520,13 +837,39 @@ namespace {
 
 }  // namespace
 
-// Workgroups (splits) per kv head for a context of n_ctx positions: one per
-// kAttnSplitPos positions, at most kAttnMaxSplits (the o-projection merges
-// that many partials per q head in its x staging).
+// Whether a context of n_ctx positions runs the grouped kernel: long
+// contexts, and q heads per kv head a power of two
+static bool attention_grouped(int n_ctx, int nh, int nkv, int hd) {
+    const int G = nkv > 0 ? nh / nkv : 0;
+    // the cache's byte offsets are 32-bit buffer offsets
+    return n_ctx >= kAttnGroupMinCtx && (G == 1 || G == 2 || G == 4 || G == 8) &&
+           (int64_t)n_ctx * nkv * hd * 2 < ((int64_t)1 << 31);
+}
+
+// CUs of the current device (256 on MI355X), read once
+static int attention_cus() {
+    static int n_cu = 0;
+    if (!n_cu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu < 1)
+            n_cu = 256;
+    }
+    return n_cu;
+}
+
+// Splits (partials per q head) for a context of n_ctx positions.  Per-q-head
+// kernel: one per kAttnSplitPos positions, at most kAttnMaxSplits (the
+// o-projection merges that many partials per q head in its x staging).
+// Grouped kernel: one workgroup per CU over the kv heads (no CU takes two)
+// unless a split would then exceed a workgroup's 8 x 16 kAttnGroupBlocks
+// positions; the merge kernel combines them before the o-projection.
 int attention_splits(int n_ctx, int nh, int nkv, int hd) {
-    (void)nh;
-    (void)nkv;
-    (void)hd;
+    if (attention_grouped(n_ctx, nh, nkv, hd)) {
+        const int cap = 8 * 16 * kAttnGroupBlocks;
+        const int need = (n_ctx + cap - 1) / cap, fill = attention_cus() / nkv;
+        return need > fill ? need : fill;
+    }
     const int S = (n_ctx + kAttnSplitPos - 1) / kAttnSplitPos;
     return S < 1 ? 1 : S > kAttnMaxSplits ? kAttnMaxSplits : S;
 }
@@ -537,8 +880,27 @@ bool attention_supported(int nh, int nkv, int hd) {
     return nkv > 0 && nh % nkv == 0 && nh / nkv <= kAttnMaxGroup && (hd == 32 || hd == 64 || hd == 128);
 }
 
+template <int LPP>
+static void attention_group_launch(const AttnArgs& a, dim3 grid, hipStream_t st) {
+    switch (a.nh / a.nkv) {
+    case 1: hipLaunchKernelGGL((attention_group_kernel<LPP, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 2: hipLaunchKernelGGL((attention_group_kernel<LPP, 2>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 4: hipLaunchKernelGGL((attention_group_kernel<LPP, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    default: hipLaunchKernelGGL((attention_group_kernel<LPP, 8>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    }
+}
+
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
+    if (attention_grouped(n_ctx, a.nh, a.nkv, a.hd)) {
+        const dim3 grid(a.nkv, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
+        switch (a.hd) {
+        case 32: attention_group_launch<4>(a, grid, st); break;
+        case 64: attention_group_launch<8>(a, grid, st); break;
+        default: attention_group_launch<16>(a, grid, st); break;
+        }
+        return MXH_OK;
+    }
     const dim3 grid(a.nh, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
     switch (a.hd) {
     case 32: hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
@@ -549,47 +911,52 @@ int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
 }
 
 // att[h][t] = sum_s w_s V_s[t] / sum_s w_s l_s, w_s = 2^(m_s - max m) over
-// the splits of q head h (a split with m_s = -inf held no position); one
-// thread per output
-__global__ void attention_merge_kernel(const float* __restrict__ part, int S, int nh, int hd, float* __restrict__ att) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nh * hd) return;
-    const int h = i / hd, t = i % hd;
+// the splits of q head h (a split with m_s = -inf held no position).  One
+// wave per (q head, 8 dims): lane s takes splits s, s + 64, ..., keeping a
+// running (max, sum, 8 V sums), so with at most 64 splits every load of the
+// wave is in flight at once; the lanes then merge by wave reductions.
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float* __restrict__ part, int S, int nh, int hd,
+                                                              float* __restrict__ att) {
+    const int lane = threadIdx.x & 63, groups = hd / 8;
+    const int wid = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    if (wid >= nh * groups) return;  // whole waves
+    const int h = wid / groups, t0 = (wid % groups) * 8;
     const float* ml = part + (size_t)nh * S * hd + (size_t)h * S * 2;
-    const float* pv = part + (size_t)h * S * hd + t;
-    // eight splits' loads in flight at a time
-    float M = -INFINITY;
-    for (int s0 = 0; s0 < S; s0 += 8) {
+    const float* pv = part + (size_t)h * S * hd + t0;
+    float m = -INFINITY, l = 0.f, v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = lane; s < S; s += 64) {
+        const float2 q = *reinterpret_cast<const float2*>(ml + 2 * s);
+        const float4 a = *reinterpret_cast<const float4*>(pv + (size_t)s * hd);
+        const float4 b = *reinterpret_cast<const float4*>(pv + (size_t)s * hd + 4);
+        // an empty split's V partial is whatever an earlier launch left
+        // (possibly not finite): skip it rather than weight it by 0
+        if (q.x == -INFINITY) continue;
+        const float mn = fmaxf(m, q.x);
+        const float al = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+        const float w = __builtin_amdgcn_exp2f(q.x - mn);
+        const float u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        l = fmaf(w, q.y, l * al);
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (s0 + u < S) M = fmaxf(M, ml[2 * (s0 + u)]);
+        for (int e = 0; e < 8; ++e) v[e] = fmaf(w, u[e], v[e] * al);
+        m = mn;
     }
-    float den = 0.f, v = 0.f;
-    for (int s0 = 0; s0 < S; s0 += 8) {
-        float2 mu[8];
-        float vu[8];
+    const float M = wave_max_all(m);
+    const float sc = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+    const float den = wave_sum_all(l * sc);
+    float out[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const bool in = s0 + u < S;
-            mu[u] = in ? *reinterpret_cast<const float2*>(ml + 2 * (s0 + u)) : make_float2(-INFINITY, 0.f);
-            vu[u] = in ? pv[(size_t)(s0 + u) * hd] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            // an empty split's V partial is whatever an earlier launch left
-            // (possibly not finite): skip it rather than weight it by 0
-            if (mu[u].x == -INFINITY) continue;
-            const float w = __builtin_amdgcn_exp2f(mu[u].x - M);
-            den = fmaf(w, mu[u].y, den);
-            v = fmaf(w, vu[u], v);
-        }
+    for (int e = 0; e < 8; ++e) out[e] = wave_sum_all(v[e] * sc);
+    if (lane == 0) {
+        float4* dst = reinterpret_cast<float4*>(att + (size_t)h * hd + t0);
+        dst[0] = make_float4(out[0] / den, out[1] / den, out[2] / den, out[3] / den);
+        dst[1] = make_float4(out[4] / den, out[5] / den, out[6] / den, out[7] / den);
     }
-    att[i] = v / den;
 }
 
 int attention_merge_launch(const float* part, int splits, int nh, int hd, float* att, hipStream_t st) {
-    if (splits < 1 || nh < 1 || hd < 1) return MXH_ERR_ARG;
-    hipLaunchKernelGGL(attention_merge_kernel, dim3((nh * hd + 63) / 64), dim3(64), 0, st, part, splits, nh, hd, att);
+    if (splits < 1 || nh < 1 || hd < 8 || hd % 8) return MXH_ERR_ARG;
+    const int waves = nh * (hd / 8);
+    hipLaunchKernelGGL(attention_merge_kernel, dim3((waves + 3) / 4), dim3(256), 0, st, part, splits, nh, hd, att);
     return MXH_OK;
 }
 

@@ -124,10 +124,13 @@ int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hi
 }
 
 // Whether the o-projection merges the attention partials in its x staging
-// (GEMV_ATTN: quantized rows of at most 4096 inputs); otherwise a merge
-// kernel writes the attention output first.
+// (GEMV_ATTN: quantized rows of at most 4096 inputs, at most kAttnMaxSplits
+// partials per q head); otherwise a merge kernel writes the attention output
+// first (always for the grouped kernel of long contexts).
 bool o_merges(const mxh_model* m, const DevW& o) {
-    return gemv_int_x(o.type) && o.cols <= 4096;
+    const mxh_model_config& c = m->cfg;
+    return gemv_int_x(o.type) && o.cols <= 4096 &&
+           attention_splits(c.n_ctx, c.n_head, c.n_head_kv, c.head_dim) <= kAttnMaxSplits;
 }
 
 // the o-projection and residual of the decode step, from the attention partials

@@ -76,16 +76,24 @@ def test_per_layer_activations_and_logits(mxh, tmp_path, name, flags):
 
 @pytest.mark.parametrize("name,n_ctx,warm", [("q4k-qknorm", 600, 300), ("q5_0-gqa8", 1100, 300),
                                              ("q8-tied", 1100, 300), ("f32-hd128", 4000, 520),
-                                             ("q4k-qknorm", 8200, 4150)])
+                                             ("q4k-qknorm", 8200, 4150), ("q5_0-gqa8", 4200, 4100),
+                                             ("f32-hd128", 4096, 600), ("q8-tied", 4500, 4480)])
 def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
-    """Contexts long enough for several attention splits per q head.  The
-    grid holds min(8, ceil(n_ctx / 256)) splits and a launch uses
+    """Contexts long enough for several attention splits per q head.
+    Below 4096 positions of context the per-q-head kernel runs: the grid
+    holds min(8, ceil(n_ctx / 256)) splits and a launch uses
     min(grid, ceil(L / 128)) of them; the rest leave empty partials that the
     merge must skip.  Checked at positions warm .. warm+5 (and 0 .. 2):
     3 of 3 splits (Q4_K o-projection merging in its x staging), 3 of 5
     (Q5_0 with hd 32 and 8 q heads per kv head; Q8_0 tied, the tiled
-    two-row merge), 5 of 8 (F32 o-projection: the separate merge kernel)
-    and 8 of 8 at L about 4150."""
+    two-row merge), 5 of 8 (F32 o-projection: the separate merge kernel).
+    From 4096 the grouped kernel runs (one workgroup per kv head and split,
+    the grid one workgroup per CU over the kv heads, at least 64 positions
+    per active split, the merge kernel before the o-projection): hd 64 with
+    2 q heads per kv head at L about 4150 (65 of 128 splits), hd 32 with 8
+    q heads per kv head at L about 4100 (65 of 256), hd 128 with one q head
+    per kv head at L about 600 (10 of 128, F32 rows), and splits of 35
+    positions near the end of a 4500-position context (all 128)."""
     p = build(tmp_path, name)
     gm = mxhip.Model(p, n_ctx)
     om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
