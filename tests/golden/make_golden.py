@@ -14,7 +14,11 @@ Outputs
                       Q4_K/Q8_0/Q5_0 block dequant, rhs-transposed matmul,
                       rmsnorm, rope (both pairings), softmax, and a 2-layer
                       decoder stack (transformer_forward_single_layer).
-The reference itself never leaves the build container; only these vectors do.
+The reference's sources never leave the build container.  The CPU library
+compiled from them (oracle/_ref/libmxref.so, git-ignored, so never committed)
+travels with the working tree to GPU runs, where only the tests' checkers and
+bench.py's reference-kind CPU-baseline leg load it; these vectors are the
+committed record of its outputs.
 """
 from __future__ import annotations
 
