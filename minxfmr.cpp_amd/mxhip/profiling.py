@@ -14,6 +14,13 @@
         python3 -m mxhip.profiling workload MODEL
     python3 -m mxhip.profiling l2reads OUT/l2
 
+    # the long-context decode attention (grouped kernel + merge) at L = 8192
+    rocprofv3 --pmc FETCH_SIZE -d OUT/lf -o run --output-format csv -- python3 -m mxhip.profiling workload_long MODEL
+    rocprofv3 --pmc WRITE_SIZE -d OUT/lw -o run --output-format csv -- python3 -m mxhip.profiling workload_long MODEL
+    rocprofv3 --kernel-trace --stats -d OUT/lt -o run --output-format csv -- \
+        python3 -m mxhip.profiling workload_long MODEL
+    python3 -m mxhip.profiling attn OUT/lf OUT/lw OUT/lt/run_kernel_stats.csv
+
     # per-kernel time table from a --kernel-trace --stats run
     python3 -m mxhip.profiling stats OUT/trace/run_kernel_stats.csv
 
@@ -78,6 +85,96 @@ def workload(path: str, reps: int = 4) -> None:
     m.close()
     print(f"[workload] {reps} passes over the model's Q4_K GEMVs, copy {COPY_BYTES} B each", file=sys.stderr,
           flush=True)
+
+
+# the long-context workload: an 8192-token prompt, then
+# decode steps at L = 8192 .. with the grouped attention kernel
+LONG_PROMPT, LONG_STEPS = 8192, 8
+
+
+def workload_long(path: str) -> None:
+    import numpy as np
+
+    import mxhip
+
+    mxhip.init(0)
+    m = mxhip.Model(path, LONG_PROMPT + LONG_STEPS + 8, mxhip.MODEL_NO_GRAPH)  # profiled runs stay off graph replay
+    prompt = np.random.default_rng(55).integers(0, m.cfg.n_vocab, LONG_PROMPT).astype(np.int32)
+    # the prompt in 1024-token pieces (batched prefill, 512-token chunks),
+    # reporting each: under --pmc every dispatch is serialized
+    for i in range(0, LONG_PROMPT - 1, 1024):
+        m.prefill(prompt[i:min(i + 1024, LONG_PROMPT - 1)])
+        mxhip.synchronize()
+        print(f"[workload_long] prefilled {min(i + 1024, LONG_PROMPT - 1)} tokens", file=sys.stderr, flush=True)
+    lg, _ = m.step(int(prompt[-1]))
+    m.set_token(int(np.argmax(lg)))
+    m.decode(LONG_STEPS - 1)
+    mxhip.synchronize()
+    print(f"[workload_long] decoded {LONG_STEPS} steps", file=sys.stderr, flush=True)
+    src = mxhip.DeviceBuffer(COPY_BYTES)
+    dst = mxhip.DeviceBuffer(COPY_BYTES)
+    mxhip.memset(src, 1)
+    mxhip.copy(dst, src, COPY_BYTES)
+    mxhip.synchronize()
+    m.close()
+    print(f"[workload_long] {LONG_PROMPT}-token prompt, {LONG_STEPS} decode steps, copy {COPY_BYTES} B",
+          file=sys.stderr, flush=True)
+
+
+def attn(fetch_dir: str, write_dir: str, stats_csv: str | None = None) -> None:
+    """HBM bytes per decode-attention dispatch of workload_long (the grouped
+    kernel and its merge kernel), calibrated by the copy as in `traffic`,
+    against the K/V rows the step reads: 2 L n_kv hd 2 bytes at L = pos + 1
+    (Qwen3-8B: n_kv 8, hd 128; 36 dispatches per step)."""
+    rows_f, rows_w = _counter_rows(fetch_dir), _counter_rows(write_dir)
+
+    def ordered(rows, counter, pick):
+        acc: dict[int, float] = {}
+        for r in rows:
+            if r.get("Counter_Name") == counter and pick(r["Kernel_Name"]):
+                acc[int(r["Dispatch_Id"])] = acc.get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
+        return sorted(acc.items())
+
+    grp = lambda n: "attention_group_kernel" in n
+    mrg = lambda n: "attention_merge_kernel" in n
+    cpy = lambda n: "copy" in n.lower()
+    af, aw = ordered(rows_f, "FETCH_SIZE", grp), ordered(rows_w, "WRITE_SIZE", grp)
+    mf, mw = ordered(rows_f, "FETCH_SIZE", mrg), ordered(rows_w, "WRITE_SIZE", mrg)
+    if not af or not aw:
+        raise SystemExit("no attention_group_kernel dispatch found")
+    cf = _big([v for k, v in ordered(rows_f, "FETCH_SIZE", cpy) if k > af[0][0]])
+    cw = _big([v for k, v in ordered(rows_w, "WRITE_SIZE", cpy) if k > aw[0][0]])
+    if not cf or not cw:
+        raise SystemExit("no calibration copy found")
+    kib = COPY_BYTES / 1024
+    f_cal, w_cal = kib / (sum(cf) / len(cf)), kib / (sum(cw) / len(cw))
+    n_kv, hd = 8, 128
+    steps = len(af) // N_LAYER
+    # the first step (the prompt's last token) is at pos LONG_PROMPT - 1
+    alg = [2 * (LONG_PROMPT + i) * n_kv * hd * 2 for i in range(steps)]
+    fb = [v * 1024 * f_cal for _, v in af]
+    wb = [v * 1024 * w_cal for _, v in aw]
+    a_avg = sum(alg[i // N_LAYER] for i in range(len(fb))) / len(fb)
+    print("| dispatch | K/V bytes read (algorithmic) | FETCH (scaled) B | WRITE (scaled) B | traffic / algorithmic |")
+    print("|---|---:|---:|---:|---:|")
+    print(f"| `attention_group_kernel<16, 4>`, {len(fb)} dispatches ({steps} steps x {N_LAYER} layers) | "
+          f"{a_avg:,.0f} | {sum(fb) / len(fb):,.0f} | {sum(wb) / len(wb):,.0f} | "
+          f"{(sum(fb) + sum(wb)) / len(fb) / a_avg:.3f} |")
+    if mf and mw:
+        print(f"| `attention_merge_kernel`, {len(mf)} dispatches | - | {sum(v for _, v in mf) / len(mf) * 1024 * f_cal:,.0f} "
+              f"| {sum(v for _, v in mw) / len(mw) * 1024 * w_cal:,.0f} | - |")
+    print()
+    print(f"Calibration: factors {f_cal:.4f} (fetch) and {w_cal:.4f} (write) from a {COPY_BYTES:,} B copy.")
+    if stats_csv:
+        with open(stats_csv, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if "attention_group_kernel" in r["Name"] or "attention_merge_kernel" in r["Name"]:
+                    us = float(r["AverageNs"]) / 1e3
+                    extra = ""
+                    if "attention_group_kernel" in r["Name"]:
+                        extra = f", {a_avg / (us * 1e-6) / 1e9:,.0f} GB/s of K/V, {a_avg / (us * 1e-6) / 8e12:.3f} of 8 TB/s"
+                    name = re.sub(r"\([^()]*\)$", "", r["Name"].replace("mxh::(anonymous namespace)::", "").replace("mxh::", "").replace("void ", ""))
+                    print(f"`{name}`: {r['Calls']} dispatches, average {us:.2f} us{extra}")
 
 
 def _counter_rows(d: str):
@@ -327,6 +424,10 @@ def main(argv: list[str]) -> int:
     cmd = argv[0]
     if cmd == "workload":
         workload(argv[1], int(argv[2]) if len(argv) > 2 else 4)
+    elif cmd == "workload_long":
+        workload_long(argv[1])
+    elif cmd == "attn":
+        attn(argv[1], argv[2], argv[3] if len(argv) > 3 else None)
     elif cmd == "traffic":
         traffic(argv[1], argv[2])
     elif cmd == "rdreq":

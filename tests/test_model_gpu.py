@@ -32,6 +32,9 @@ VARIANTS = {
     "q4k-m-q6k": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q6_K, embd_type=mxhip.F16, attn_v_type=mxhip.Q6_K,
                       ffn_down_type=mxhip.Q6_K, qk_norm=False, arch="llama", rope_theta=5e5),
     "f16": dict(wtype=mxhip.F16, out_type=mxhip.F16, embd_type=mxhip.F16, qk_norm=True),
+    # the Qwen3-8B attention shape: 4 q heads per kv head, head_dim 128
+    "q4k-g4-hd128": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True, n_head=8,
+                         n_head_kv=2, head_dim=128),
 }
 
 
@@ -77,7 +80,8 @@ def test_per_layer_activations_and_logits(mxh, tmp_path, name, flags):
 @pytest.mark.parametrize("name,n_ctx,warm", [("q4k-qknorm", 600, 300), ("q5_0-gqa8", 1100, 300),
                                              ("q8-tied", 1100, 300), ("f32-hd128", 4000, 520),
                                              ("q4k-qknorm", 8200, 4150), ("q5_0-gqa8", 4200, 4100),
-                                             ("f32-hd128", 4096, 600), ("q8-tied", 4500, 4480)])
+                                             ("f32-hd128", 4096, 600), ("q8-tied", 4500, 4480),
+                                             ("q4k-g4-hd128", 600, 300), ("q4k-g4-hd128", 4400, 4380)])
 def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
     """Contexts long enough for several attention splits per q head.
     Below 4096 positions of context the per-q-head kernel runs: the grid
@@ -92,8 +96,9 @@ def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
     per active split, the merge kernel before the o-projection): hd 64 with
     2 q heads per kv head at L about 4150 (65 of 128 splits), hd 32 with 8
     q heads per kv head at L about 4100 (65 of 256), hd 128 with one q head
-    per kv head at L about 600 (10 of 128, F32 rows), and splits of 35
-    positions near the end of a 4500-position context (all 128)."""
+    per kv head at L about 600 (10 of 128, F32 rows), splits of 35
+    positions near the end of a 4500-position context (all 128), and the
+    Qwen3-8B shape (4 q heads per kv head, hd 128) on both kernels."""
     p = build(tmp_path, name)
     gm = mxhip.Model(p, n_ctx)
     om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
