@@ -238,14 +238,18 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
     const int nch = (p1 - p0 + CH - 1) / CH;
     const size_t col = (size_t)g * HD + sub * 8;
 
+    // K and V through buffer descriptors over the rows [0, rows_end): rows
+    // past them read 0 without a branch, so every wait below is for exactly
+    // the loads it needs (predicated loads left the compiler waiting for all)
     uint4 kraw[DB][NP], vraw[DB][NP];
+    const __amdgpu_buffer_rsrc_t krs = buf_rsrc(a.kc, rows_end * kvd * 2);
+    const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(a.vc, rows_end * kvd * 2);
     auto load = [&](int b, int c) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             const int j = p0 + c * CH + i * PR + pr;
-            const bool in = j < rows_end;
-            kraw[b][i] = in ? *reinterpret_cast<const uint4*>(a.kc + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
-            vraw[b][i] = in ? *reinterpret_cast<const uint4*>(a.vc + (size_t)j * kvd + col) : make_uint4(0, 0, 0, 0);
+            kraw[b][i] = ld_buf16(krs, (j * kvd + (int)col) * 2);
+            vraw[b][i] = ld_buf16(vrs, (j * kvd + (int)col) * 2);
         }
     };
     // wave 0: q; in the last split wave 1: k, wave 2: v of the current
@@ -259,9 +263,10 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
     if (prep)
         hin = head_fetch(a.qkv + off, a.bias ? a.bias + off : nullptr,
                          wave == 0 ? a.q_norm : is_k ? a.k_norm : nullptr, cs, HD);
+    // unconditionally (chunks past the split read zeros and are not used), so
+    // the preparation below waits for its own inputs only
 #pragma unroll
-    for (int b = 0; b < DB; ++b)
-        if (wave + NW * b < nch) load(b, wave + NW * b);
+    for (int b = 0; b < DB; ++b) load(b, wave + NW * b);
     MXH_ATTN_STAMP(2);
 
     if (wave == 0) {

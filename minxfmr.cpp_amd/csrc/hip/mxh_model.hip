@@ -309,6 +309,9 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     if (!attention_supported(c.n_head, c.n_head_kv, c.head_dim))
         return fail(MXH_ERR_UNSUPPORTED, "unsupported head layout (head_dim 32/64/128, at most 8 q heads per kv head)");
     const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
+    // the decode attention addresses a layer's cache with 32-bit buffer offsets
+    if ((int64_t)n_ctx * kvd * 2 >= ((int64_t)1 << 31))
+        return fail(MXH_ERR_UNSUPPORTED, "context too long: one layer's K cache must stay below 2 GiB");
 
     // --- place every tensor in one HBM blob ---
     std::vector<Placement> place;
