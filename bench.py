@@ -191,10 +191,22 @@ def run_long_context(mxhip, path: Path, seed: int, flags: int = 0) -> dict:
     mxhip.synchronize()
     dt = time.perf_counter() - t0
     kv_bytes = 2 * m.cfg.n_layer * m.cfg.n_head_kv * m.cfg.head_dim * 2 * (n_prompt + n_dec // 2)
+    # the decode attention alone at the final position (every layer, as the
+    # step launches it: the grouped kernel and its merge at this context),
+    # timed with HIP events on the library stream
+    m.bench_attention(1)
+    a_ms, a_launch, a_bytes = m.bench_attention(5)
+    a_us = a_ms * 1e3 / a_launch
+    a_gbs = a_bytes / a_launch / (a_us * 1e-6) / 1e9
     m.close()
     out = {"prompt": n_prompt, "decode_tokens": n_dec, "prefill_tok_s": round(n_prompt / (pf_ms * 1e-3), 1),
            "decode_tok_s": round(n_dec / dt, 2),
-           "decode_hbm_gbs": round((m.cfg.step_read_bytes + kv_bytes) / (dt / n_dec) / 1e9, 1)}
+           "decode_hbm_gbs": round((m.cfg.step_read_bytes + kv_bytes) / (dt / n_dec) / 1e9, 1),
+           "attention_roofline": {"bound": "hbm", "achieved": round(a_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(a_gbs / HBM_PEAK_GBS, 4), "us_per_layer": round(a_us, 3),
+                                  "per_launch_bytes": int(a_bytes / a_launch),
+                                  "kernel": "decode attention at L = 8320 (grouped kernel + merge kernel), "
+                                            "algorithmic bytes = the K and V rows read"}}
     log(f"long context: {out}")
     return out
 

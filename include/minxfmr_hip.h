@@ -317,6 +317,14 @@ int mxh_model_set_token(mxh_model *m, int token);
  * reports device time, launch count and algorithmic bytes (weights + fp32 x
  * and y).  Benchmark support, no reference counterpart. */
 int mxh_model_bench_gemv(mxh_model *m, int type, int reps, float *ms, int64_t *launches, int64_t *bytes);
+/* Enqueue the decode attention of every layer (and, where the context runs
+ * the grouped kernel, its merge) at the model's current position `reps`
+ * times on the library stream, as the decode step launches it; reports
+ * device time, launch count (layers x reps) and algorithmic bytes (the K and
+ * V rows read, 2 pos n_kv head_dim 2 per layer).  It rewrites cache row pos
+ * (which the next step writes before any read) and the split partials.
+ * Benchmark support, no reference counterpart. */
+int mxh_model_bench_attention(mxh_model *m, int reps, float *ms, int64_t *launches, int64_t *bytes);
 void mxh_model_close(mxh_model *m);
 
 /* Seeded synthetic GGUF writer (weights N(0, 0.02) quantized per type, norms

@@ -142,6 +142,28 @@ int o_proj(mxh_model* m, const Layer& L, hipStream_t st) {
     return rc | gemv(L.o, m->att, m->x, m->x, m->form, st);
 }
 
+// The decode attention of layer L at the device position
+AttnArgs attn_args(const mxh_model* m, const Layer& L) {
+    const mxh_model_config& c = m->cfg;
+    AttnArgs aa{};
+    aa.qkv = m->qkv;
+    aa.bias = L.bias;
+    aa.q_norm = L.q_norm;
+    aa.k_norm = L.k_norm;
+    aa.rope_cs = m->rope_cs;
+    aa.pos = m->pos;
+    aa.kc = L.kc;
+    aa.vc = L.vc;
+    aa.part = m->part;
+    aa.nh = c.n_head;
+    aa.nkv = c.n_head_kv;
+    aa.hd = c.head_dim;
+    aa.neox = m->neox;
+    aa.eps = c.eps;
+    aa.scale = 1.0f / sqrtf((float)c.head_dim);
+    return aa;
+}
+
 // Enqueue one token step at the device position.  with_head: the final
 // norm, lm-head and argmax (writing tokens[pos+1]) and the position advance
 // are fused into the head GEMV; without: a prompt step.
@@ -162,23 +184,7 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
             if (L.k.p) rc |= gemv(L.k, m->x, m->qkv + qd, nullptr, m->form, st, L.attn_norm, c.eps);
             rc |= gemv(L.v, m->x, m->qkv + qd + kvd, nullptr, m->form, st, L.attn_norm, c.eps);
         }
-        AttnArgs aa{};
-        aa.qkv = m->qkv;
-        aa.bias = L.bias;
-        aa.q_norm = L.q_norm;
-        aa.k_norm = L.k_norm;
-        aa.rope_cs = m->rope_cs;
-        aa.pos = m->pos;
-        aa.kc = L.kc;
-        aa.vc = L.vc;
-        aa.part = m->part;
-        aa.nh = nh;
-        aa.nkv = nkv;
-        aa.hd = hd;
-        aa.neox = m->neox;
-        aa.eps = c.eps;
-        aa.scale = 1.0f / sqrtf((float)hd);
-        rc |= attention_run(aa, c.n_ctx, st);
+        rc |= attention_run(attn_args(m, L), c.n_ctx, st);
         rc |= o_proj(m, L, st);
         if (L.gu_fused) {
             rc |= gemv(L.gu, m->x, m->h, nullptr, m->form, st, L.ffn_norm, c.eps, GEMV_SILU);
@@ -979,6 +985,37 @@ int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* l
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return rc;
+}
+
+int mxh_model_bench_attention(mxh_model* m, int reps, float* ms, int64_t* launches, int64_t* bytes) {
+    if (!m || reps <= 0 || !ms) return set_error(MXH_ERR_ARG, "bench_attention: bad arguments");
+    if (m->host_pos < 1 || m->host_pos >= m->cfg.n_ctx)
+        return set_error(MXH_ERR_ARG, "bench_attention: position %d has no cached rows or no room", m->host_pos);
+    hipStream_t st = lib_stream();
+    const mxh_model_config& c = m->cfg;
+    const int splits = attention_splits(c.n_ctx, c.n_head, c.n_head_kv, c.head_dim);
+    const bool merge = splits > kAttnMaxSplits;  // the grouped kernel's partials go through the merge kernel
+    hipEvent_t e0, e1;
+    if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
+    (void)hipEventCreate(&e1);
+    int rc = check_hip(hipEventRecord(e0, st), "event");
+    for (int r = 0; r < reps && !rc; ++r)
+        for (const Layer& L : m->layers) {
+            rc = attention_run(attn_args(m, L), c.n_ctx, st);
+            if (!rc && merge) rc = attention_merge_launch(m->part, splits, c.n_head, c.head_dim, m->att, st);
+            if (rc) break;
+        }
+    if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
+    if (!rc) rc = check_hip(hipEventSynchronize(e1), "bench_attention");
+    if (!rc) rc = check_hip(hipEventElapsedTime(ms, e0, e1), "event");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc) return rc;
+    // the K and V rows read at L = pos + 1 (the current row comes from q|k|v)
+    const int64_t per = 2 * (int64_t)m->host_pos * c.n_head_kv * c.head_dim * 2;
+    if (launches) *launches = (int64_t)reps * c.n_layer;
+    if (bytes) *bytes = per * reps * c.n_layer;
+    return MXH_OK;
 }
 
 void mxh_model_close(mxh_model* m) { free_model(m); }

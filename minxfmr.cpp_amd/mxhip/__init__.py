@@ -106,6 +106,7 @@ def _load() -> C.CDLL:
         "mxh_model_decode": (ip, [vp, ip, vp, C.POINTER(C.c_float)]),
         "mxh_model_set_token": (ip, [vp, ip]),
         "mxh_model_bench_gemv": (ip, [vp, ip, ip, C.POINTER(C.c_float), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+        "mxh_model_bench_attention": (ip, [vp, ip, C.POINTER(C.c_float), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
         "mxh_write_synthetic_gguf": (ip, [C.c_char_p, C.POINTER(SynthArch), C.c_uint64, ip]),
     }
     for name, (res, args) in sig.items():
@@ -122,7 +123,7 @@ EXPORTED = (
     "mxh_release_resources mxh_host_matmul_rhs_t mxh_host_matmul_f32 mxh_host_matmul_q mxh_host_matvec_strided "
     "mxh_host_vec_dot_rows mxh_host_vec_dot_rows_ring mxh_host_vec_mul_rows_cols mxh_model_open "
     "mxh_model_config_get mxh_model_reset mxh_model_position mxh_model_step mxh_model_prefill mxh_model_set_sampling mxh_model_set_logit_edits mxh_sample mxh_model_generate mxh_model_close "
-    "mxh_write_synthetic_gguf mxh_model_decode mxh_model_set_token mxh_model_bench_gemv"
+    "mxh_write_synthetic_gguf mxh_model_decode mxh_model_set_token mxh_model_bench_gemv mxh_model_bench_attention"
 ).split()
 
 
@@ -340,6 +341,12 @@ class Model:
     def set_token(self, token: int) -> None:
         """Make `token` the id at the current position (the next decode input)."""
         check(lib.mxh_model_set_token(self.h, token), "set_token")
+
+    def bench_attention(self, reps: int = 1):
+        """(device ms, launches, algorithmic bytes) of every layer's decode attention at the current position."""
+        ms, n, b = C.c_float(), C.c_int64(), C.c_int64()
+        check(lib.mxh_model_bench_attention(self.h, reps, C.byref(ms), C.byref(n), C.byref(b)), "bench_attention")
+        return ms.value, n.value, b.value
 
     def bench_gemv(self, type_: int, reps: int = 1):
         """(device ms, launches, algorithmic bytes) of every `type_` GEMV of the model."""

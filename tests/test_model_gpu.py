@@ -120,6 +120,33 @@ def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
     gm.close()
 
 
+@pytest.mark.parametrize("n_ctx", [128, 4200])
+def test_bench_attention_leaves_decoding_unchanged(mxh, tmp_path, n_ctx):
+    """mxh_model_bench_attention reruns every layer's decode attention at the
+    current position (the per-q-head kernel at 128 positions of context, the
+    grouped kernel and its merge at 4200): its launch and byte counts follow
+    the position, and decoding afterwards gives the ids of an uninterrupted
+    run (the cache row it rewrites is written again by the next step)."""
+    p = build(tmp_path, "q4k-g4-hd128")
+    prompt = np.random.default_rng(21).integers(0, TINY["n_vocab"], 30).astype(np.int32)
+    a = mxhip.Model(p, n_ctx)
+    ids_a, _, _ = a.generate(prompt, 8)
+    rest_a, _ = a.decode(12)
+    b = mxhip.Model(p, n_ctx)
+    ids_b, _, _ = b.generate(prompt, 8)
+    pos = b.position
+    ms, n, nbytes = b.bench_attention(3)
+    cfg = b.cfg
+    assert n == 3 * cfg.n_layer
+    assert nbytes == 3 * cfg.n_layer * 2 * pos * cfg.n_head_kv * cfg.head_dim * 2
+    assert ms > 0
+    rest_b, _ = b.decode(12)
+    assert np.array_equal(ids_a, ids_b)
+    assert np.array_equal(rest_a, rest_b)
+    a.close()
+    b.close()
+
+
 @pytest.mark.parametrize("name", ["q4k-qknorm", "q4k-mixed-q5k"])
 def test_graph_generate_matches_eager_steps_and_oracle(mxh, tmp_path, name):
     p = build(tmp_path, name)
