@@ -17,6 +17,7 @@
 #include <exception>
 #include <new>
 #include <initializer_list>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -241,7 +242,26 @@ namespace {
 struct Placement {
     const GgufTensor* t;
     size_t off;
+    std::shared_ptr<std::vector<uint8_t>> conv;  // bytes to upload instead of t->data (a promoted copy)
 };
+
+// A Q4_K row as Q5_K: each 144-byte block (d, dmin, 12 scale bytes, 128
+// nibble bytes) becomes a 176-byte Q5_K block with the same header, a zero
+// high-bit plane and the same nibbles.  Both types decode a sub-block as
+// d sc q - dmin m with the same 6-bit scale/min unpacking, so every weight
+// keeps its value exactly.
+std::shared_ptr<std::vector<uint8_t>> q4k_as_q5k(const GgufTensor* t) {
+    const int64_t nb = t->rows() * (t->cols() / 256);
+    auto out = std::make_shared<std::vector<uint8_t>>((size_t)nb * 176, (uint8_t)0);
+    const uint8_t* src = static_cast<const uint8_t*>(t->data);
+    for (int64_t b = 0; b < nb; ++b) {
+        const uint8_t* in = src + (size_t)b * 144;
+        uint8_t* o = out->data() + (size_t)b * 176;
+        std::memcpy(o, in, 16);            // d, dmin, scales
+        std::memcpy(o + 48, in + 16, 128);  // qs after the 32 zero qh bytes
+    }
+    return out;
+}
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -325,19 +345,35 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     auto put = [&](const GgufTensor* t) -> size_t {
         off = align_up(off, 256);
         const size_t o = off;
-        place.push_back({t, o});
+        place.push_back({t, o, nullptr});
         off += t->nbytes;
         return o;
     };
-    // contiguous run of same-typed matrices sharing cols -> one fused matrix
-    auto put_run = [&](std::vector<const GgufTensor*> ts) -> size_t {
+    // contiguous run of same-typed matrices sharing cols -> one fused matrix;
+    // with `as_q5k`, Q4_K members are promoted to Q5_K (q4k_as_q5k)
+    auto put_run = [&](std::vector<const GgufTensor*> ts, bool as_q5k = false) -> size_t {
         off = align_up(off, 256);
         const size_t o = off;
         for (const GgufTensor* t : ts) {
-            place.push_back({t, off});
-            off += t->nbytes;
+            if (as_q5k && t->type == MXH_Q4_K) {
+                auto conv = q4k_as_q5k(t);
+                place.push_back({t, off, conv});
+                off += conv->size();
+            } else {
+                place.push_back({t, off, nullptr});
+                off += t->nbytes;
+            }
         }
         return o;
+    };
+    // a mix of Q4_K and Q5_K rows fuses as Q5_K
+    auto k45 = [](std::initializer_list<const GgufTensor*> ts) {
+        bool any5 = false;
+        for (const GgufTensor* t : ts) {
+            if (t->type != MXH_Q4_K && t->type != MXH_Q5_K) return false;
+            any5 |= t->type == MXH_Q5_K;
+        }
+        return any5;
     };
     auto need = [&](const std::string& n, int64_t rows, int64_t cols) -> const GgufTensor* {
         const GgufTensor* t = f.find(n);
@@ -361,6 +397,8 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         size_t qkv, q, k, v, o, gu, g, u, down, an, fn, qn, kn, bias;
         const GgufTensor *tq, *tk, *tv, *to, *tg, *tu, *td, *bq, *bk, *bv;
         bool fq, fqk, fgu;
+        int tqkv, tgu;  // storage types of the fused runs
+        int64_t promoted;  // bytes added by Q4_K -> Q5_K promotion
     };
     std::vector<LOff> lo((size_t)c.n_layer);
     for (int l = 0; l < c.n_layer; ++l) {
@@ -377,10 +415,16 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
             return fail(MXH_ERR_ARG, "layer " + std::to_string(l) + ": projection weight missing or misshaped");
         for (const GgufTensor* t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td})
             if (!gemv_type_ok(t->type)) return fail(MXH_ERR_UNSUPPORTED, t->name + ": unsupported type " + std::to_string(t->type));
-        L.fq = L.tq->type == L.tk->type && L.tk->type == L.tv->type;
+        L.promoted = 0;
+        const bool qkv45 = k45({L.tq, L.tk, L.tv});
+        L.fq = (L.tq->type == L.tk->type && L.tk->type == L.tv->type) || qkv45;
         L.fqk = !L.fq && L.tq->type == L.tk->type;  // q and k rows share one GEMV, v has its own type
+        L.tqkv = qkv45 ? MXH_Q5_K : L.tq->type;
         if (L.fq) {
-            L.qkv = put_run({L.tq, L.tk, L.tv});
+            L.qkv = put_run({L.tq, L.tk, L.tv}, qkv45);
+            if (qkv45)
+                for (const GgufTensor* t : {L.tq, L.tk, L.tv})
+                    if (t->type == MXH_Q4_K) L.promoted += (int64_t)t->nbytes / 144 * 32;
         } else {
             if (L.fqk) {
                 L.q = put_run({L.tq, L.tk});
@@ -391,9 +435,14 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
             L.v = put(L.tv);
         }
         L.o = put(L.to);
-        L.fgu = L.tg->type == L.tu->type;
+        const bool gu45 = k45({L.tg, L.tu});
+        L.fgu = L.tg->type == L.tu->type || gu45;
+        L.tgu = gu45 ? MXH_Q5_K : L.tg->type;
         if (L.fgu) {
-            L.gu = put_run({L.tg, L.tu});
+            L.gu = put_run({L.tg, L.tu}, gu45);
+            if (gu45)
+                for (const GgufTensor* t : {L.tg, L.tu})
+                    if (t->type == MXH_Q4_K) L.promoted += (int64_t)t->nbytes / 144 * 32;
         } else {
             L.g = put(L.tg);
             L.u = put(L.tu);
@@ -429,10 +478,13 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     c.weight_bytes = (int64_t)m->blob_bytes;
     if (int rc = dalloc(&m->blob, m->blob_bytes)) { free_model(m); return rc; }
     for (const Placement& p : place)
-        if (int rc = check_hip(hipMemcpy(m->blob + p.off, p.t->data, p.t->nbytes, hipMemcpyHostToDevice), "weight upload")) {
+        if (int rc = check_hip(hipMemcpy(m->blob + p.off, p.conv ? p.conv->data() : p.t->data,
+                                         p.conv ? p.conv->size() : p.t->nbytes, hipMemcpyHostToDevice),
+                               "weight upload")) {
             free_model(m);
             return rc;
         }
+    place.clear();  // the promoted host copies
 
     auto dw = [&](size_t o, int type, int64_t rows, int64_t cols) { return DevW{m->blob + o, type, rows, cols}; };
     auto fptr = [&](size_t o) -> const float* { return o == SIZE_MAX ? nullptr : (const float*)(m->blob + o); };
@@ -446,7 +498,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         const LOff& L = lo[(size_t)l];
         Layer& D = m->layers[(size_t)l];
         D.qkv_fused = L.fq;
-        if (L.fq) D.qkv = dw(L.qkv, L.tq->type, qd + 2 * kvd, c.n_embd);
+        if (L.fq) D.qkv = dw(L.qkv, L.tqkv, qd + 2 * kvd, c.n_embd);
         else {
             // with q and k fused, D.q covers both row ranges and D.k is empty
             D.q = dw(L.q, L.tq->type, L.fqk ? qd + kvd : qd, c.n_embd);
@@ -455,7 +507,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         }
         D.o = dw(L.o, L.to->type, c.n_embd, qd);
         D.gu_fused = L.fgu;
-        if (L.fgu) D.gu = dw(L.gu, L.tg->type, 2 * (int64_t)c.n_ff, c.n_embd);
+        if (L.fgu) D.gu = dw(L.gu, L.tgu, 2 * (int64_t)c.n_ff, c.n_embd);
         else {
             D.g = dw(L.g, L.tg->type, c.n_ff, c.n_embd);
             D.u = dw(L.u, L.tu->type, c.n_ff, c.n_embd);
@@ -467,6 +519,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         D.k_norm = fptr(L.kn);
         D.bias = fptr(L.bias);
         for (const GgufTensor* t : {L.tq, L.tk, L.tv, L.to, L.tg, L.tu, L.td}) step_bytes += (int64_t)t->nbytes;
+        step_bytes += L.promoted;
     }
     c.step_read_bytes = step_bytes;
     c.has_qk_norm = m->layers[0].q_norm != nullptr;
