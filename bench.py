@@ -86,7 +86,10 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int, p0: int, n_c
 
     import mxo
 
-    m = mxo.Model(path, n_ctx=n_ctx, threads=threads)
+    max_steps = 48
+    # the oracle's cache holds its own steps (the GPU run's context may end
+    # before p0 + max_steps with few timed steps)
+    m = mxo.Model(path, n_ctx=max(n_ctx, p0 + max_steps + 1), threads=threads)
     m.set_pos(p0)
     t0 = time.perf_counter()
     n = 0
@@ -96,7 +99,7 @@ def cpu_baseline(path: Path, prompt, budget_s: float, threads: int, p0: int, n_c
         tok = int(np.argmax(lg))
         n += 1
         el = time.perf_counter() - t0
-        if el > budget_s or n >= 48:
+        if el > budget_s or n >= max_steps:
             break
     m.close()
     return {"value": round(n / el, 4), "unit": "tok/s", "cores": threads, "kind": "port",
