@@ -928,6 +928,8 @@ int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen,
     (void)hipEventCreate(&e1);
     (void)hipEventCreate(&e2);
     int rc = check_hip(hipMemcpyAsync(m->tokens, prompt, sizeof(int) * n_prompt, hipMemcpyHostToDevice, st), "prompt");
+    // the chunk buffers are allocated once per model, before the timed window
+    if (!rc && n_prompt > 1 && batched_prefill_supported(m)) rc = ensure_prefill_buffers(m);
     if (!rc) rc = check_hip(hipEventRecord(e0, st), "event");
     // prompt positions 0 .. n_prompt-2 need no logits (batched on the
     // matrix cores, or token by token); the last prompt token runs with the
