@@ -11,6 +11,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
+#include <limits.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -1039,8 +1040,14 @@ static void layer_forward(mxo_model *m, int l, int pos)
     if (L->bv) for (int i = 0; i < kvd; ++i) m->v[i] += L->bv[i];
     if (L->q_norm) for (int h = 0; h < nh; ++h) mxo_rmsnorm(m->q + h * hd, L->q_norm, m->q + h * hd, (size_t)hd, eps);
     if (L->k_norm) for (int h = 0; h < nkv; ++h) mxo_rmsnorm(m->k + h * hd, L->k_norm, m->k + h * hd, (size_t)hd, eps);
-    mxo_rope(m->q, (size_t)nh, (size_t)hd, 0, (size_t)pos, m->hp.theta, neox);
-    mxo_rope(m->k, (size_t)nkv, (size_t)hd, 0, (size_t)pos, m->hp.theta, neox);
+    /* the cache is a ring of n_ctx rows (kv_cache.cpp:50-75): `cached` rows
+     * are held (cache->lengths, which stops growing at n_ctx), the oldest at
+     * row `head` once the ring is full; RoPE takes start_pos = cached
+     * (transformer.cpp:506), so positions past n_ctx all rotate by n_ctx */
+    const int cached = pos < m->n_ctx ? pos : m->n_ctx;
+    const int head = pos < m->n_ctx ? 0 : (pos - m->n_ctx) % m->n_ctx;
+    mxo_rope(m->q, (size_t)nh, (size_t)hd, 0, (size_t)cached, m->hp.theta, neox);
+    mxo_rope(m->k, (size_t)nkv, (size_t)hd, 0, (size_t)cached, m->hp.theta, neox);
 
     float *kc = m->kcache + (size_t)l * m->n_ctx * kvd;
     float *vc = m->vcache + (size_t)l * m->n_ctx * kvd;
@@ -1052,19 +1059,20 @@ static void layer_forward(mxo_model *m, int l, int pos)
         }
     }
 
-    /* attention (transformer.cpp:529-629): scores over pos cached rows plus
+    /* attention (transformer.cpp:529-629): scores over the cached rows,
+     * oldest first (row (head + j) % n_ctx, backend_vec_dot_rows_ring), plus
      * the current row, double-accumulated dots, x 1/sqrt(hd) in float,
      * softmax, then V: cached rows accumulate out += w*v in float, the
      * current row is a double dot (cpu_vec_mul_rows_cols) added last. */
     const int group = nh / nkv;
     const float scale = 1.0f / sqrtf((float)hd);
-    const int J = pos + 1;
+    const int J = cached + 1;
     for (int h = 0; h < nh; ++h) {
         int kvh = h / (group > 0 ? group : 1);
         if (kvh > nkv - 1) kvh = nkv - 1;
         const float *qh = m->q + h * hd;
         for (int j = 0; j < J; ++j) {
-            const float *kr = j < pos ? kc + (size_t)j * kvd + kvh * hd : m->k + kvh * hd;
+            const float *kr = j < cached ? kc + (size_t)((head + j) % m->n_ctx) * kvd + kvh * hd : m->k + kvh * hd;
             double acc = 0.0;
             for (int t = 0; t < hd; ++t) acc += (double)qh[t] * (double)kr[t];
             m->scores[j] = (float)acc;
@@ -1073,16 +1081,18 @@ static void layer_forward(mxo_model *m, int l, int pos)
         mxo_softmax(m->scores, (size_t)J);
         float *out = m->att + h * hd;
         for (int t = 0; t < hd; ++t) out[t] = 0.0f;
-        for (int j = 0; j < pos; ++j) {
+        for (int j = 0; j < cached; ++j) {
             const float w = m->scores[j];
-            const float *vr = vc + (size_t)j * kvd + kvh * hd;
+            const float *vr = vc + (size_t)((head + j) % m->n_ctx) * kvd + kvh * hd;
             for (int t = 0; t < hd; ++t) out[t] = fmaf(w, vr[t], out[t]);
         }
-        const float wc = m->scores[pos];
+        const float wc = m->scores[cached];
         for (int t = 0; t < hd; ++t) out[t] += (float)((double)wc * (double)m->v[kvh * hd + t]);
     }
-    memcpy(kc + (size_t)pos * kvd, m->k, sizeof(float) * (size_t)kvd);
-    memcpy(vc + (size_t)pos * kvd, m->v, sizeof(float) * (size_t)kvd);
+    /* kvcache_append: the next free row, or the oldest one once full */
+    const int row = pos < m->n_ctx ? pos : head;
+    memcpy(kc + (size_t)row * kvd, m->k, sizeof(float) * (size_t)kvd);
+    memcpy(vc + (size_t)row * kvd, m->v, sizeof(float) * (size_t)kvd);
 
     proj(m, &L->wo, m->att, m->o);
     for (int i = 0; i < d; ++i) m->x[i] += m->o[i];
@@ -1097,7 +1107,7 @@ static void layer_forward(mxo_model *m, int l, int pos)
 
 int mxo_model_step(mxo_model *m, int token, float *logits, float *hidden_trace)
 {
-    if (!m || token < 0 || (size_t)token >= m->embd.rows || m->pos >= m->n_ctx) return -1;
+    if (!m || token < 0 || (size_t)token >= m->embd.rows || m->pos == INT_MAX) return -1;
     const int d = m->hp.n_embd;
     /* token_embedding_row_into: dequantize row `token` (minxfmr.cpp:210-343) */
     if (m->embd.type == MXO_F32)

@@ -14,9 +14,10 @@
  *
  * Pins (tests/test_oracle_pins.py, tests/test_oracle_layer.py,
  * tests/test_oracle_qknorm.py): fp16 decode, Q4_K/Q8_0/Q5_0 dequant,
- * matmul_rhs_t, rmsnorm, rope, softmax and the layer stack are checked
- * against the reference's own KATs, vectors from the reference source
- * compiled under oracle/_ref, closed forms and brute force.  Where the
+ * matmul_rhs_t, rmsnorm, rope, softmax and the layer stack (also past a
+ * full cache, where the reference's KV ring overwrites the oldest row) are
+ * checked against the reference's own KATs, vectors from the reference
+ * source compiled under oracle/_ref, closed forms and brute force.  Where the
  * reference has no code:
  *   - mxo_dequant_q6k_block and the F16 decode: pinned against the
  *     reference's own GGUF loader (gguf_dequant_q6_k, gguf_read_f32_tensor)
@@ -120,7 +121,9 @@ mxo_model *mxo_model_open(const char *path, int n_ctx, int flags, int nthreads);
 void mxo_model_close(mxo_model *m);
 void mxo_model_info_get(const mxo_model *m, mxo_model_info *info);
 void mxo_model_reset(mxo_model *m);
-/* Run one token at the next cache position.  logits (n_vocab) may be NULL;
+/* Run one token at the next cache position; past n_ctx tokens the cache is
+ * the reference's ring (the oldest row is overwritten, RoPE stays at
+ * position n_ctx).  logits (n_vocab) may be NULL;
  * hidden_trace, when non-NULL, receives n_layer*n_embd floats (hidden state
  * after each layer) followed by n_embd floats of the final-normed hidden. */
 int mxo_model_step(mxo_model *m, int token, float *logits, float *hidden_trace);

@@ -151,3 +151,22 @@ def layer_trace():
 
 if __name__ == "__main__" and "--layers" in sys.argv:
     layer_trace()
+
+
+def ring_trace():
+    """The same stack with a cache of RING_SEQ_MAX rows run past its end."""
+    import tempfile
+    sys.path.insert(0, str(ROOT / "tests"))
+    import gguf_synth
+    from layer_trace import RING_SEQ_MAX, RING_TOKENS, TINY, ref_stack_trace
+    keep = {}
+    with tempfile.TemporaryDirectory() as td:
+        gguf_synth.build(Path(td) / "tiny.gguf", gguf_synth.Arch(**TINY), seed=123, keep=keep)
+    hidden = ref_stack_trace(keep, TINY, RING_TOKENS, seq_max=RING_SEQ_MAX)
+    np.savez_compressed(HERE / "ref_ring_trace.npz", hidden=hidden, tokens=np.array(RING_TOKENS),
+                        seq_max=np.array(RING_SEQ_MAX))
+    print("wrote", HERE / "ref_ring_trace.npz", hidden.shape)
+
+
+if __name__ == "__main__" and "--ring" in sys.argv:
+    ring_trace()

@@ -15,13 +15,18 @@ import mxo
 TINY = dict(name="qwen3", n_layer=2, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=300,
             qk_norm=False, tied=False, wtype=mxo.Q4_K, out_type=mxo.Q8_0, embd_type=mxo.Q8_0)
 TOKENS = [5, 17, 299, 0, 42, 42, 7]
+# a cache of RING_SEQ_MAX rows run past its end: the reference's ring
+# (kv_cache.cpp:50-75) overwrites the oldest row and RoPE positions stop at
+# seq_max (transformer.cpp:506)
+RING_SEQ_MAX = 5
+RING_TOKENS = [5, 17, 299, 0, 42, 42, 7, 3, 250, 11, 11, 64, 128, 9]
 
 
-def ref_stack_trace(keep: dict, arch: dict, tokens: list[int]) -> np.ndarray:
+def ref_stack_trace(keep: dict, arch: dict, tokens: list[int], seq_max: int = 64) -> np.ndarray:
     ref = mxo.load_ref()
     d, nl = arch["n_embd"], arch["n_layer"]
     kvd = arch["n_head_kv"] * arch["head_dim"]
-    cache = ref.ref_cache_new(nl, 64, kvd)
+    cache = ref.ref_cache_new(nl, seq_max, kvd)
     t_e, ne_e, emb = keep["token_embd.weight"]
     emb_rows = mxo.dequant(t_e, emb, arch["n_vocab"], d)
     roles = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
