@@ -245,7 +245,12 @@ enum {
                                      integer codes, activations as fp16 hi + lo) */
 };
 
-/* Load a GGUF file into HBM with room for n_ctx positions.
+/* Load a GGUF file into HBM with a KV cache of n_ctx rows (the reference's
+ * seq_max).  Past n_ctx tokens the cache is the reference's ring
+ * (src/cache/kv_cache.cpp:50-75): each step attends the last n_ctx cached
+ * tokens and itself, RoPE stays at position n_ctx (transformer.cpp:506), and
+ * the oldest row is overwritten.  The id history holds max(n_ctx + 1, 2^20)
+ * ids; prefill, decode and generate stop with an error before it is full.
  * Replaces minxfmr_open's load path (src/api/minxfmr.cpp:702-1415). */
 int mxh_model_open(const char *gguf_path, int n_ctx, int flags, mxh_model **out);
 int mxh_model_config_get(const mxh_model *m, mxh_model_config *cfg);
@@ -287,10 +292,12 @@ int mxh_sample(const float *logits, int n, int top_k, double temperature, double
                uint64_t draw, int *token);
 
 /* Feed n prompt tokens at the current position without producing logits:
- * batched on the matrix cores in chunks of up to 512 tokens (dequant-to-bf16
- * MFMA GEMMs, row-batched QK-norm/RoPE/KV append and causal attention),
- * unless the model was opened with MXH_MODEL_TOKEN_PREFILL.  Replaces the
- * reference's token-by-token prompt loop (src/api/minxfmr.cpp:1503-1548). */
+ * batched on the matrix cores in chunks of up to 512 tokens (exact-weight fp16
+ * MFMA GEMMs, row-batched QK-norm/RoPE/KV append and causal attention) while
+ * the cache has room for them, then token by token past a full cache, and
+ * token by token throughout when the model was opened with
+ * MXH_MODEL_TOKEN_PREFILL.  Replaces the reference's token-by-token prompt
+ * loop (src/api/minxfmr.cpp:1503-1548). */
 int mxh_model_prefill(mxh_model *m, const int *tokens, int n);
 int mxh_model_step(mxh_model *m, int token, float *logits, float *trace);
 /* Greedy generation from position 0: prefill n_prompt ids, then n_gen

@@ -78,13 +78,23 @@ struct AttnArgs {
     const float* bias;    // [bq | bk | bv] or null
     const float* q_norm;  // per-head rmsnorm weights or null
     const float* k_norm;
-    const double* rope_cs;  // [n_ctx][hd/2][cos, sin]
-    const int* pos;       // current position (device)
-    __half* kc;           // this layer's K cache [n_ctx][nkv*hd]
+    const double* rope_cs;  // [n_ctx + 1][hd/2][cos, sin]
+    const int* pos;       // current position (device): tokens run so far
+    __half* kc;           // this layer's K cache (see ring)
     __half* vc;
     float* part;          // split partials (attention_scratch_floats)
     int nh, nkv, hd, neox;
     float eps, scale;
+    // ring > 0: the cache is the reference's ring of `ring` rows
+    // (kv_cache.cpp:50-75) held as ring + 1 slots stored twice,
+    // [2 (ring + 1)][nkv*hd]: token p goes to slot p % (ring + 1), and from
+    // p = ring on also to that slot's copy ring + 1 rows on, so the rows a
+    // step attends are always contiguous (a window [o, o + ring] reads the
+    // second copy only of slots below o, all written after the ring filled).
+    // Past a full ring RoPE stays at position ring (transformer.cpp:506).
+    // ring == 0: the kernels without the ring's arithmetic, for steps below
+    // a full cache (the same cache rows: token p at row p).
+    int ring;
 };
 int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st);
 // the attention output [nh][hd] merged from `splits` partials (for

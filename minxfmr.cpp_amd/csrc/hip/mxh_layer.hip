@@ -195,7 +195,7 @@ __device__ __forceinline__ float fold_position_groups_max(float v) {
 // rounded through fp16 as every cached position and used from LDS; the
 // workgroup of the kv head's first q head appends them to the cache.  No
 // cache row written in this launch is read in it.
-template <int LPP, int DB>
+template <int LPP, int DB, bool RING>
 // pos, the caches and q|k|v, needed first, also come as leading scalars that
 // the command processor preloads into SGPRs (-amdgpu-kernarg-preload-count).
 __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half* pkc, __half* pvc, const float* pqkv,
@@ -217,7 +217,13 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
     const int s = blockIdx.y, SM = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane % LPP, pr = lane / LPP;
-    const int pos = *a.pos, L = pos + 1;
+    // the rows attended: positions 0 .. pos of the window that starts at
+    // cache row wrow (RING, past a full ring: the last `ring` tokens, oldest
+    // first, then the current one at pos = ring, also its RoPE position)
+    const int P = *a.pos;
+    const bool wrapped = RING && P >= a.ring;
+    const int pos = wrapped ? a.ring : P, L = pos + 1;
+    const int wrow = wrapped ? (P + 1) % (a.ring + 1) : 0;
     const int S = min(SM, (L + kAttnRunSplitPos - 1) / kAttnRunSplitPos);
     MXH_ATTN_STAMP(1);
     float* part_v = a.part;                              // [nh][SM][HD]
@@ -242,8 +248,8 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
     // past them read 0 without a branch, so every wait below is for exactly
     // the loads it needs (predicated loads left the compiler waiting for all)
     uint4 kraw[DB][NP], vraw[DB][NP];
-    const __amdgpu_buffer_rsrc_t krs = buf_rsrc(a.kc, rows_end * kvd * 2);
-    const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(a.vc, rows_end * kvd * 2);
+    const __amdgpu_buffer_rsrc_t krs = buf_rsrc(a.kc + (size_t)wrow * kvd, rows_end * kvd * 2);
+    const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(a.vc + (size_t)wrow * kvd, rows_end * kvd * 2);
     auto load = [&](int b, int c) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
@@ -278,16 +284,21 @@ __global__ __launch_bounds__(512) void attention_kernel(const int* ppos, __half*
             __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         }
         // rounded through fp16 like every cached position; appended once
-        // per kv head
+        // per kv head (past a full ring to both copies of the token's slot)
         const bool append = qh % group == 0;
-        __half* cache = (is_k ? a.kc : a.vc) + (size_t)pos * kvd + (size_t)g * HD;
+        const int prow = wrow + pos;
+        __half* cache = (is_k ? a.kc : a.vc) + (size_t)prow * kvd + (size_t)g * HD;
+        __half* twin = wrapped ? cache + (prow <= a.ring ? 1 : -1) * (ptrdiff_t)(a.ring + 1) * kvd : nullptr;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const int t = lane + 64 * r;
             if (t < HD) {
                 const __half hv = __float2half_rn(is_k ? kvt[t] : hin.v[r]);
                 kvh[is_k ? 0 : 1][t] = hv;
-                if (append) cache[t] = hv;
+                if (append) {
+                    cache[t] = hv;
+                    if (twin) twin[t] = hv;
+                }
             }
         }
     }
@@ -464,7 +475,7 @@ __device__ __forceinline__ void fold_pairs(float (&v)[N], float (&w)[N / 4]) {
 // split the wave whose blocks hold position pos prepares the current token's
 // k and v, rounds them through fp16, appends them to the cache and uses them
 // from LDS, as attention_kernel does.
-template <int LPP, int G>
+template <int LPP, int G, bool RING>
 __global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, __half* pkc, __half* pvc,
                                                               const float* pqkv, AttnArgs a) {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -489,7 +500,11 @@ __global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, _
     const int g = blockIdx.x, s = blockIdx.y, SM = gridDim.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane % LPP, pr = lane / LPP, l16 = lane & 15, quad = lane >> 4;
-    const int pos = *a.pos, L = pos + 1;
+    // the window of rows attended, as in attention_kernel
+    const int P = *a.pos;
+    const bool wrapped = RING && P >= a.ring;
+    const int pos = wrapped ? a.ring : P, L = pos + 1;
+    const int wrow = wrapped ? (P + 1) % (a.ring + 1) : 0;
     const int S = min(SM, (L + kAttnGroupRunPos - 1) / kAttnGroupRunPos);
     float* part_v = a.part;                            // [nh][SM][HD]
     float* part_ml = a.part + (size_t)a.nh * SM * HD;  // [nh][SM][2]
@@ -533,9 +548,12 @@ __global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, _
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         // rounded through fp16 like every cached position and appended (this
-        // workgroup is the only one of kv head g holding position pos)
-        __half* kdst = a.kc + (size_t)pos * kvd + (size_t)g * HD;
-        __half* vdst = a.vc + (size_t)pos * kvd + (size_t)g * HD;
+        // workgroup is the only one of kv head g holding position pos; past a
+        // full ring to both copies of the token's slot)
+        const int prow = wrow + pos;
+        const ptrdiff_t twin = wrapped ? (prow <= a.ring ? 1 : -1) * (ptrdiff_t)(a.ring + 1) * kvd : 0;
+        __half* kdst = a.kc + (size_t)prow * kvd + (size_t)g * HD;
+        __half* vdst = a.vc + (size_t)prow * kvd + (size_t)g * HD;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const int e = lane + 64 * r;
@@ -545,6 +563,10 @@ __global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, _
                 kvh[1][e] = vh;
                 kdst[e] = kh;
                 vdst[e] = vh;
+                if (twin) {
+                    kdst[e + twin] = kh;
+                    vdst[e + twin] = vh;
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -552,8 +574,8 @@ __global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, _
     }
     // K (matrix-core operand layout) and V (row layout) of block b into slot b % 2
     uint4 kraw[2][KS], vraw[2][RB];
-    const __amdgpu_buffer_rsrc_t krs = buf_rsrc(a.kc, rows_end * kvd * 2);
-    const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(a.vc, rows_end * kvd * 2);
+    const __amdgpu_buffer_rsrc_t krs = buf_rsrc(a.kc + (size_t)wrow * kvd, rows_end * kvd * 2);
+    const __amdgpu_buffer_rsrc_t vrs = buf_rsrc(a.vc + (size_t)wrow * kvd, rows_end * kvd * 2);
     auto issue = [&](int b) {
         const int b0 = p0 + (wave + NW * b) * 16;
 #pragma unroll
@@ -718,6 +740,8 @@ __global__ __launch_bounds__(512) void attention_group_kernel(const int* ppos, _
 // (z, h) is one wave for q head h, k head h - nh or v head h - nh - nkv of
 // token z.  q goes to q_out (fp32), k and v (rounded to fp16) to the cache at
 // position p0 + z (transformer.cpp:385-470 per token; QK-norm as head_prep).
+// Batched prompts stay below a full ring (AttnArgs::ring), whose rows need no
+// second copy.
 __global__ __launch_bounds__(64) void qkv_prep_rows_kernel(const float* __restrict__ qkv, int ldq,
                                                            const float* __restrict__ bias,
                                                            const float* __restrict__ q_norm,
@@ -885,33 +909,48 @@ bool attention_supported(int nh, int nkv, int hd) {
     return nkv > 0 && nh % nkv == 0 && nh / nkv <= kAttnMaxGroup && (hd == 32 || hd == 64 || hd == 128);
 }
 
-template <int LPP>
+template <int LPP, bool RING>
 static void attention_group_launch(const AttnArgs& a, dim3 grid, hipStream_t st) {
+#define MXH_GROUP_CASE(G) \
+    hipLaunchKernelGGL((attention_group_kernel<LPP, G, RING>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a)
     switch (a.nh / a.nkv) {
-    case 1: hipLaunchKernelGGL((attention_group_kernel<LPP, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    case 2: hipLaunchKernelGGL((attention_group_kernel<LPP, 2>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    case 4: hipLaunchKernelGGL((attention_group_kernel<LPP, 4>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    default: hipLaunchKernelGGL((attention_group_kernel<LPP, 8>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 1: MXH_GROUP_CASE(1); break;
+    case 2: MXH_GROUP_CASE(2); break;
+    case 4: MXH_GROUP_CASE(4); break;
+    default: MXH_GROUP_CASE(8); break;
     }
+#undef MXH_GROUP_CASE
 }
 
-int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
-    if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
+template <bool RING>
+static void attention_dispatch(const AttnArgs& a, int n_ctx, hipStream_t st) {
     if (attention_grouped(n_ctx, a.nh, a.nkv, a.hd)) {
         const dim3 grid(a.nkv, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
         switch (a.hd) {
-        case 32: attention_group_launch<4>(a, grid, st); break;
-        case 64: attention_group_launch<8>(a, grid, st); break;
-        default: attention_group_launch<16>(a, grid, st); break;
+        case 32: attention_group_launch<4, RING>(a, grid, st); break;
+        case 64: attention_group_launch<8, RING>(a, grid, st); break;
+        default: attention_group_launch<16, RING>(a, grid, st); break;
         }
-        return MXH_OK;
+        return;
     }
     const dim3 grid(a.nh, attention_splits(n_ctx, a.nh, a.nkv, a.hd));
+#define MXH_HEAD_CASE(LPP) \
+    hipLaunchKernelGGL((attention_kernel<LPP, 1, RING>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a)
     switch (a.hd) {
-    case 32: hipLaunchKernelGGL((attention_kernel<4, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    case 64: hipLaunchKernelGGL((attention_kernel<8, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
-    default: hipLaunchKernelGGL((attention_kernel<16, 1>), grid, dim3(512), 0, st, a.pos, a.kc, a.vc, a.qkv, a); break;
+    case 32: MXH_HEAD_CASE(4); break;
+    case 64: MXH_HEAD_CASE(8); break;
+    default: MXH_HEAD_CASE(16); break;
     }
+#undef MXH_HEAD_CASE
+}
+
+// ring > 0 selects the kernels that handle a full ring; a step below a full
+// cache runs the same on either (the host picks them only for steps at or
+// past n_ctx tokens, which keeps the others free of the ring's arithmetic)
+int attention_run(const AttnArgs& a, int n_ctx, hipStream_t st) {
+    if (!attention_supported(a.nh, a.nkv, a.hd)) return MXH_ERR_UNSUPPORTED;
+    if (a.ring > 0) attention_dispatch<true>(a, n_ctx, st);
+    else attention_dispatch<false>(a, n_ctx, st);
     return MXH_OK;
 }
 

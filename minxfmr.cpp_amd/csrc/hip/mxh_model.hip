@@ -65,12 +65,16 @@ struct mxh_model {
     int* red_idx = nullptr;
     int red_cap = 0;
     int* counters = nullptr;  // [0]: lm-head argmax
-    int* tokens = nullptr;  // [n_ctx + 1]: prompt then generated ids
+    int* tokens = nullptr;  // [token_cap]: prompt then generated ids
+    int token_cap = 0;      // ids the history holds (steps run while host_pos + 1 < token_cap)
     int* pos = nullptr;     // current position
     int host_pos = 0;
     bool trace_on = false;
     bool token_prefill = false;  // prompt token by token instead of batched
     hipGraphExec_t g_prefill = nullptr, g_decode = nullptr, g_sample = nullptr;
+    // the same steps at or past a full cache (the ring's kernels), captured
+    // on first use and dropped whenever the ones above change
+    hipGraphExec_t g_prefill_w = nullptr, g_decode_w = nullptr, g_sample_w = nullptr;
     // sampling instead of greedy argmax (mxh_model_set_sampling)
     bool sampling = false;
     int top_k = 1;
@@ -143,8 +147,9 @@ int o_proj(mxh_model* m, const Layer& L, hipStream_t st) {
     return rc | gemv(L.o, m->att, m->x, m->x, m->form, st);
 }
 
-// The decode attention of layer L at the device position
-AttnArgs attn_args(const mxh_model* m, const Layer& L) {
+// The decode attention of layer L at the device position (wrapped: a step
+// at or past n_ctx tokens, which runs the ring's kernels)
+AttnArgs attn_args(const mxh_model* m, const Layer& L, bool wrapped) {
     const mxh_model_config& c = m->cfg;
     AttnArgs aa{};
     aa.qkv = m->qkv;
@@ -162,13 +167,15 @@ AttnArgs attn_args(const mxh_model* m, const Layer& L) {
     aa.neox = m->neox;
     aa.eps = c.eps;
     aa.scale = 1.0f / sqrtf((float)c.head_dim);
+    aa.ring = wrapped ? c.n_ctx : 0;
     return aa;
 }
 
 // Enqueue one token step at the device position.  with_head: the final
 // norm, lm-head and argmax (writing tokens[pos+1]) and the position advance
-// are fused into the head GEMV; without: a prompt step.
-int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
+// are fused into the head GEMV; without: a prompt step.  wrapped: the step
+// is at or past n_ctx tokens (the ring's attention kernels).
+int enqueue_step(mxh_model* m, bool with_head, bool wrapped, hipStream_t st) {
     const mxh_model_config& c = m->cfg;
     const int d = c.n_embd, hd = c.head_dim, nh = c.n_head, nkv = c.n_head_kv;
     const int qd = nh * hd, kvd = nkv * hd;
@@ -185,7 +192,7 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
             if (L.k.p) rc |= gemv(L.k, m->x, m->qkv + qd, nullptr, m->form, st, L.attn_norm, c.eps);
             rc |= gemv(L.v, m->x, m->qkv + qd + kvd, nullptr, m->form, st, L.attn_norm, c.eps);
         }
-        rc |= attention_run(attn_args(m, L), c.n_ctx, st);
+        rc |= attention_run(attn_args(m, L, wrapped), c.n_ctx, st);
         rc |= o_proj(m, L, st);
         if (L.gu_fused) {
             rc |= gemv(L.gu, m->x, m->h, nullptr, m->form, st, L.ffn_norm, c.eps, GEMV_SILU);
@@ -222,17 +229,22 @@ int enqueue_step(mxh_model* m, bool with_head, hipStream_t st) {
     return rc ? set_error(MXH_ERR_HIP, "step enqueue failed") : MXH_OK;
 }
 
-int capture(mxh_model* m, bool with_head, hipGraphExec_t* out) {
+int capture(mxh_model* m, bool with_head, bool wrapped, hipGraphExec_t* out) {
     hipStream_t st = lib_stream();
     hipGraph_t g = nullptr;
     if (int rc = check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture")) return rc;
-    const int rc = enqueue_step(m, with_head, st);
+    const int rc = enqueue_step(m, with_head, wrapped, st);
     const hipError_t e = hipStreamEndCapture(st, &g);
     if (rc) return rc;
     if (int r2 = check_hip(e, "end capture")) return r2;
     const hipError_t ie = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     return check_hip(ie, "graph instantiate");
+}
+
+void drop_graph(hipGraphExec_t& g) {
+    if (g) (void)hipGraphExecDestroy(g);
+    g = nullptr;
 }
 
 }  // namespace
@@ -268,9 +280,8 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int free_model(mxh_model* m) {
     if (!m) return MXH_OK;
     (void)hipStreamSynchronize(lib_stream());
-    if (m->g_prefill) (void)hipGraphExecDestroy(m->g_prefill);
-    if (m->g_decode) (void)hipGraphExecDestroy(m->g_decode);
-    if (m->g_sample) (void)hipGraphExecDestroy(m->g_sample);
+    for (hipGraphExec_t* g : {&m->g_prefill, &m->g_decode, &m->g_sample, &m->g_prefill_w, &m->g_decode_w, &m->g_sample_w})
+        drop_graph(*g);
     void* bufs[] = {m->blob, m->out_copy, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
                     m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
                     m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part,
@@ -335,9 +346,10 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     if (!attention_supported(c.n_head, c.n_head_kv, c.head_dim))
         return fail(MXH_ERR_UNSUPPORTED, "unsupported head layout (head_dim 32/64/128, at most 8 q heads per kv head)");
     const int qd = c.n_head * c.head_dim, kvd = c.n_head_kv * c.head_dim;
-    // the decode attention addresses a layer's cache with 32-bit buffer offsets
-    if ((int64_t)n_ctx * kvd * 2 >= ((int64_t)1 << 31))
-        return fail(MXH_ERR_UNSUPPORTED, "context too long: one layer's K cache must stay below 2 GiB");
+    // the decode attention addresses the rows of a layer's cache it reads with
+    // 32-bit buffer offsets
+    if ((int64_t)(n_ctx + 1) * kvd * 2 >= ((int64_t)1 << 31))
+        return fail(MXH_ERR_UNSUPPORTED, "context too long: one layer's K cache window must stay below 2 GiB");
 
     // --- place every tensor in one HBM blob ---
     std::vector<Placement> place;
@@ -569,7 +581,9 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     }
 
     // --- caches, RoPE table, activations ---
-    const size_t kv_per_layer = (size_t)n_ctx * kvd;
+    // the K and V caches: the reference's ring of n_ctx rows as n_ctx + 1
+    // slots stored twice (AttnArgs::ring)
+    const size_t kv_per_layer = 2 * ((size_t)n_ctx + 1) * kvd;
     int rc = dalloc(&m->kv, 2 * kv_per_layer * (size_t)c.n_layer);
     for (int l = 0; l < c.n_layer && !rc; ++l) {
         m->layers[(size_t)l].kc = m->kv + (size_t)(2 * l) * kv_per_layer;
@@ -578,10 +592,11 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     const int half = c.head_dim / 2;
     if (!rc) {
         // cos/sin of pos * theta^(-2i/rot) in double, as rope.cpp:26-31 computes them
-        std::vector<double> cs((size_t)n_ctx * half * 2);
+        // (positions 0 .. n_ctx: past a full ring RoPE stays at n_ctx)
+        std::vector<double> cs(((size_t)n_ctx + 1) * half * 2);
         for (int i = 0; i < half; ++i) {
             const double inv_freq = 1.0 / std::pow((double)c.rope_theta, (2.0 * (double)i) / (double)c.head_dim);
-            for (int p = 0; p < n_ctx; ++p) {
+            for (int p = 0; p <= n_ctx; ++p) {
                 const double ang = (double)p * inv_freq;
                 cs[((size_t)p * half + i) * 2] = std::cos(ang);
                 cs[((size_t)p * half + i) * 2 + 1] = std::sin(ang);
@@ -603,7 +618,9 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
                                                                                        c.head_dim, n_ctx)),
                        "attention partials init");
     if (!rc) rc = dalloc(&m->trace, (size_t)(c.n_layer + 1) * c.n_embd);
-    if (!rc) rc = dalloc(&m->tokens, (size_t)n_ctx + 1);
+    // the id history outlives the ring: up to 2^20 ids (or n_ctx + 1)
+    m->token_cap = std::max(n_ctx + 1, 1 << 20);
+    if (!rc) rc = dalloc(&m->tokens, (size_t)m->token_cap);
     if (!rc) rc = dalloc(&m->pos, 1);
     // >= workgroups of the head GEMV: at most one per row group (>= 2 rows)
     // and never more than the resident grid
@@ -620,7 +637,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     if (!rc) rc = check_hip(hipMemset(m->ecnt, 0, sizeof(int) * (size_t)c.n_vocab), "edit counts init");
     if (!rc) rc = dalloc(&m->counters, (size_t)c.n_head_kv + 1);
     if (!rc) rc = check_hip(hipMemset(m->counters, 0, sizeof(int) * ((size_t)c.n_head_kv + 1)), "counter init");
-    if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * ((size_t)n_ctx + 1)), "token init");
+    if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * (size_t)m->token_cap), "token init");
     if (!rc) rc = check_hip(hipMemset(m->pos, 0, sizeof(int)), "position init");
     if (!rc) rc = check_hip(hipDeviceSynchronize(), "model init");
     if (rc) {
@@ -630,7 +647,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     m->token_prefill = (flags & MXH_MODEL_TOKEN_PREFILL) != 0;
     m->bf16_prefill = (flags & MXH_MODEL_BF16_PREFILL) != 0;
     if (!(flags & MXH_MODEL_NO_GRAPH)) {
-        if ((rc = capture(m, false, &m->g_prefill)) || (rc = capture(m, true, &m->g_decode))) {
+        if ((rc = capture(m, false, false, &m->g_prefill)) || (rc = capture(m, true, false, &m->g_decode))) {
             free_model(m);
             return rc;
         }
@@ -662,10 +679,20 @@ int mxh_model_position(const mxh_model* m) { return m ? m->host_pos : -1; }
 
 namespace {
 
-int run_step(mxh_model* m, bool with_head) {
+// One step at position pos (the device position when it runs)
+int run_step(mxh_model* m, bool with_head, int pos) {
     hipStream_t st = lib_stream();
+    const bool wrapped = pos >= m->cfg.n_ctx;
     hipGraphExec_t g = with_head ? (m->sampling ? m->g_sample : m->g_decode) : m->g_prefill;
-    if (m->trace_on || !g) return enqueue_step(m, with_head, st);
+    if (m->trace_on || !g) return enqueue_step(m, with_head, wrapped, st);
+    if (wrapped) {
+        hipGraphExec_t* w = with_head ? (m->sampling ? &m->g_sample_w : &m->g_decode_w) : &m->g_prefill_w;
+        if (!*w) {
+            if (int rc = check_hip(hipStreamSynchronize(st), "ring graph")) return rc;
+            if (int rc = capture(m, with_head, true, w)) return rc;
+        }
+        g = *w;
+    }
     return check_hip(hipGraphLaunch(g, st), "graph launch");
 }
 
@@ -674,12 +701,13 @@ int run_step(mxh_model* m, bool with_head) {
 int mxh_model_step(mxh_model* m, int token, float* logits, float* trace) {
     if (!m) return set_error(MXH_ERR_ARG, "step: null model");
     if (token < 0 || token >= m->embd.rows) return set_error(MXH_ERR_ARG, "step: token %d out of range", token);
-    if (m->host_pos >= m->cfg.n_ctx) return set_error(MXH_ERR_ARG, "step: context of %d positions is full", m->cfg.n_ctx);
+    if (m->host_pos + 1 >= m->token_cap)
+        return set_error(MXH_ERR_ARG, "step: the id history of %d tokens is full", m->token_cap);
     hipStream_t st = lib_stream();
     if (int rc = check_hip(hipMemcpyAsync(m->tokens + m->host_pos, &token, sizeof(int), hipMemcpyHostToDevice, st), "token"))
         return rc;
     m->trace_on = trace != nullptr;
-    int rc = run_step(m, true);
+    int rc = run_step(m, true, m->host_pos);
     m->trace_on = false;
     if (rc) return rc;
     m->host_pos++;
@@ -794,22 +822,31 @@ int enqueue_prefill_chunk(mxh_model* m, int p0, int rows, hipStream_t st) {
     return rc ? set_error(MXH_ERR_HIP, "prefill enqueue failed") : MXH_OK;
 }
 
-// tokens[host_pos .. host_pos + n) (already on the device) in chunks
-int run_prefill(mxh_model* m, int n) {
-    if (n <= 0) return MXH_OK;
-    if (int rc = ensure_prefill_buffers(m)) return rc;
-    hipStream_t st = lib_stream();
-    for (int done = 0; done < n;) {
-        const int rows = std::min(m->pf_rows, n - done);
-        if (int rc = enqueue_prefill_chunk(m, m->host_pos + done, rows, st)) return rc;
-        done += rows;
-    }
-    return MXH_OK;
-}
-
 bool batched_prefill_supported(const mxh_model* m) {
     const mxh_model_config& c = m->cfg;
     return !m->token_prefill && c.n_embd % 64 == 0 && c.n_ff % 64 == 0 && (c.n_head * c.head_dim) % 64 == 0;
+}
+
+// Prompt tokens tokens[p .. p + n) (already on the device) without logits,
+// the device position at p: in batched chunks while the cache has room for
+// them, token by token past a full cache (every step of the ring is its own:
+// RoPE and the rows attended depend on what the step before evicted), and
+// token by token throughout with MXH_MODEL_TOKEN_PREFILL.
+int run_prefill(mxh_model* m, int p, int n) {
+    if (n <= 0) return MXH_OK;
+    const int batched = batched_prefill_supported(m) ? std::max(0, std::min(n, m->cfg.n_ctx - p)) : 0;
+    if (batched > 0) {
+        if (int rc = ensure_prefill_buffers(m)) return rc;
+        hipStream_t st = lib_stream();
+        for (int done = 0; done < batched;) {
+            const int rows = std::min(m->pf_rows, batched - done);
+            if (int rc = enqueue_prefill_chunk(m, p + done, rows, st)) return rc;
+            done += rows;
+        }
+    }
+    for (int i = batched; i < n; ++i)
+        if (int rc = run_step(m, false, p + i)) return rc;
+    return MXH_OK;
 }
 
 }  // namespace
@@ -837,9 +874,9 @@ int mxh_model_set_sampling(mxh_model* m, int top_k, double temperature, double t
     m->top_k = top_k;
     m->sampling = true;
     if (recapture) {
-        if (m->g_sample) (void)hipGraphExecDestroy(m->g_sample);
-        m->g_sample = nullptr;
-        if (int rc = capture(m, true, &m->g_sample)) {
+        drop_graph(m->g_sample);
+        drop_graph(m->g_sample_w);
+        if (int rc = capture(m, true, false, &m->g_sample)) {
             m->sampling = false;
             return rc;
         }
@@ -878,17 +915,17 @@ int mxh_model_set_logit_edits(mxh_model* m, const int* suppress, int n_suppress,
     // its own mode: capture() records the current `sampling` choice)
     const bool sampling = m->sampling;
     int rc = MXH_OK;
+    drop_graph(m->g_decode_w);
+    drop_graph(m->g_sample_w);
     if (m->g_decode) {
-        (void)hipGraphExecDestroy(m->g_decode);
-        m->g_decode = nullptr;
+        drop_graph(m->g_decode);
         m->sampling = false;
-        rc = capture(m, true, &m->g_decode);
+        rc = capture(m, true, false, &m->g_decode);
     }
     if (!rc && m->g_sample) {
-        (void)hipGraphExecDestroy(m->g_sample);
-        m->g_sample = nullptr;
+        drop_graph(m->g_sample);
         m->sampling = true;
-        rc = capture(m, true, &m->g_sample);
+        rc = capture(m, true, false, &m->g_sample);
     }
     m->sampling = sampling;
     return rc;
@@ -896,19 +933,16 @@ int mxh_model_set_logit_edits(mxh_model* m, const int* suppress, int n_suppress,
 
 int mxh_model_prefill(mxh_model* m, const int* tokens, int n) {
     if (!m || (!tokens && n > 0) || n < 0) return set_error(MXH_ERR_ARG, "prefill: bad arguments");
-    if (m->host_pos + n > m->cfg.n_ctx)
-        return set_error(MXH_ERR_ARG, "prefill: position %d + %d exceeds the context of %d", m->host_pos, n, m->cfg.n_ctx);
+    if ((int64_t)m->host_pos + n >= m->token_cap)
+        return set_error(MXH_ERR_ARG, "prefill: position %d + %d exceeds the id history of %d", m->host_pos, n,
+                         m->token_cap);
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= m->embd.rows) return set_error(MXH_ERR_ARG, "prefill: id %d out of range", tokens[i]);
     if (n == 0) return MXH_OK;
     hipStream_t st = lib_stream();
     int rc = check_hip(hipMemcpyAsync(m->tokens + m->host_pos, tokens, sizeof(int) * n, hipMemcpyHostToDevice, st),
                        "prefill ids");
-    if (!rc) {
-        if (batched_prefill_supported(m)) rc = run_prefill(m, n);
-        else
-            for (int i = 0; i < n && !rc; ++i) rc = run_step(m, false);
-    }
+    if (!rc) rc = run_prefill(m, m->host_pos, n);
     if (!rc) rc = check_hip(hipStreamSynchronize(st), "prefill");
     if (!rc) m->host_pos += n;
     return rc;
@@ -917,8 +951,9 @@ int mxh_model_prefill(mxh_model* m, const int* tokens, int n) {
 int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen, int* out, float* prefill_ms,
                        float* decode_ms) {
     if (!m || !prompt || n_prompt <= 0 || n_gen <= 0 || !out) return set_error(MXH_ERR_ARG, "generate: bad arguments");
-    if (n_prompt + n_gen - 1 > m->cfg.n_ctx)
-        return set_error(MXH_ERR_ARG, "generate: %d + %d tokens exceed the context of %d", n_prompt, n_gen, m->cfg.n_ctx);
+    if ((int64_t)n_prompt + n_gen >= m->token_cap)
+        return set_error(MXH_ERR_ARG, "generate: %d + %d tokens exceed the id history of %d", n_prompt, n_gen,
+                         m->token_cap);
     for (int i = 0; i < n_prompt; ++i)
         if (prompt[i] < 0 || prompt[i] >= m->embd.rows) return set_error(MXH_ERR_ARG, "generate: prompt id %d out of range", prompt[i]);
     if (int rc = mxh_model_reset(m)) return rc;
@@ -934,11 +969,9 @@ int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen,
     // prompt positions 0 .. n_prompt-2 need no logits (batched on the
     // matrix cores, or token by token); the last prompt token runs with the
     // head and yields the first generated id (minxfmr.cpp:1860)
-    if (!rc && batched_prefill_supported(m)) rc = run_prefill(m, n_prompt - 1);
-    else
-        for (int i = 0; i < n_prompt - 1 && !rc; ++i) rc = run_step(m, false);
+    if (!rc) rc = run_prefill(m, 0, n_prompt - 1);
     if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
-    for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true);
+    for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true, n_prompt - 1 + i);
     if (!rc) rc = check_hip(hipEventRecord(e2, st), "event");
     if (!rc) rc = check_hip(hipMemcpyAsync(out, m->tokens + n_prompt, sizeof(int) * n_gen, hipMemcpyDeviceToHost, st), "ids");
     if (!rc) rc = check_hip(hipStreamSynchronize(st), "generate");
@@ -957,14 +990,15 @@ int mxh_model_generate(mxh_model* m, const int* prompt, int n_prompt, int n_gen,
 int mxh_model_decode(mxh_model* m, int n_gen, int* out, float* decode_ms) {
     if (!m || n_gen <= 0) return set_error(MXH_ERR_ARG, "decode: bad arguments");
     const int p0 = m->host_pos;
-    if (p0 + n_gen > m->cfg.n_ctx)
-        return set_error(MXH_ERR_ARG, "decode: position %d + %d exceeds the context of %d", p0, n_gen, m->cfg.n_ctx);
+    if ((int64_t)p0 + n_gen >= m->token_cap)
+        return set_error(MXH_ERR_ARG, "decode: position %d + %d exceeds the id history of %d", p0, n_gen,
+                         m->token_cap);
     hipStream_t st = lib_stream();
     hipEvent_t e0, e1;
     if (int rc = check_hip(hipEventCreate(&e0), "event")) return rc;
     (void)hipEventCreate(&e1);
     int rc = check_hip(hipEventRecord(e0, st), "event");
-    for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true);
+    for (int i = 0; i < n_gen && !rc; ++i) rc = run_step(m, true, p0 + i);
     if (!rc) rc = check_hip(hipEventRecord(e1, st), "event");
     if (!rc && out) rc = check_hip(hipMemcpyAsync(out, m->tokens + p0 + 1, sizeof(int) * n_gen, hipMemcpyDeviceToHost, st), "ids");
     if (!rc) rc = check_hip(hipStreamSynchronize(st), "decode");
@@ -980,8 +1014,8 @@ int mxh_model_decode(mxh_model* m, int n_gen, int* out, float* decode_ms) {
 int mxh_model_set_token(mxh_model* m, int token) {
     if (!m) return set_error(MXH_ERR_ARG, "set_token: null model");
     if (token < 0 || token >= m->embd.rows) return set_error(MXH_ERR_ARG, "set_token: token %d out of range", token);
-    // tokens[] holds n_ctx + 1 ids, so the current position indexes it even
-    // when the context is full
+    // the history holds token_cap ids and every step leaves host_pos below
+    // it, so the current position indexes it
     hipStream_t st = lib_stream();
     int rc = check_hip(hipMemcpyAsync(m->tokens + m->host_pos, &token, sizeof(int), hipMemcpyHostToDevice, st), "token");
     if (!rc) rc = check_hip(hipStreamSynchronize(st), "set_token");
@@ -1044,8 +1078,7 @@ int mxh_model_bench_gemv(mxh_model* m, int type, int reps, float* ms, int64_t* l
 
 int mxh_model_bench_attention(mxh_model* m, int reps, float* ms, int64_t* launches, int64_t* bytes) {
     if (!m || reps <= 0 || !ms) return set_error(MXH_ERR_ARG, "bench_attention: bad arguments");
-    if (m->host_pos < 1 || m->host_pos >= m->cfg.n_ctx)
-        return set_error(MXH_ERR_ARG, "bench_attention: position %d has no cached rows or no room", m->host_pos);
+    if (m->host_pos < 1) return set_error(MXH_ERR_ARG, "bench_attention: position %d has no cached rows", m->host_pos);
     hipStream_t st = lib_stream();
     const mxh_model_config& c = m->cfg;
     const int splits = attention_splits(c.n_ctx, c.n_head, c.n_head_kv, c.head_dim);
@@ -1056,7 +1089,7 @@ int mxh_model_bench_attention(mxh_model* m, int reps, float* ms, int64_t* launch
     int rc = check_hip(hipEventRecord(e0, st), "event");
     for (int r = 0; r < reps && !rc; ++r)
         for (const Layer& L : m->layers) {
-            rc = attention_run(attn_args(m, L), c.n_ctx, st);
+            rc = attention_run(attn_args(m, L, m->host_pos >= c.n_ctx), c.n_ctx, st);
             if (!rc && merge) rc = attention_merge_launch(m->part, splits, c.n_head, c.head_dim, m->att, st);
             if (rc) break;
         }
@@ -1066,8 +1099,9 @@ int mxh_model_bench_attention(mxh_model* m, int reps, float* ms, int64_t* launch
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     if (rc) return rc;
-    // the K and V rows read at L = pos + 1 (the current row comes from q|k|v)
-    const int64_t per = 2 * (int64_t)m->host_pos * c.n_head_kv * c.head_dim * 2;
+    // the K and V rows read: the cached ones (at most the ring's n_ctx; the
+    // current row comes from q|k|v)
+    const int64_t per = 2 * (int64_t)std::min(m->host_pos, c.n_ctx) * c.n_head_kv * c.head_dim * 2;
     if (launches) *launches = (int64_t)reps * c.n_layer;
     if (bytes) *bytes = per * reps * c.n_layer;
     return MXH_OK;

@@ -120,6 +120,66 @@ def test_multi_split_attention(mxh, tmp_path, name, n_ctx, warm):
     gm.close()
 
 
+@pytest.mark.parametrize("name,n_ctx,n_steps", [("q4k-qknorm", 24, 70), ("q5_0-gqa8", 40, 100),
+                                                ("q4k-g4-hd128", 300, 620), ("q4k-g4-hd128", 4096, 4125)])
+def test_ring_past_full_cache(mxh, tmp_path, name, n_ctx, n_steps):
+    """Past n_ctx tokens the cache is the reference's ring (kv_cache.cpp:50-75):
+    each step attends the last n_ctx tokens and itself with RoPE at position
+    n_ctx, and overwrites the oldest row.  Hidden states and logits against
+    the oracle's ring, before the cache fills, across the wrap and after more
+    than one full turn of the ring (two turns at 300), on the per-q-head
+    kernel (1, 2 and 8 q heads per kv head; 2 splits at 300) and the grouped
+    kernel (4096)."""
+    p = build(tmp_path, name)
+    gm = mxhip.Model(p, n_ctx)
+    om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
+    toks = np.random.default_rng(11).integers(0, TINY["n_vocab"], n_steps)
+    checks = set(range(3)) | set(range(n_ctx - 2, n_ctx + 4)) | set(range(n_steps - 4, n_steps))
+    worst = 0.0
+    for i, tok in enumerate(toks):
+        check = i in checks
+        lg, tr = gm.step(int(tok), trace=check, logits=check)
+        olg, otr = om.step(int(tok), trace=check)
+        if not check:
+            continue
+        ok, e1 = close_enough(tr, otr)
+        assert ok, f"position {i}: hidden trace error {e1}"
+        ok, e2 = close_enough(lg, olg)
+        assert ok, f"position {i}: logits error {e2}"
+        worst = max(worst, e1 / max(1.0, float(np.abs(otr).max())), e2)
+    assert worst < 1e-3, worst
+    gm.close()
+
+
+@pytest.mark.parametrize("name,n_ctx", [("q4k-qknorm", 24), ("q4k-g4-hd128", 4096)])
+def test_prompt_longer_than_cache(mxh, tmp_path, name, n_ctx):
+    """A prompt longer than the cache: batched chunks up to n_ctx, then token
+    steps on the ring.  The next step's logits match the oracle fed token by
+    token, and greedy decoding from there (HIP graph) gives the ids of the
+    step-by-step eager path."""
+    p = build(tmp_path, name)
+    n_prompt = n_ctx + min(n_ctx // 2, 40) + 5
+    prompt = np.random.default_rng(12).integers(0, TINY["n_vocab"], n_prompt).astype(np.int32)
+    gm = mxhip.Model(p, n_ctx)
+    om = mxo.Model(p, n_ctx, mxo.OPEN_KV_FP16)
+    gm.prefill(prompt[:-1])
+    assert gm.position == n_prompt - 1
+    for t in prompt[:-1]:
+        om.step(int(t), trace=False)
+    lg, _ = gm.step(int(prompt[-1]))
+    olg, _ = om.step(int(prompt[-1]), trace=False)
+    ok, err = close_enough(lg, olg)
+    assert ok and err < 1e-3, f"logits after the prompt: error {err}"
+    ids, _ = gm.decode(12)
+    gm.close()
+    em = mxhip.Model(p, n_ctx, mxhip.MODEL_NO_GRAPH | mxhip.MODEL_TOKEN_PREFILL)
+    em.prefill(prompt[:-1])
+    em.step(int(prompt[-1]))
+    eids, _ = em.decode(12)
+    em.close()
+    assert ids.tolist() == eids.tolist()
+
+
 @pytest.mark.parametrize("n_ctx", [128, 4200])
 def test_bench_attention_leaves_decoding_unchanged(mxh, tmp_path, n_ctx):
     """mxh_model_bench_attention reruns every layer's decode attention at the
@@ -295,10 +355,15 @@ def test_step_errors_are_reported(mxh, tmp_path):
         gm.step(TINY["n_vocab"])
     with pytest.raises(mxhip.MxhError, match="out of range"):
         gm.set_token(-1)
-    for t in range(4):
+    # past the 4-row cache the ring keeps going (test_ring_past_full_cache)
+    for t in range(6):
         gm.step(t, logits=False)
-    with pytest.raises(mxhip.MxhError, match="full"):
-        gm.step(0)
+    # the id history is bounded (2^20 ids): decode and generate refuse a run
+    # that would outgrow it before they start
+    with pytest.raises(mxhip.MxhError, match="id history"):
+        gm.decode(1 << 20)
+    with pytest.raises(mxhip.MxhError, match="id history"):
+        gm.generate(np.zeros(8, np.int32), 1 << 20)
     with pytest.raises(mxhip.MxhError):
         mxhip.Model(tmp_path / "missing.gguf", 16)
 
