@@ -187,53 +187,6 @@ __device__ __forceinline__ double wave_sum_d_all(double v) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
-// Stores and loads that are coherent across the per-XCD L2 caches by
-// themselves (agent-scope relaxed atomics, issued with sc1): data one
-// workgroup hands to another within a launch goes through these, so no
-// device-wide fence (an L2 writeback and invalidate) is needed.
-//
-// The hand-off protocol and the invariant it relies on.  A producer writes
-// its data with st_agent (sc1: written through its XCD's L2 to the device
-// coherence point), then waits for its own stores with s_waitcnt vmcnt(0)
-// (wait_mem: on this target a store leaves the count only when the write is
-// acknowledged), then publishes with a relaxed agent-scope atomic add on a
-// counter.  The consumer that sees the final count (the add's return value
-// in the attention merge) then reads the data with ld_agent / ld_agent4
-// (sc1 loads, which do not return a line its own XCD's L2 may hold stale).
-// The C++ memory model would want release / acquire orderings here; they
-// are not used because at agent scope they lower to an L2 writeback before
-// the atomic and an L2 invalidate after it, which cost microseconds with
-// hundreds of workgroups.  What makes the relaxed form correct is the
-// hardware order above: every data store is complete at the coherence
-// point before the counter update is issued, and the consumer's data loads
-// are issued after its atomic returned and bypass stale cached copies.
-// Code that hands data over must keep that shape: sc1 stores, a full vmcnt
-// wait, the atomic; the atomic's result, then sc1 loads.
-__device__ __forceinline__ void st_agent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_agent(int* p, int v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int add_agent(int* p, int v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// 16-byte load with the cache policy of ld_agent (sc1, as agent-scope atomic
-// loads carry it) through a buffer descriptor over [base, base + bytes): one
-// instruction where four ld_agent would be four.  Descriptor dword 3 is the
-// CDNA raw-buffer setting (32-bit data format); out-of-range offsets read 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t agent_rsrc(const void* base, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-__device__ __forceinline__ float4 ld_agent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* sc1 */));
-    return make_float4(v.x, v.y, v.z, v.w);
-}
-
 // 16-byte load through a buffer descriptor over [base, base + bytes) with
 // the default cache policy; offsets at or past `bytes` read 0 without a
 // branch, so a run of such loads keeps a fixed count for s_waitcnt
@@ -245,8 +198,5 @@ __device__ __forceinline__ uint4 ld_buf16(__amdgpu_buffer_rsrc_t r, int byte_off
     const u4 v = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-
-// wait until every memory operation this thread issued has completed
-__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 }  // namespace mxh

@@ -88,25 +88,6 @@ __device__ __forceinline__ uint4 ldg16(const uint8_t* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// dot of 4 x values with the 4 bytes of `b` as unsigned / signed integers
-__device__ __forceinline__ float dot4_ubyte(float4 x, uint32_t b, float acc) {
-    acc = fmaf(x.x, (float)(b & 0xffu), acc);
-    acc = fmaf(x.y, (float)((b >> 8) & 0xffu), acc);
-    acc = fmaf(x.z, (float)((b >> 16) & 0xffu), acc);
-    acc = fmaf(x.w, (float)(b >> 24), acc);
-    return acc;
-}
-
-__device__ __forceinline__ float dot4_sbyte(float4 x, uint32_t b, float acc) {
-    acc = fmaf(x.x, (float)(int)(int8_t)(b & 0xffu), acc);
-    acc = fmaf(x.y, (float)(int)(int8_t)((b >> 8) & 0xffu), acc);
-    acc = fmaf(x.z, (float)(int)(int8_t)((b >> 16) & 0xffu), acc);
-    acc = fmaf(x.w, (float)(int)(int8_t)(b >> 24), acc);
-    return acc;
-}
-
-__device__ __forceinline__ float sum4(float4 v) { return (v.x + v.y) + (v.z + v.w); }
-
 // Load a B-byte block (B = 4n+2) starting at the 2-aligned byte offset `o` of
 // a 4-aligned base into ceil(B/4) dwords without touching bytes outside
 // [o, o+B): n dwords from the aligned window plus two 16-bit tail loads.

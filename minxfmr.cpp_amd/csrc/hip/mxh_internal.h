@@ -29,12 +29,11 @@ struct GemvArgs {
     const float* norm_w;  // when set, x is rmsnorm(x) * norm_w
     float eps;
     int n, k, form;
-    // ARGMAX: per-workgroup winners, completion counter (zero between
-    // launches), token array and device position
+    // ARGMAX: per-workgroup winners (red_cap slots), token array and device
+    // position
     float* red_val;
     int* red_idx;
     int red_cap;
-    int* counter;
     int* tokens;
     int* pos;
     // ATTN: x is the decode attention's output, merged here from its split

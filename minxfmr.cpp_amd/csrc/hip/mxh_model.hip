@@ -64,7 +64,6 @@ struct mxh_model {
           *part = nullptr, *trace = nullptr, *red_val = nullptr;
     int* red_idx = nullptr;
     int red_cap = 0;
-    int* counters = nullptr;  // [0]: lm-head argmax
     int* tokens = nullptr;  // [token_cap]: prompt then generated ids
     int token_cap = 0;      // ids the history holds (steps run while host_pos + 1 < token_cap)
     int* pos = nullptr;     // current position
@@ -116,7 +115,6 @@ int gemv(const DevW& w, const float* x, float* y, const float* res, int form, hi
         a.red_val = m->red_val;
         a.red_idx = m->red_idx;
         a.red_cap = m->red_cap;
-        a.counter = m->counters;
         a.tokens = m->tokens;
         a.pos = m->pos;
     }
@@ -283,7 +281,7 @@ int free_model(mxh_model* m) {
     for (hipGraphExec_t* g : {&m->g_prefill, &m->g_decode, &m->g_sample, &m->g_prefill_w, &m->g_decode_w, &m->g_sample_w})
         drop_graph(*g);
     void* bufs[] = {m->blob, m->out_copy, m->kv, m->rope_cs, m->x, m->xn, m->qkv, m->att, m->gu, m->h, m->logits, m->part,
-                    m->trace, m->tokens, m->pos, m->red_val, m->red_idx, m->counters,
+                    m->trace, m->tokens, m->pos, m->red_val, m->red_idx,
                     m->pf_x, m->pf_qkv, m->pf_q, m->pf_att, m->pf_gu, m->pf_a, m->pf_a_lo, m->pf_part,
                     m->pf_h16, m->pf_l16, m->pf_sh, m->pf_sl, m->pf_rscale, m->sprm, m->scand, m->eprm, m->esup,
                     m->ecnt};
@@ -635,8 +633,6 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     if (!rc) rc = dalloc(&m->ecnt, (size_t)c.n_vocab);
     if (!rc) rc = check_hip(hipMemset(m->eprm, 0, sizeof(EditParams)), "edit params init");
     if (!rc) rc = check_hip(hipMemset(m->ecnt, 0, sizeof(int) * (size_t)c.n_vocab), "edit counts init");
-    if (!rc) rc = dalloc(&m->counters, (size_t)c.n_head_kv + 1);
-    if (!rc) rc = check_hip(hipMemset(m->counters, 0, sizeof(int) * ((size_t)c.n_head_kv + 1)), "counter init");
     if (!rc) rc = check_hip(hipMemset(m->tokens, 0, sizeof(int) * (size_t)m->token_cap), "token init");
     if (!rc) rc = check_hip(hipMemset(m->pos, 0, sizeof(int)), "position init");
     if (!rc) rc = check_hip(hipDeviceSynchronize(), "model init");
