@@ -180,13 +180,14 @@ def test_prompt_longer_than_cache(mxh, tmp_path, name, n_ctx):
     assert ids.tolist() == eids.tolist()
 
 
-@pytest.mark.parametrize("n_ctx", [128, 4200])
+@pytest.mark.parametrize("n_ctx", [128, 4200, 24])
 def test_bench_attention_leaves_decoding_unchanged(mxh, tmp_path, n_ctx):
     """mxh_model_bench_attention reruns every layer's decode attention at the
     current position (the per-q-head kernel at 128 positions of context, the
-    grouped kernel and its merge at 4200): its launch and byte counts follow
-    the position, and decoding afterwards gives the ids of an uninterrupted
-    run (the cache row it rewrites is written again by the next step)."""
+    grouped kernel and its merge at 4200, the ring's kernels past a 24-row
+    cache): its launch and byte counts follow the rows attended, and
+    decoding afterwards gives the ids of an uninterrupted run (the cache row
+    it rewrites is written again by the next step)."""
     p = build(tmp_path, "q4k-g4-hd128")
     prompt = np.random.default_rng(21).integers(0, TINY["n_vocab"], 30).astype(np.int32)
     a = mxhip.Model(p, n_ctx)
@@ -198,7 +199,7 @@ def test_bench_attention_leaves_decoding_unchanged(mxh, tmp_path, n_ctx):
     ms, n, nbytes = b.bench_attention(3)
     cfg = b.cfg
     assert n == 3 * cfg.n_layer
-    assert nbytes == 3 * cfg.n_layer * 2 * pos * cfg.n_head_kv * cfg.head_dim * 2
+    assert nbytes == 3 * cfg.n_layer * 2 * min(pos, n_ctx) * cfg.n_head_kv * cfg.head_dim * 2
     assert ms > 0
     rest_b, _ = b.decode(12)
     assert np.array_equal(ids_a, ids_b)

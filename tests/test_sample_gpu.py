@@ -74,8 +74,9 @@ def test_sample_rejects_bad_top_k(mxh):
 from test_model_gpu import TINY, build  # noqa: E402
 
 
-@pytest.mark.parametrize("name,k", [("q4k-qknorm", 8), ("q4k-mixed-q5k", 8), ("q4k-qknorm", 100)])
-def test_model_sampling_matches_oracle(mxh, tmp_path, name, k):
+@pytest.mark.parametrize("name,k,n_ctx", [("q4k-qknorm", 8, 128), ("q4k-mixed-q5k", 8, 128), ("q4k-qknorm", 100, 128),
+                                        ("q4k-qknorm", 8, 40)])
+def test_model_sampling_matches_oracle(mxh, tmp_path, name, k, n_ctx):
     """Seeded top-k=8, T=0.8 decoding (the BASELINE Llama-3 workload's
     sampler) of a tiny model, and top-k 100 (the radix-select form, inside
     the captured decode graph): a reset replays the same stream; graph
@@ -86,20 +87,22 @@ def test_model_sampling_matches_oracle(mxh, tmp_path, name, k):
     cumulative boundary often enough that the fp32-cache oracle's logits,
     about 1e-3 from the fp16-cache device's, can choose the neighbour, so
     there the end-to-end comparison is replaced by the one on the device's
-    logits."""
+    logits.  With a 40-row cache the 64 tokens run past it into the
+    reference's ring (the sampled graph's ring variant, captured on first
+    use), against the oracle's ring end to end."""
     p = build(tmp_path, name)
     prompt = np.random.default_rng(9).integers(0, TINY["n_vocab"], 16).astype(np.int32)
     t, seed, n_gen = 0.8, 4242, 48
-    gm = mxhip.Model(p, 128)
+    gm = mxhip.Model(p, n_ctx)
     gm.set_sampling(k, t, seed=seed)
     ids, _, _ = gm.generate(prompt, n_gen)
     ids2, _, _ = gm.generate(prompt, n_gen)
     assert np.array_equal(ids, ids2)
-    em = mxhip.Model(p, 128, mxhip.MODEL_NO_GRAPH)
+    em = mxhip.Model(p, n_ctx, mxhip.MODEL_NO_GRAPH)
     em.set_sampling(k, t, seed=seed)
     ids3, _, _ = em.generate(prompt, n_gen)
     assert np.array_equal(ids, ids3)
-    tm = mxhip.Model(p, 128)
+    tm = mxhip.Model(p, n_ctx)
     tm.prefill(prompt[:-1])
     lg, _ = tm.step(int(prompt[-1]))
     state = seed
@@ -109,7 +112,7 @@ def test_model_sampling_matches_oracle(mxh, tmp_path, name, k):
         lg, _ = tm.step(int(ids[i]))
     tm.close()
     if k <= 64:
-        om = mxo.Model(p, 128)
+        om = mxo.Model(p, n_ctx)
         lg = None
         for tok in prompt:
             lg, _ = om.step(int(tok))
@@ -122,7 +125,7 @@ def test_model_sampling_matches_oracle(mxh, tmp_path, name, k):
     # back to greedy
     gm.set_sampling(1, 0.0)
     g1, _, _ = gm.generate(prompt, 8)
-    g2, _, _ = mxhip.Model(p, 128).generate(prompt, 8)
+    g2, _, _ = mxhip.Model(p, n_ctx).generate(prompt, 8)
     assert np.array_equal(g1, g2)
     for m in (gm, em):
         m.close()
