@@ -35,7 +35,13 @@ enum {
     MXH_Q8_0 = 8,
     MXH_Q4_K = 12,
     MXH_Q5_K = 13,
-    MXH_Q6_K = 14
+    MXH_Q6_K = 14,
+    /* GGUF type 41, which the reference reads in gguf_dequant_q1_0
+     * (third_party/gguf/gguf_reader.cpp:1010-1098): its tensor size rule
+     * gives 1 byte per element for this type (:575-584), so it takes each
+     * byte as the weight's value, 0..255.  mxh_model_open widens such
+     * tensors to F32 when it loads them, as the reference does. */
+    MXH_Q1_0 = 41
 };
 
 /* flag of the tiled weight layout (mxh_tile_rows): MXH_TILED_FLAG | type */

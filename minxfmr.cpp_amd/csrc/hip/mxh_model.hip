@@ -14,6 +14,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <deque>
 #include <exception>
 #include <new>
 #include <initializer_list>
@@ -318,6 +319,27 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
     std::string err;
     if (!f.open(gguf_path, &err)) return set_error(MXH_ERR_ARG, "model_open: %s", err.c_str());
     if (int rc = mxh_init(0)) return rc;
+    // Tensors of GGUF type 41 are widened to F32 here, as the reference's
+    // loader does (gguf_dequant_q1_0: each byte is the value): `get` returns
+    // an F32 copy over the widened values, kept until the upload below.
+    std::deque<GgufTensor> widened;
+    std::vector<std::vector<uint8_t>> widened_data;
+    auto get = [&](const std::string& n) -> const GgufTensor* {
+        const GgufTensor* t = f.find(n);
+        if (!t || t->type != MXH_Q1_0 || !t->data) return t;
+        for (const GgufTensor& w : widened)
+            if (w.name == n) return &w;
+        std::vector<uint8_t> buf(t->nbytes * sizeof(float));
+        float* d = reinterpret_cast<float*>(buf.data());
+        for (size_t i = 0; i < t->nbytes; ++i) d[i] = (float)t->data[i];
+        GgufTensor w = *t;
+        w.type = MXH_F32;
+        w.data = buf.data();
+        w.nbytes = buf.size();
+        widened_data.push_back(std::move(buf));
+        widened.push_back(w);
+        return &widened.back();
+    };
 
     mxh_model* m = new mxh_model();
     mxh_model_config& c = m->cfg;
@@ -386,15 +408,15 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         return any5;
     };
     auto need = [&](const std::string& n, int64_t rows, int64_t cols) -> const GgufTensor* {
-        const GgufTensor* t = f.find(n);
+        const GgufTensor* t = get(n);
         if (!t || !t->data || t->rows() != rows || t->cols() != cols) return nullptr;
         return t;
     };
-    const GgufTensor* te = f.find("token_embd.weight");
+    const GgufTensor* te = get("token_embd.weight");
     if (!te || !te->data || te->cols() != c.n_embd) return fail(MXH_ERR_ARG, "token_embd.weight missing or misshaped");
-    const GgufTensor* to = f.find("output.weight");
+    const GgufTensor* to = get("output.weight");
     if (to && (!to->data || to->cols() != c.n_embd)) return fail(MXH_ERR_ARG, "output.weight misshaped");
-    const GgufTensor* tn = f.find("output_norm.weight");
+    const GgufTensor* tn = get("output_norm.weight");
     if (!tn || tn->type != MXH_F32 || tn->cols() != c.n_embd) return fail(MXH_ERR_ARG, "output_norm.weight missing");
     c.n_vocab = (int)(to ? to->rows() : te->rows());
     // every id the head can produce must index the embedding table
@@ -459,7 +481,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
         }
         L.down = put(L.td);
         auto norm = [&](const std::string& n, int64_t len, bool required, size_t* o) -> bool {
-            const GgufTensor* t = f.find(n);
+            const GgufTensor* t = get(n);
             if (!t) { *o = SIZE_MAX; return !required; }
             if (t->type != MXH_F32 || t->cols() != len) return false;
             *o = put(t);
@@ -473,9 +495,9 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
                    !norm(p + "attn_k_norm.weight", c.head_dim, false, &L.kn)) {
             return fail(MXH_ERR_ARG, "layer " + std::to_string(l) + ": QK-norm weights misshaped");
         }
-        L.bq = f.find(p + "attn_q.bias");
-        L.bk = f.find(p + "attn_k.bias");
-        L.bv = f.find(p + "attn_v.bias");
+        L.bq = get(p + "attn_q.bias");
+        L.bk = get(p + "attn_k.bias");
+        L.bv = get(p + "attn_v.bias");
         L.bias = SIZE_MAX;
         if (L.bq || L.bk || L.bv) {
             if (!L.bq || !L.bk || !L.bv || L.bq->type != MXH_F32 || L.bk->type != MXH_F32 || L.bv->type != MXH_F32 ||
@@ -495,6 +517,7 @@ static int model_open_impl(const char* gguf_path, int n_ctx, int flags, mxh_mode
             return rc;
         }
     place.clear();  // the promoted host copies
+    widened_data.clear();
 
     auto dw = [&](size_t o, int type, int64_t rows, int64_t cols) { return DevW{m->blob + o, type, rows, cols}; };
     auto fptr = [&](size_t o) -> const float* { return o == SIZE_MAX ? nullptr : (const float*)(m->blob + o); };

@@ -29,6 +29,7 @@ BlockInfo block_info(int type) {
     case 12: return {256, 144};
     case 13: return {256, 176};
     case 14: return {256, 210};
+    case 41: return {1, 1};  // one byte per element, the reference's reading
     }
     return {0, 0};
 }
@@ -215,6 +216,9 @@ size_t tensor_bytes(int type, int64_t rows, int64_t cols) {
 void quantize_row(int type, const float* x, int64_t n, uint8_t* out) {
     if (type == 0) {
         std::memcpy(out, x, (size_t)n * 4);
+    } else if (type == 41) {
+        // byte values, for synthetic files: small non-negative integers
+        for (int64_t i = 0; i < n; ++i) out[i] = (uint8_t)qround(x[i] * 64.f + 2.f, 0, 255);
     } else if (type == 1) {
         for (int64_t i = 0; i < n; ++i) put16(out + 2 * i, f2h(x[i]));
     } else if (type == 8) {

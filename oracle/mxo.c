@@ -216,7 +216,7 @@ void mxo_dequant_q6k_block(const uint8_t *blk, float *y)
 size_t mxo_block_elems(int type)
 {
     switch (type) {
-    case MXO_F32: case MXO_F16: return 1;
+    case MXO_F32: case MXO_F16: case MXO_Q1_0: return 1;
     case MXO_Q5_0: case MXO_Q8_0: return 32;
     case MXO_Q4_K: case MXO_Q5_K: case MXO_Q6_K: return 256;
     }
@@ -228,6 +228,7 @@ size_t mxo_block_bytes(int type)
     switch (type) {
     case MXO_F32: return 4;
     case MXO_F16: return 2;
+    case MXO_Q1_0: return 1;
     case MXO_Q5_0: return 22;
     case MXO_Q8_0: return 34;
     case MXO_Q4_K: return 144;
@@ -255,6 +256,7 @@ static void dequant_block(int type, const uint8_t *blk, float *y, int form)
     case MXO_Q6_K: mxo_dequant_q6k_block(blk, y); break;
     case MXO_F32: memcpy(y, blk, 4); break;
     case MXO_F16: y[0] = mxo_fp16_to_fp32(rd16(blk)); break;
+    case MXO_Q1_0: y[0] = (float)blk[0]; break; /* gguf_reader.cpp:1038 */
     }
 }
 
@@ -322,10 +324,11 @@ int mxo_matmul_rhs_t(int type, const float *A, size_t M, size_t K, const void *B
                      float *out, int form, int nthreads)
 {
     if (!A || !B || !out) return -1;
-    if (type == MXO_F16 || type == MXO_Q6_K) {
-        /* the reference converts F16 and Q6_K weights to F32 when it loads
-         * them (gguf_reader.cpp:759-785, :905-1008) and multiplies the F32
-         * values: each row is decoded, then summed as an F32 row below */
+    if (type == MXO_F16 || type == MXO_Q6_K || type == MXO_Q1_0) {
+        /* the reference converts F16, Q6_K and type-41 weights to F32 when
+         * it loads them (gguf_reader.cpp:759-785, :905-1008, :1010-1098) and
+         * multiplies the F32 values: each row is decoded, then summed as an
+         * F32 row below */
         const size_t rb = mxo_row_bytes(type, K);
         if (!rb) return -1;
 #pragma omp parallel for num_threads(nthreads > 0 ? nthreads : 1) schedule(static)

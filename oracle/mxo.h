@@ -54,6 +54,10 @@ enum {
     MXO_Q4_K = 12,
     MXO_Q5_K = 13,
     MXO_Q6_K = 14,
+    /* type 41, read by the reference's gguf_dequant_q1_0
+     * (gguf_reader.cpp:1010-1098) as one byte per element, the byte's value
+     * (its size rule gives 1 byte per element, :575-584) */
+    MXO_Q1_0 = 41,
 };
 
 /* Q4_K / Q5_K 6-bit scale unpacking forms.

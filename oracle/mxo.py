@@ -16,10 +16,11 @@ LIB = HERE / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libmxref.so"
 
 F32, F16, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 6, 8, 12, 13, 14
+Q1_0 = 41  # GGUF type 41: one byte per element, the byte's value (widened to F32 at load)
 FORM_REF, FORM_GGML = 0, 1
 OPEN_ROPE_NEOX, OPEN_KV_FP16, OPEN_GGML_FORM, OPEN_NO_QK_NORM = 1, 2, 4, 8
 BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
-         Q6_K: (256, 210)}
+         Q6_K: (256, 210), Q1_0: (1, 1)}
 
 
 def _p(a: np.ndarray) -> int:
@@ -113,6 +114,8 @@ def quantize(t: int, x: np.ndarray) -> np.ndarray:
         return x.view(np.uint8).reshape(-1).copy()
     if t == F16:
         return x.astype(np.float16).view(np.uint8).reshape(-1).copy()
+    if t == Q1_0:  # the synthetic writer's bytes: small non-negative integers
+        return np.clip(np.rint(x * np.float32(64) + np.float32(2)), 0, 255).astype(np.uint8).reshape(-1)
     n = x.size
     out = np.empty(n // BLOCK[t][0] * BLOCK[t][1], np.uint8)
     getattr(lib, _QUANT[t])(_p(x), n, _p(out))

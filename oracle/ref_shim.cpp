@@ -127,7 +127,8 @@ int ref_layer_forward(const float* in, float* out, size_t seq, size_t d, void* c
 }
 
 // The reference's load-time conversion of a GGUF tensor to F32
-// (gguf_reader.cpp:759-785 for F32 / F16, :905-1008 for Q6_K) over `nbytes`
+// (gguf_reader.cpp:759-785 for F32 / F16, :905-1008 for Q6_K, :1010-1098 for
+// type 41) over `nbytes`
 // of tensor data held in memory; out receives rows x cols floats.  -1 when
 // the reference declines the tensor.
 int ref_gguf_to_f32(int ggml_type, const void* data, size_t nbytes, uint32_t rows, uint32_t cols, float* out) {
@@ -140,7 +141,9 @@ int ref_gguf_to_f32(int ggml_type, const void* data, size_t nbytes, uint32_t row
     info.cols = cols;
     info.ggml_type = (uint32_t)ggml_type;
     Tensor* t = nullptr;
-    const bool ok = ggml_type == 14 ? gguf_dequant_q6_k(f, info, t) : gguf_read_f32_tensor(f, info, t);
+    const bool ok = ggml_type == 14   ? gguf_dequant_q6_k(f, info, t)
+                    : ggml_type == 41 ? gguf_dequant_q1_0(f, info, t)
+                                      : gguf_read_f32_tensor(f, info, t);
     if (!ok || !t) return -1;
     std::memcpy(out, t->data, sizeof(float) * (size_t)rows * cols);
     tensor_free(t);

@@ -35,6 +35,10 @@ VARIANTS = {
     # the Qwen3-8B attention shape: 4 q heads per kv head, head_dim 128
     "q4k-g4-hd128": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True, n_head=8,
                          n_head_kv=2, head_dim=128),
+    # GGUF type 41 (one byte per element, the byte's value) for attn_v and
+    # ffn_down, widened to F32 rows when the model opens
+    "q4k-byte41": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True,
+                       attn_v_type=mxhip.Q1_0, ffn_down_type=mxhip.Q1_0),
 }
 
 

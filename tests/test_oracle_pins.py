@@ -235,6 +235,37 @@ def test_q6k_and_f16_decode_vs_reference_loader():
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_type41_is_the_byte_value():
+    """GGUF type 41 holds one byte per element (the reference's size rule,
+    gguf_reader.cpp:575-584, gives it rows * cols bytes) and its reader
+    takes each byte as the weight, 0..255 (:1023-1041); the oracle's decode
+    is that closed form for every byte value, and its matmul over such rows
+    equals the matmul over the widened F32 rows."""
+    b = np.arange(256, dtype=np.uint8)
+    assert np.array_equal(mxo.dequant(mxo.Q1_0, b, 1, 256)[0], np.arange(256, dtype=np.float32))
+    rng = np.random.default_rng(41)
+    raw = rng.integers(0, 256, 7 * 96, dtype=np.uint8)
+    a = rng.standard_normal((3, 96)).astype(np.float32)
+    wide = raw.astype(np.float32).reshape(7, 96)
+    assert same_bits(mxo.matmul_rhs_t(mxo.Q1_0, a, raw, 7), mxo.matmul_rhs_t(mxo.F32, a, wide, 7))
+    # and the F32 rows' float fma chain is the product to fp32 rounding
+    assert np.allclose(mxo.matmul_rhs_t(mxo.Q1_0, a, raw, 7), a.astype(np.float64) @ wide.T.astype(np.float64),
+                       rtol=1e-6, atol=1e-4)
+
+
+@pytest.mark.skipif(REF is None, reason="oracle/_ref not built (reference tree absent)")
+def test_type41_decode_vs_reference_loader():
+    """The reference's own type-41 reader (gguf_reader.cpp:1010-1098),
+    compiled under oracle/_ref, gives the same bits as the oracle for every
+    byte value, on rows of several lengths."""
+    rng = np.random.default_rng(4141)
+    for rows, cols in ((1, 256), (5, 300), (16, 4096)):
+        raw = rng.integers(0, 256, rows * cols, dtype=np.uint8)
+        want = np.empty((rows, cols), np.float32)
+        assert REF.ref_gguf_to_f32(41, raw.ctypes.data, raw.size, rows, cols, want.ctypes.data) == 0
+        assert same_bits(mxo.dequant(mxo.Q1_0, raw, rows, cols), want)
+
+
 @pytest.mark.parametrize("t,tol", [(mxo.Q8_0, 0.008), (mxo.Q4_K, 0.12), (mxo.Q5_K, 0.06), (mxo.Q5_0, 0.06),
                                    (mxo.Q6_K, 0.03)])
 def test_quantizer_round_trip(t, tol):

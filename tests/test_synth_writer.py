@@ -77,3 +77,28 @@ def test_q4_k_m_mix_opens_in_the_oracle(tmp_path):
     lg, tr = m.step(1, trace=True)
     assert np.all(np.isfinite(lg)) and np.all(np.isfinite(tr))
     m.close()
+
+
+def test_type41_tensors(tmp_path):
+    """GGUF type 41 (one byte per element, the byte's value) for attn_v and
+    ffn_down: the file holds rows * cols bytes for them, the writer's bytes
+    are round(64 x + 2) of its N(0, 0.02) draws, and the oracle opens and
+    steps the model."""
+    import struct
+    p = _write(tmp_path / "t41.gguf", 2, wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0,
+               attn_v_type=mxhip.Q1_0, ffn_down_type=mxhip.Q1_0, n_layer=1)
+    raw = p.read_bytes()
+    name = b"blk.0.ffn_down.weight"
+    at = raw.index(name) + len(name)
+    n_dims = struct.unpack_from("<I", raw, at)[0]
+    ne = struct.unpack_from("<" + "Q" * n_dims, raw, at + 4)
+    ttype, off = struct.unpack_from("<IQ", raw, at + 4 + 8 * n_dims)
+    assert ttype == 41 and ne == (512, 256)
+    data0 = (at + 4 + 8 * n_dims + 12 + 31) // 32 * 32
+    w = np.frombuffer(raw, np.uint8, 256 * 512, data0 + off).astype(np.float64)
+    assert abs(w.mean() - 2.0) < 0.05 and abs(w.std() - 1.28) < 0.08
+    m = mxo.Model(p, 4)
+    assert m.info.type_wffn_down == mxo.Q1_0
+    lg, tr = m.step(5, trace=True)
+    assert np.all(np.isfinite(lg)) and np.all(np.isfinite(tr))
+    m.close()
