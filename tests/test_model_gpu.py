@@ -276,6 +276,49 @@ def test_q4_k_m_tiled_q6k_vs_oracle(mxh, tmp_path):
     om.close()
 
 
+@pytest.mark.parametrize("flags", [0, mxhip.MODEL_GGML_FORM], ids=["ref-form", "ggml-form"])
+def test_qwen3_8b_widths_vs_oracle(mxh, tmp_path, flags):
+    """Hidden size 4096, FFN 12288 and 32 / 8 heads of 128, the Qwen3-8B
+    widths, at two layers: every Q4_K projection runs the form it runs in
+    the 8B model (q|k|v twelve waves in one step with the fused norm, o
+    eight waves merging the attention splits, gate|up twelve waves in four
+    SwiGLU steps, down eight waves in three steps of K = 12288).  Per-layer
+    hidden states and logits within the bar (and 1e-3) of the oracle over 8
+    token steps, in both scale forms, then 16 greedy ids from a prompt equal
+    to the oracle's."""
+    V = 1000
+    p = build(tmp_path, "q4k-qknorm", n_layer=2, n_embd=4096, n_head=32, n_head_kv=8, head_dim=128, n_ff=12288,
+              n_vocab=V)
+    gm = mxhip.Model(p, 128, flags)
+    oflags = mxo.OPEN_KV_FP16 | (mxo.OPEN_GGML_FORM if flags & mxhip.MODEL_GGML_FORM else 0)
+    om = mxo.Model(p, 128, oflags, threads=16)
+    rng = np.random.default_rng(29)
+    worst = 0.0
+    for step in range(8):
+        tok = int(rng.integers(0, V))
+        lg, tr = gm.step(tok, trace=True)
+        olg, otr = om.step(tok, trace=True)
+        ok, e1 = close_enough(tr, otr)
+        assert ok, f"step {step}: hidden trace error {e1}"
+        ok, e2 = close_enough(lg, olg)
+        assert ok, f"step {step}: logits error {e2}"
+        worst = max(worst, e1 / max(1.0, float(np.abs(otr).max())), e2)
+    assert worst < 1e-3, worst
+    prompt = rng.integers(0, V, 12).astype(np.int32)
+    ids, _, _ = gm.generate(prompt, 16)
+    gm.close()
+    om.reset()
+    lg = None
+    for t in prompt:
+        lg, _ = om.step(int(t))
+    for i in range(16):
+        top = np.sort(lg)[-2:]
+        want = int(np.argmax(lg))
+        assert int(ids[i]) == want, f"step {i}: id {ids[i]} != oracle {want} (top-2 margin {top[1] - top[0]:.3g})"
+        lg, _ = om.step(want)
+    om.close()
+
+
 SWAP_EDITS = dict(suppress=[7, 11], repeat_last_n=24, repeat_penalty=1.3, frequency_penalty=0.4, presence_penalty=2.0)
 
 
