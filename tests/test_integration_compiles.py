@@ -1,11 +1,12 @@
-"""INTEGRATION.md's changes to the reference compile in the reference.
+"""The integration guide's changes to the reference compile in the reference.
 
-Every change INTEGRATION.md asks a maintainer to make to a reference file is
-written there as a hunk: a ```cpp block whose first line is
+Every change the guide (the repository's integration document, read from the
+path in DOC) asks a maintainer to make to a reference file is written there as
+a hunk: a ```cpp block whose first line is
 `// >>> <file>:<line> <before|after> | <fragment of that line>`.  This test
 applies all of them to a scratch copy of the reference's sources (line
 numbers are those of the unmodified files), puts the wrapper header where
-INTEGRATION.md puts it (src/backend/hip/hip_backend.h), and compiles the
+the guide puts it (src/backend/hip/hip_backend.h), and compiles the
 patched src/backend/backend_runtime.cpp and src/api/minxfmr.cpp with
 `g++ -fsyntax-only`: with MINXFMR_ENABLE_HIP (the HIP build) and without it
 (the reference as it was).  Warnings on a hunk's own lines fail the test.

@@ -325,7 +325,8 @@ SWAP_EDITS = dict(suppress=[7, 11], repeat_last_n=24, repeat_penalty=1.3, freque
 @pytest.mark.parametrize("host_steps", [1, 2], ids=["handover-at-swap", "handover-after-host-step"])
 @pytest.mark.parametrize("sampled", [False, True], ids=["greedy", "topk8"])
 def test_first_token_swap_then_device(mxh, tmp_path, sampled, host_steps):
-    """The coarse-step protocol of INTEGRATION.md against the oracle.
+    """The coarse-step protocol (the reference's first step on the host, then
+    the device from the host's id on) against the oracle.
 
     Host phase (device edits off, greedy head): the device returns the head's
     raw logits; the host applies the reference's edits (minxfmr.cpp:2047-2089)
