@@ -39,6 +39,9 @@ VARIANTS = {
     # ffn_down, widened to F32 rows when the model opens
     "q4k-byte41": dict(wtype=mxhip.Q4_K, out_type=mxhip.Q8_0, embd_type=mxhip.Q8_0, qk_norm=True,
                        attn_v_type=mxhip.Q1_0, ffn_down_type=mxhip.Q1_0),
+    # a type-41 token embedding, tied: the embedding rows and the lm-head
+    # are the widened F32 rows
+    "q8-tied-byte41": dict(wtype=mxhip.Q8_0, out_type=mxhip.Q8_0, embd_type=mxhip.Q1_0, qk_norm=True, tied=True),
 }
 
 
