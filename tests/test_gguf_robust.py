@@ -43,6 +43,8 @@ def open_err(path):
     ("element count overflow", dict(ne=(32, 1 << 40, 1 << 40)), "too many elements"),
     ("rows not whole blocks", dict(ne=(48, 4), ttype=8), "whole number of blocks"),
     ("truncated directory", dict(truncate=40), "truncated"),
+    # type 41: one byte per element, so 32 x 32 needs 1024 bytes of a 512-byte data section
+    ("type-41 tensor past the end", dict(ne=(32, 32), ttype=41), "past end"),
 ])
 def test_malformed_gguf_is_rejected(tmp_path, case, kw, msg):
     rc, err = open_err(gguf(tmp_path / "bad.gguf", **kw))
@@ -50,8 +52,9 @@ def test_malformed_gguf_is_rejected(tmp_path, case, kw, msg):
     assert msg in err, (case, err)
 
 
-def test_wellformed_gguf_gets_past_the_reader(tmp_path):
-    rc, err = open_err(gguf(tmp_path / "ok.gguf"))
+@pytest.mark.parametrize("ttype", [0, 41], ids=["f32", "type41"])
+def test_wellformed_gguf_gets_past_the_reader(tmp_path, ttype):
+    rc, err = open_err(gguf(tmp_path / "ok.gguf", ttype=ttype))
     # without a GPU the next step (device init) fails; with one, the model
     # lacks layers; either way the reader accepted the file
     assert rc != 0
